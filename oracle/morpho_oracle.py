@@ -1,0 +1,218 @@
+"""CPU/eager restatement of the Morphottention attention math -- TEST INFRASTRUCTURE ONLY.
+
+This module is the parity oracle for the HIP hot path. Only ``tests/``,
+``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg may import
+it, and only as the checker (or as the timed CPU baseline). The product path in
+``morphottention_amd`` never routes through it.
+
+It restates, in plain eager PyTorch (fp32 or fp64), the algorithm of the
+reference CUDA extension (paths relative to the reference repo root):
+
+* projection   ``packages/morphottention/csrc/cuda/sm120/project.cuh:26-45``
+  (``Z = X W_phi_h``; ``phi = sigmoid(Z)``; ``code = g_self * phi``;
+  ``bias = sum_c g_partner,c * code_c`` with fp32 gates)
+* sigmoid      ``packages/morphottention/csrc/cuda/morfology/cube.cuh:12-14``
+* scores/mask/online softmax/epilogue
+               ``packages/morphottention/csrc/cuda/attention/attention.cu:113-188``
+  (``s = (2 S_raw - qb_i - cb_j) * scale * log2e``, causal drop ``k > q``,
+  ``lse = m + log2(l)`` in base 2, ``-FLT_MAX`` for an empty row)
+* parameters   ``packages/morphottention/torch-ext/morphottention/autograd.py:91-140``
+  (``W_phi [D, H*m]``, ``gate_q/gate_k [H, m]``, ``W_V [D, D]``, head ``h``
+  owns columns ``h*m..`` and ``h*dv..``; init ``N(0, D^-0.5)`` drawn in fp32 on
+  the parameter's device, gates filled with 1; RNG order ``W_phi`` then ``W_V``)
+* shape contract ``packages/morphottention/csrc/cuda/attention/attention.cpp:15-57``
+
+Gradients are those of ``torch.autograd`` through this restatement, i.e. the
+mathematically complete gradient (the reference CUDA backward drops the
+query-side code gradient, ``attention.cu:446-451,472-482``; that defect is not
+reproduced).
+
+Pinning (all in ``tests/test_oracle.py``): fp64 ``gradcheck``; equivalence with
+``F.scaled_dot_product_attention`` on augmented operands; a brute-force
+pure-Python loop restatement; the binary-hypercube Hamming closed form; causal
+row 0, ``N == 1`` and ``scale == 0`` special cases; score symmetry; head and
+batch independence; the identity ``sum_j dS_ij = 0``; committed golden
+fixtures. The reference itself ships no tests or golden vectors and cannot run
+(CUDA-only), so nothing from it is executed.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+LOG2E = 1.4426950408889634
+FLT_MAX = 3.4028234663852886e38
+
+
+def init_params(dim: int, num_heads: int, cube_m: int, *, dtype=torch.float32, device="cpu"):
+    """Default parameter init of ``MorphoAttention`` (``autograd.py:123-135``).
+
+    ``W_phi`` then ``W_V`` are drawn ``N(0, dim^-0.5)`` in fp32 on ``device``
+    from the global generator and cast to ``dtype``; gates are ones.
+    """
+    std = dim ** -0.5
+    head_dim_v = dim // num_heads
+    W_phi = torch.empty(dim, num_heads * cube_m, dtype=torch.float32, device=device).normal_(0.0, std)
+    W_V = torch.empty(dim, num_heads * head_dim_v, dtype=torch.float32, device=device).normal_(0.0, std)
+    gate_q = torch.ones(num_heads, cube_m, dtype=torch.float32, device=device)
+    gate_k = torch.ones(num_heads, cube_m, dtype=torch.float32, device=device)
+    return W_phi.to(dtype), gate_q.to(dtype), gate_k.to(dtype), W_V.to(dtype)
+
+
+def project(x, W_phi, gate_q, gate_k, num_heads: int, cube_m: int):
+    """Per-head soft-hypercube projection (``project.cuh:26-45``, ``cube.cuh:12-14``).
+
+    Returns ``phi, q, k, qb, cb`` with ``phi, q, k`` shaped ``[B, H, N, m]`` and
+    ``qb, cb`` shaped ``[B, H, N]``.
+    """
+    B, N, _ = x.shape
+    z = x @ W_phi                                               # [B, N, H*m]
+    phi = torch.sigmoid(z).view(B, N, num_heads, cube_m).permute(0, 2, 1, 3)
+    gq = gate_q.to(phi.dtype)[None, :, None, :]
+    gk = gate_k.to(phi.dtype)[None, :, None, :]
+    q = gq * phi                                                # code = g_self * phi
+    k = gk * phi
+    qb = (gk * q).sum(-1)                                       # sum_c g_partner * code
+    cb = (gq * k).sum(-1)
+    return phi, q, k, qb, cb
+
+
+def scores(q, k, qb, cb, scale: float):
+    """Natural-log scores ``scale * (2 q.k - qb_i - cb_j)`` (``attention.cu:117-125``)."""
+    S = q @ k.transpose(-1, -2)
+    return scale * (2.0 * S - qb[..., :, None] - cb[..., None, :])
+
+
+def causal_mask(N: int, device) -> torch.Tensor:
+    """True where key ``j > i`` is dropped (``attention.cu:129-130``)."""
+    idx = torch.arange(N, device=device)
+    return idx[None, :] > idx[:, None]
+
+
+def morpho_attention_ref(x, W_phi, gate_q, gate_k, W_V, num_heads: int, cube_m: int, *,
+                         scale: float = 1.0, causal: bool = False, return_lse: bool = False):
+    """Forward of the fused op in the dtype of ``x`` (use fp32 or fp64).
+
+    Returns ``out [B, N, D]`` and, if ``return_lse``, the base-2 row
+    log-sum-exp ``lse [B*H, N]`` exactly as ``morphottention::forward`` returns
+    it (``attention.cu:173-188``).
+    """
+    B, N, D = x.shape
+    H, m = num_heads, cube_m
+    dv = D // H
+    W_phi = W_phi.to(x.dtype)
+    W_V = W_V.to(x.dtype)
+    _, q, k, qb, cb = project(x, W_phi, gate_q, gate_k, H, m)
+    s = scores(q, k, qb, cb, scale)                             # [B, H, N, N]
+    if causal:
+        s = s.masked_fill(causal_mask(N, x.device), float("-inf"))
+    lse_nat = torch.logsumexp(s, dim=-1)                        # [B, H, N]
+    P = torch.exp(s - lse_nat[..., None])
+    V = (x @ W_V).view(B, N, H, dv).permute(0, 2, 1, 3)         # [B, H, N, dv]
+    O = P @ V
+    out = O.permute(0, 2, 1, 3).reshape(B, N, D)
+    if not return_lse:
+        return out
+    lse = (lse_nat * LOG2E).reshape(B * H, N)
+    return out, lse
+
+
+def morpho_attention_ref_grads(x, W_phi, gate_q, gate_k, W_V, num_heads: int, cube_m: int, *,
+                               scale: float = 1.0, causal: bool = False, dout=None,
+                               dtype=torch.float32, batch_chunk: int | None = None):
+    """Forward + autograd backward of the restatement, chunked over the batch.
+
+    Inputs are upcast to ``dtype``. ``dout`` defaults to ones (i.e. the
+    gradient of ``out.sum()``). Returns ``out, lse, (dX, dW_phi, d_gate_q,
+    d_gate_k, dW_V)`` in ``dtype``. Chunking over the batch bounds the
+    ``[N, N]`` score memory; parameter gradients are summed over chunks, which
+    is exact because the batch rows never interact.
+    """
+    B = x.shape[0]
+    chunk = batch_chunk or B
+    params = [p.detach().to(dtype).clone().requires_grad_(True) for p in (W_phi, gate_q, gate_k, W_V)]
+    outs, lses, dxs = [], [], []
+    for b0 in range(0, B, chunk):
+        xb = x[b0:b0 + chunk].detach().to(dtype).clone().requires_grad_(True)
+        out, lse = morpho_attention_ref(xb, *params[:3], params[3], num_heads, cube_m,
+                                        scale=scale, causal=causal, return_lse=True)
+        g = torch.ones_like(out) if dout is None else dout[b0:b0 + chunk].to(dtype)
+        out.backward(g)
+        outs.append(out.detach())
+        lses.append(lse.detach())
+        dxs.append(xb.grad.detach())
+    grads = (torch.cat(dxs), *(p.grad.detach() for p in params))
+    return torch.cat(outs), torch.cat(lses), grads
+
+
+def brute_force_forward(x, W_phi, gate_q, gate_k, W_V, num_heads: int, cube_m: int, *,
+                        scale: float = 1.0, causal: bool = False):
+    """Pure-Python scalar loops (tiny inputs only), an independent restatement.
+
+    Follows the reference kernel's order of operations: base-2 scores, row max,
+    ``exp2``, normalise (``attention.cu:117-188``). Returns nested lists
+    ``out[b][i][d]`` and ``lse[b*H + h][i]``.
+    """
+    B, N, D = x.shape
+    H, m = num_heads, cube_m
+    dv = D // H
+    X = x.tolist()
+    Wp = W_phi.tolist()
+    Wv = W_V.tolist()
+    gq = gate_q.tolist()
+    gk = gate_k.tolist()
+    out = [[[0.0] * D for _ in range(N)] for _ in range(B)]
+    lse = [[0.0] * N for _ in range(B * H)]
+    for b in range(B):
+        for h in range(H):
+            phi = []
+            for t in range(N):
+                row = []
+                for c in range(m):
+                    z = sum(X[b][t][d] * Wp[d][h * m + c] for d in range(D))
+                    row.append(1.0 / (1.0 + math.exp(-z)))
+                phi.append(row)
+            qc = [[gq[h][c] * phi[t][c] for c in range(m)] for t in range(N)]
+            kc = [[gk[h][c] * phi[t][c] for c in range(m)] for t in range(N)]
+            qb = [sum(gk[h][c] * qc[t][c] for c in range(m)) for t in range(N)]
+            cb = [sum(gq[h][c] * kc[t][c] for c in range(m)) for t in range(N)]
+            V = [[sum(X[b][t][d] * Wv[d][h * dv + e] for d in range(D)) for e in range(dv)] for t in range(N)]
+            for i in range(N):
+                s2 = []
+                for j in range(N):
+                    if causal and j > i:
+                        continue
+                    sraw = sum(qc[i][c] * kc[j][c] for c in range(m))
+                    s2.append((j, (2.0 * sraw - qb[i] - cb[j]) * scale * LOG2E))
+                mx = max(v for _, v in s2)
+                l = sum(2.0 ** (v - mx) for _, v in s2)
+                for e in range(dv):
+                    acc = sum(2.0 ** (v - mx) * V[j][e] for j, v in s2)
+                    out[b][i][h * dv + e] = acc / l
+                lse[b * H + h][i] = mx + math.log2(l)
+    return out, lse
+
+
+def sdpa_equivalent(x, W_phi, gate_q, gate_k, W_V, num_heads: int, cube_m: int, *,
+                    scale: float = 1.0, causal: bool = False):
+    """The attention core written as plain scaled-dot-product attention.
+
+    With ``Q~_i = [2*scale*q_i, 1]`` and ``K~_j = [k_j, -scale*cb_j]`` the score
+    ``Q~_i . K~_j = s_ij + scale*qb_i``; the row constant ``scale*qb_i`` cancels
+    in the softmax, so ``SDPA(Q~, K~, V, scale=1)`` equals the morpho output.
+    Used only to pin ``morpho_attention_ref`` against a library routine.
+    """
+    import torch.nn.functional as F
+
+    B, N, D = x.shape
+    H, m = num_heads, cube_m
+    dv = D // H
+    _, q, k, qb, cb = project(x, W_phi.to(x.dtype), gate_q, gate_k, H, m)
+    ones = torch.ones_like(q[..., :1])
+    Qt = torch.cat([2.0 * scale * q, ones], dim=-1)
+    Kt = torch.cat([k, (-scale * cb)[..., None]], dim=-1)
+    V = (x @ W_V.to(x.dtype)).view(B, N, H, dv).permute(0, 2, 1, 3)
+    O = F.scaled_dot_product_attention(Qt, Kt, V, is_causal=causal, scale=1.0)
+    return O.permute(0, 2, 1, 3).reshape(B, N, D)

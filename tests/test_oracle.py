@@ -1,0 +1,261 @@
+"""Pins for the parity oracle (CPU only).
+
+The reference has no tests, golden vectors or runnable CPU path, so each check
+here fixes the oracle against something independent of its own formula: a
+library routine (SDPA), a brute-force scalar loop, fp64 finite differences,
+closed forms and invariants. The ``test_planted_*`` cases plant a plausible
+mistake in a copy of the oracle and show that one of the pins catches it.
+"""
+
+from __future__ import annotations
+
+import glob
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import morpho_oracle as mo
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def _inputs(B, N, D, H, m, seed=0, dtype=torch.float64, gates="random", x_mult=1.0):
+    g = torch.Generator().manual_seed(seed)
+    x = x_mult * torch.randn(B, N, D, generator=g, dtype=dtype)
+    W_phi = torch.randn(D, H * m, generator=g, dtype=dtype) * D ** -0.5
+    W_V = torch.randn(D, D, generator=g, dtype=dtype) * D ** -0.5
+    if gates == "random":
+        gq = 1.0 + 0.5 * torch.randn(H, m, generator=g, dtype=dtype)
+        gk = 1.0 + 0.5 * torch.randn(H, m, generator=g, dtype=dtype)
+    else:
+        gq = torch.ones(H, m, dtype=dtype)
+        gk = torch.ones(H, m, dtype=dtype)
+    return x, W_phi, gq, gk, W_V
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_gradcheck_fp64(causal):
+    x, W_phi, gq, gk, W_V = _inputs(2, 5, 6, 2, 3, seed=1)
+    args = [t.clone().requires_grad_(True) for t in (x, W_phi, gq, gk, W_V)]
+
+    def f(x, W_phi, gq, gk, W_V):
+        return mo.morpho_attention_ref(x, W_phi, gq, gk, W_V, 2, 3, scale=0.7, causal=causal)
+
+    assert torch.autograd.gradcheck(f, args, eps=1e-6, atol=1e-7, rtol=1e-5)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("scale", [1.0, 0.37, 2.5])
+def test_sdpa_equivalence(causal, scale):
+    x, W_phi, gq, gk, W_V = _inputs(2, 17, 16, 4, 5, seed=2)
+    out = mo.morpho_attention_ref(x, W_phi, gq, gk, W_V, 4, 5, scale=scale, causal=causal)
+    ref = mo.sdpa_equivalent(x, W_phi, gq, gk, W_V, 4, 5, scale=scale, causal=causal)
+    assert torch.allclose(out, ref, atol=1e-12, rtol=0)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_brute_force_loops(causal):
+    x, W_phi, gq, gk, W_V = _inputs(2, 6, 8, 2, 3, seed=3)
+    out, lse = mo.morpho_attention_ref(x, W_phi, gq, gk, W_V, 2, 3, scale=0.8, causal=causal, return_lse=True)
+    bout, blse = mo.brute_force_forward(x, W_phi, gq, gk, W_V, 2, 3, scale=0.8, causal=causal)
+    assert torch.allclose(out, torch.tensor(bout, dtype=out.dtype), atol=1e-12, rtol=0)
+    assert torch.allclose(lse, torch.tensor(blse, dtype=lse.dtype), atol=1e-12, rtol=0)
+
+
+def test_hamming_closed_form():
+    """Binary hypercube: gates 1, saturated sigmoid -> score = -scale * Hamming."""
+    B, N, D, H, m, scale = 1, 24, 16, 2, 6, 0.9
+    x, W_phi, gq, gk, W_V = _inputs(B, N, D, H, m, seed=4, gates="ones")
+    z = x @ W_phi
+    assert z.abs().min() > 1e-3  # keeps every coordinate saturated below
+    W_big = W_phi * 1e6
+    out, lse = mo.morpho_attention_ref(x, W_big, gq, gk, W_V, H, m, scale=scale, return_lse=True)
+    bits = (z > 0).to(torch.int64).view(B, N, H, m).permute(0, 2, 1, 3)
+    ham = (bits[..., :, None, :] != bits[..., None, :, :]).sum(-1).to(torch.float64)
+    s = -scale * ham
+    P = torch.softmax(s, dim=-1)
+    V = (x @ W_V).view(B, N, H, D // H).permute(0, 2, 1, 3)
+    exp_out = (P @ V).permute(0, 2, 1, 3).reshape(B, N, D)
+    assert torch.allclose(out, exp_out, atol=1e-12, rtol=0)
+    exp_lse = (torch.logsumexp(s, -1) * mo.LOG2E).reshape(B * H, N)
+    assert torch.allclose(lse, exp_lse, atol=1e-12, rtol=0)
+
+
+def test_causal_first_row_is_v0():
+    x, W_phi, gq, gk, W_V = _inputs(2, 9, 12, 3, 4, seed=5)
+    out = mo.morpho_attention_ref(x, W_phi, gq, gk, W_V, 3, 4, scale=1.3, causal=True)
+    V = x @ W_V
+    assert torch.allclose(out[:, 0], V[:, 0], atol=1e-13, rtol=0)
+
+
+def test_single_token_is_v():
+    x, W_phi, gq, gk, W_V = _inputs(3, 1, 12, 3, 4, seed=6)
+    for causal in (False, True):
+        out = mo.morpho_attention_ref(x, W_phi, gq, gk, W_V, 3, 4, scale=1.0, causal=causal)
+        assert torch.allclose(out, x @ W_V, atol=1e-13, rtol=0)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_scale_zero_is_mean_and_kills_code_grads(causal):
+    B, N, D, H, m = 2, 7, 8, 2, 3
+    x, W_phi, gq, gk, W_V = _inputs(B, N, D, H, m, seed=7)
+    out, _, grads = mo.morpho_attention_ref_grads(x, W_phi, gq, gk, W_V, H, m, scale=0.0, causal=causal,
+                                                  dtype=torch.float64)
+    V = x @ W_V
+    if causal:
+        exp = torch.cumsum(V, dim=1) / torch.arange(1, N + 1, dtype=V.dtype)[None, :, None]
+    else:
+        exp = V.mean(dim=1, keepdim=True).expand_as(V)
+    assert torch.allclose(out, exp, atol=1e-13, rtol=0)
+    _, dW_phi, dgq, dgk, _ = grads
+    assert dW_phi.abs().max() == 0 and dgq.abs().max() == 0 and dgk.abs().max() == 0
+
+
+def test_score_matrix_symmetric():
+    x, W_phi, gq, gk, W_V = _inputs(2, 11, 8, 2, 5, seed=8)
+    _, q, k, qb, cb = mo.project(x, W_phi, gq, gk, 2, 5)
+    assert torch.allclose(qb, cb, atol=1e-14, rtol=0)
+    s = mo.scores(q, k, qb, cb, 1.7)
+    assert torch.allclose(s, s.transpose(-1, -2), atol=1e-13, rtol=0)
+    # score = -scale * gated soft Hamming distance
+    phi = torch.sigmoid(x @ W_phi).view(2, 11, 2, 5).permute(0, 2, 1, 3)
+    G = (gq * gk)[None, :, None, None, :]
+    a, b = phi[..., :, None, :], phi[..., None, :, :]
+    ham = (G * (a + b - 2 * a * b)).sum(-1)
+    assert torch.allclose(s, -1.7 * ham, atol=1e-13, rtol=0)
+
+
+def test_head_and_batch_independence():
+    B, N, D, H, m = 2, 10, 12, 3, 4
+    x, W_phi, gq, gk, W_V = _inputs(B, N, D, H, m, seed=9)
+    out = mo.morpho_attention_ref(x, W_phi, gq, gk, W_V, H, m, causal=True)
+    W2 = W_phi.clone()
+    W2[:, 1 * m:2 * m] += 0.3
+    out2 = mo.morpho_attention_ref(x, W2, gq, gk, W_V, H, m, causal=True)
+    dv = D // H
+    changed = (out2 - out).abs().amax(dim=(0, 1)).view(H, dv).amax(-1)
+    assert changed[0] == 0 and changed[2] == 0 and changed[1] > 1e-6
+    x2 = x.clone()
+    x2[1] += 0.1
+    out3 = mo.morpho_attention_ref(x2, W_phi, gq, gk, W_V, H, m, causal=True)
+    assert torch.equal(out3[0], out[0]) and not torch.equal(out3[1], out[1])
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_query_bias_gradient_vanishes(causal):
+    """sum_j dS_ij = 0, so the query-side bias qb never receives gradient."""
+    B, N, D, H, m = 2, 8, 8, 2, 4
+    x, W_phi, gq, gk, W_V = _inputs(B, N, D, H, m, seed=10)
+    _, q, k, qb, cb = mo.project(x, W_phi, gq, gk, H, m)
+    qb = qb.detach().clone().requires_grad_(True)
+    s = mo.scores(q.detach(), k.detach(), qb, cb.detach(), 1.1)
+    if causal:
+        s = s.masked_fill(mo.causal_mask(N, s.device), float("-inf"))
+    P = torch.softmax(s, -1)
+    V = (x @ W_V).view(B, N, H, D // H).permute(0, 2, 1, 3)
+    dout = torch.randn_like(P @ V)
+    ((P @ V) * dout).sum().backward()
+    assert qb.grad.abs().max() < 1e-14
+
+
+def test_lse_is_log2e_logsumexp():
+    x, W_phi, gq, gk, W_V = _inputs(2, 13, 8, 2, 4, seed=11)
+    _, lse = mo.morpho_attention_ref(x, W_phi, gq, gk, W_V, 2, 4, scale=0.6, causal=True, return_lse=True)
+    _, q, k, qb, cb = mo.project(x, W_phi, gq, gk, 2, 4)
+    s = mo.scores(q, k, qb, cb, 0.6).masked_fill(mo.causal_mask(13, x.device), float("-inf"))
+    ref = (torch.logsumexp(s, -1) / math.log(2.0)).reshape(4, 13)
+    assert torch.allclose(lse, ref, atol=1e-13, rtol=0)
+
+
+def test_batch_chunking_is_exact():
+    x, W_phi, gq, gk, W_V = _inputs(3, 9, 8, 2, 4, seed=12)
+    a = mo.morpho_attention_ref_grads(x, W_phi, gq, gk, W_V, 2, 4, causal=True, dtype=torch.float64)
+    b = mo.morpho_attention_ref_grads(x, W_phi, gq, gk, W_V, 2, 4, causal=True, dtype=torch.float64,
+                                      batch_chunk=1)
+    assert torch.allclose(a[0], b[0], atol=1e-14)
+    for ga, gb in zip(a[2], b[2]):
+        assert torch.allclose(ga, gb, atol=1e-13)
+
+
+def test_default_init_matches_module_protocol():
+    """RNG order W_phi then W_V, N(0, dim^-0.5) in fp32, gates ones."""
+    torch.manual_seed(0)
+    W_phi, gq, gk, W_V = mo.init_params(64, 4, 8)
+    torch.manual_seed(0)
+    a = torch.empty(64, 32).normal_(0.0, 64 ** -0.5)
+    b = torch.empty(64, 64).normal_(0.0, 64 ** -0.5)
+    assert torch.equal(W_phi, a) and torch.equal(W_V, b)
+    assert torch.equal(gq, torch.ones(4, 8)) and torch.equal(gk, torch.ones(4, 8))
+
+
+@pytest.mark.parametrize("path", sorted(glob.glob(os.path.join(GOLDEN, "*.npz"))), ids=os.path.basename)
+def test_golden_fixtures(path):
+    d = np.load(path)
+    H, m, scale, causal = int(d["H"]), int(d["cube_m"]), float(d["scale"]), bool(d["causal"])
+    t = {k: torch.from_numpy(d[k]) for k in ("x", "W_phi", "gate_q", "gate_k", "W_V", "dout")}
+    out, lse, grads = mo.morpho_attention_ref_grads(t["x"], t["W_phi"], t["gate_q"], t["gate_k"], t["W_V"],
+                                                    H, m, scale=scale, causal=causal, dout=t["dout"],
+                                                    dtype=torch.float64)
+    assert np.allclose(out.numpy(), d["out"], atol=1e-6, rtol=1e-6)
+    assert np.allclose(lse.numpy(), d["lse"], atol=1e-5, rtol=1e-6)
+    for name, g in zip(("dX", "dW_phi", "d_gate_q", "d_gate_k", "dW_V"), grads):
+        ref = d[name]
+        assert np.abs(g.numpy() - ref).max() <= 1e-6 * max(1.0, np.abs(ref).max()), name
+    # fp32 evaluation of the oracle stays close to the fp64 fixture
+    out32, _, grads32 = mo.morpho_attention_ref_grads(t["x"], t["W_phi"], t["gate_q"], t["gate_k"], t["W_V"],
+                                                      H, m, scale=scale, causal=causal, dout=t["dout"],
+                                                      dtype=torch.float32)
+    assert np.abs(out32.numpy() - d["out"]).max() < 1e-4
+
+
+# ---------------------------------------------------------------- planted mistakes
+def _planted_scores(kind):
+    def f(q, k, qb, cb, scale):
+        S = q @ k.transpose(-1, -2)
+        if kind == "drop_factor_two":
+            return scale * (S - qb[..., :, None] - cb[..., None, :])
+        if kind == "sign_of_bias":
+            return scale * (2.0 * S - qb[..., :, None] + cb[..., None, :])
+        if kind == "unscaled_bias":
+            return scale * 2.0 * S - qb[..., :, None] - cb[..., None, :]
+        raise AssertionError(kind)
+    return f
+
+
+@pytest.mark.parametrize("kind", ["drop_factor_two", "sign_of_bias", "unscaled_bias"])
+def test_planted_score_mistakes_are_caught(kind, monkeypatch):
+    x, W_phi, gq, gk, W_V = _inputs(2, 12, 8, 2, 4, seed=13)
+    good = mo.sdpa_equivalent(x, W_phi, gq, gk, W_V, 2, 4, scale=1.2, causal=True)
+    monkeypatch.setattr(mo, "scores", _planted_scores(kind))
+    bad = mo.morpho_attention_ref(x, W_phi, gq, gk, W_V, 2, 4, scale=1.2, causal=True)
+    assert not torch.allclose(bad, good, atol=1e-6)
+
+
+def test_planted_partner_gate_mistake_is_caught(monkeypatch):
+    """cb built with the wrong partner gate (gk instead of gq): the brute-force
+    loop, which does not share ``project``, catches it."""
+    x, W_phi, gq, gk, W_V = _inputs(1, 7, 8, 2, 3, seed=14)
+    real_project = mo.project
+
+    def wrong(x, W_phi, gate_q, gate_k, H, m):
+        phi, q, k, qb, _ = real_project(x, W_phi, gate_q, gate_k, H, m)
+        cb = (gate_k.to(phi.dtype)[None, :, None, :] * k).sum(-1)
+        return phi, q, k, qb, cb
+
+    monkeypatch.setattr(mo, "project", wrong)
+    out = mo.morpho_attention_ref(x, W_phi, gq, gk, W_V, 2, 3, causal=False)
+    bout, _ = mo.brute_force_forward(x, W_phi, gq, gk, W_V, 2, 3, causal=False)
+    assert not torch.allclose(out, torch.tensor(bout, dtype=out.dtype), atol=1e-6)
+
+
+def test_gate_gradients_share_one_factor():
+    """The output depends on the gates only through G = gate_q * gate_k, so
+    d_gate_q * gate_q == d_gate_k * gate_k elementwise."""
+    x, W_phi, gq, gk, W_V = _inputs(2, 9, 8, 2, 4, seed=15)
+    _, _, grads = mo.morpho_attention_ref_grads(x, W_phi, gq, gk, W_V, 2, 4, scale=0.9, causal=True,
+                                                dout=torch.randn(2, 9, 8, dtype=torch.float64),
+                                                dtype=torch.float64)
+    assert torch.allclose(grads[2] * gq, grads[3] * gk, atol=1e-13, rtol=0)
