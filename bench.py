@@ -1,0 +1,222 @@
+"""Benchmark of the MI355X morpho-attention hot path (one GPU).
+
+A step is one forward + backward of ``MorphoAttentionFunction`` (the drop-in
+autograd bridge) over one synthetic batch already resident in HBM. The default
+workload is BASELINE configs[2] (B=4, N=4096, D=1024, H=16, cube_m=16,
+causal, fp16), the configuration the headline metric is quoted on.
+
+Prints ONE JSON line on stdout; diagnostics go to stderr.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+CONFIGS = {
+    # name: B, N, D, H, m, scale, causal, seed, x_mult
+    "C2": (8, 1024, 512, 8, 16, 1.0, False, 1, 1.0),
+    "C3": (4, 4096, 1024, 16, 16, 1.0, True, 2, 1.0),
+    "C4": (1, 16384, 1024, 16, 32, 0.5, True, 3, 1.0),
+    "C5": (16, 2048, 2048, 32, 64, 2.0, False, 4, 4.0),
+}
+PEAK_FP16_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
+PEAK_HBM_GBS = 8000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def pairs(B, N, H, causal):
+    return B * H * (N * (N + 1) // 2 if causal else N * N)
+
+
+def kernel_flops(name, B, N, D, H, m, causal):
+    """Algorithmic FLOPs of one launch of each library kernel."""
+    T, dv, HM = B * N, D // H, H * m
+    P = pairs(B, N, H, causal)
+    return {
+        "proj_fwd": 2.0 * T * D * (HM + D),
+        "attn_fwd": 2.0 * P * (m + dv),
+        "attn_bwd": 2.0 * P * (3 * m + 2 * dv),
+        "dx_gemm": 2.0 * T * (HM + D) * D,
+        "dw_gemm": 2.0 * T * D * (HM + D),
+    }.get(name)
+
+
+def step_flops(B, N, D, H, m, causal):
+    T, dv, HM = B * N, D // H, H * m
+    P = pairs(B, N, H, causal)
+    f_fwd = 2.0 * T * D * (HM + D) + 2.0 * P * (m + dv)
+    f_bwd = 4.0 * T * D * (HM + D) + 2.0 * P * (3 * m + 2 * dv)
+    return f_fwd, f_bwd
+
+
+def make_inputs(cfg, device):
+    from morphottention_amd import MorphoAttention
+    B, N, D, H, m, scale, causal, seed, xm = cfg
+    torch.manual_seed(seed)
+    mod = MorphoAttention(D, H, m, scale=scale, causal=causal, dtype=torch.float16, device="cpu")
+    params = [p.detach().to(device).requires_grad_(True) for p in (mod.W_phi, mod.gate_q, mod.gate_k, mod.W_V)]
+    torch.manual_seed(seed)
+    x = (xm * torch.randn(B, N, D)).half().to(device).requires_grad_(True)
+    torch.manual_seed(seed + 1000)
+    dout = torch.randn(B, N, D).half().to(device)
+    return x, params, dout
+
+
+def cpu_baseline(cfg, budget_s=20.0):
+    """Time the eager fp32 oracle (oracle/morpho_oracle.py) on the host CPU on a
+    bounded sample of the workload: one batch row (all heads, full sequence)."""
+    from oracle import morpho_oracle as mo
+    B, N, D, H, m, scale, causal, seed, xm = cfg
+    torch.manual_seed(seed)
+    W_phi, gq, gk, W_V = mo.init_params(D, H, m)
+    torch.manual_seed(seed)
+    x = (xm * torch.randn(1, N, D)).half().float()
+    dout = torch.randn(1, N, D)
+    times = []
+    t_start = time.perf_counter()
+    while True:
+        t0 = time.perf_counter()
+        mo.morpho_attention_ref_grads(x, W_phi, gq, gk, W_V, H, m, scale=scale, causal=causal, dout=dout,
+                                      dtype=torch.float32, head_chunk=4)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start > budget_s * 0.5 or len(times) >= 5:
+            break
+    t = statistics.median(times)
+    return {
+        "value": N / t, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+        "sample": f"oracle fp32 fwd+bwd of 1 of {B} batch rows (N={N}, all {H} heads), median of {len(times)} runs, "
+                  f"{t * 1e3:.0f} ms each; CPU: {platform.processor() or platform.machine()}, "
+                  f"os.cpu_count()={os.cpu_count()}",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="C3", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--timing-steps", type=int, default=5, help="steps re-run with per-kernel HIP events")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU only; the path is sharded over "
+                                   "(batch x head) without collectives, see DESIGN.md"}))
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no ROCm GPU visible"}))
+        sys.exit(1)
+
+    from morphottention_amd import MorphoAttentionFunction, capi
+
+    cfg = CONFIGS[args.config]
+    B, N, D, H, m, scale, causal, seed, xm = cfg
+    dev = torch.device("cuda:0")
+    x, params, dout = make_inputs(cfg, dev)
+    leaves = [x, *params]
+
+    def fwd():
+        return MorphoAttentionFunction.apply(x, *params, H, m, scale, causal)
+
+    def step():
+        out = fwd()
+        return torch.autograd.grad(out, leaves, dout)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # --- timed region: exactly K fwd+bwd steps
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms_step = e0.elapsed_time(e1) / args.steps
+
+    # --- forward only (reported beside)
+    with torch.no_grad():
+        for _ in range(3):
+            fwd()
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(args.steps):
+            fwd()
+        e1.record()
+        torch.cuda.synchronize()
+    ms_fwd = e0.elapsed_time(e1) / args.steps
+
+    # --- per-kernel durations with HIP events on the launch stream
+    capi.timing_enable(True)
+    capi.timing_read()
+    for _ in range(args.timing_steps):
+        step()
+    torch.cuda.synchronize()
+    recs = capi.timing_read()
+    capi.timing_enable(False)
+    per = {}
+    for name, ms in recs:
+        per.setdefault(name, []).append(ms)
+    kernels = {}
+    for name, v in per.items():
+        avg = sum(v) / len(v)
+        f = kernel_flops(name, B, N, D, H, m, causal)
+        kernels[name] = {"avg_ms": round(avg, 5), "launches_per_step": len(v) / args.timing_steps,
+                         "tflops": round(f / (avg * 1e-3) / 1e12, 1) if f else None}
+    dominant = max(per, key=lambda k: sum(per[k]))
+    dom_avg = sum(per[dominant]) / len(per[dominant])
+    dom_flops = kernel_flops(dominant, B, N, D, H, m, causal)
+    achieved = dom_flops / (dom_avg * 1e-3) / 1e12
+    f_fwd, f_bwd = step_flops(B, N, D, H, m, causal)
+    for k, v in sorted(kernels.items(), key=lambda kv: -kv[1]["avg_ms"]):
+        log(f"  {k:18s} {v['avg_ms']:8.4f} ms  x{v['launches_per_step']:.0f}/step  {v['tflops']} TFLOP/s")
+    log(f"step {ms_step:.4f} ms  fwd {ms_fwd:.4f} ms  step-level {(f_fwd + f_bwd) / (ms_step * 1e-3) / 1e12:.1f} "
+        f"TFLOP/s")
+
+    result = {
+        "metric": "fwd+bwd ms & tokens/s at B4 N4096 D1024 H16 causal fp16; % of roofline",
+        "value": round(B * N / (ms_step * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic (x ~ N(0,1), dout ~ N(0,1), default MorphoAttention init)",
+        "config": {"workload": f"{args.config}: B={B} N={N} D={D} H={H} cube_m={m} scale={scale} "
+                               f"causal={causal} fwd+bwd", "global_batch": B, "seq_len": N},
+        "fwd_ms": round(ms_fwd, 4),
+        "fwd_tokens_per_s": round(B * N / (ms_fwd * 1e-3), 1),
+        "step_roofline_frac": round((f_fwd + f_bwd) / 2.5e15 / (ms_step * 1e-3), 4),
+        "roofline": {"bound": "mfma", "kernel": dominant, "achieved": round(achieved, 2),
+                     "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
+                     "traffic": None},
+        "kernels": kernels,
+    }
+    if not args.no_cpu_baseline:
+        log("cpu baseline (oracle on host cores)...")
+        result["cpu_baseline"] = cpu_baseline(cfg)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

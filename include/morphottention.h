@@ -1,0 +1,106 @@
+/*
+ * morphottention -- MI355X (gfx950) native fused morpho-attention, C ABI.
+ *
+ * Drop-in boundary for the reference extension's host launchers
+ *   attention_forward_kernel_launcher   packages/morphottention/csrc/cuda/attention/attention.cuh:28-31
+ *   attention_backward_kernel_launcher  packages/morphottention/csrc/cuda/attention/attention.cuh:33-38
+ * and of the ATen ops that wrap them
+ *   morpho_forward / morpho_backward    packages/morphottention/csrc/cuda/attention/attention.cpp:15-117
+ *
+ * Differences from the reference launchers, all deliberate:
+ *   - `causal` is honoured at run time (the reference drops it, attention.cpp:46-54);
+ *   - cube_m in {16, 32, 64} and head_dim_v = D / H in {32, 64, 128} are accepted
+ *     (the reference accepts only 64 / 64, attention.cu:494,535);
+ *   - the backward returns the complete gradient, including the query-side code
+ *     gradient the reference drops (attention.cu:446-451,472-482);
+ *   - scratch memory is passed in by the caller (`workspace`), sized by the
+ *     *_workspace_size queries, so the library never allocates device memory;
+ *   - errors are returned as status codes instead of C++ exceptions.
+ *
+ * Data layout (all device pointers, row-major, contiguous, float16 = IEEE binary16):
+ *   X, out, grad_out, dX   [B, N, D]           float16
+ *   W_phi, dW_phi          [D, H * cube_m]     float16  (head h owns columns h*cube_m ..)
+ *   gate_q, gate_k, d_*    [H, cube_m]         float16
+ *   W_V, dW_V              [D, D]              float16  (head h owns columns h*(D/H) ..)
+ *   lse                    [B * H, N]          float32  base-2 log-sum-exp of the row scores
+ *
+ * All calls are asynchronous on `stream` (a hipStream_t; NULL = legacy default
+ * stream) and use the device that is current on the calling thread. Calls that
+ * share a workspace must be ordered on one stream.
+ */
+#ifndef MORPHOTTENTION_H
+#define MORPHOTTENTION_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* morpho_stream_t; /* identical to hipStream_t */
+
+enum morpho_status {
+  MORPHO_OK = 0,
+  MORPHO_ERR_INVALID_ARGUMENT = 1, /* bad shape, null pointer, unsupported size */
+  MORPHO_ERR_UNSUPPORTED = 2,      /* valid request this build does not implement */
+  MORPHO_ERR_WORKSPACE = 3,        /* workspace missing or too small */
+  MORPHO_ERR_HIP = 4               /* a HIP runtime call failed */
+};
+
+/* Library version, MAJOR * 10000 + MINOR * 100 + PATCH. No reference counterpart. */
+int morpho_version(void);
+
+/* Short text for a status code. No reference counterpart (the reference throws c10::Error). */
+const char* morpho_status_string(int status);
+
+/* Human-readable detail of the last failure on the calling thread, "" if none.
+ * Carries the same messages as the reference's TORCH_CHECKs (attention.cpp:9-38,
+ * attention.cu:491-495). */
+const char* morpho_last_error(void);
+
+/* Bytes of device workspace morpho_forward needs (0 on invalid sizes).
+ * The forward workspace holds the projected codes and values; passing it
+ * unchanged to morpho_backward lets the backward skip recomputing them. */
+size_t morpho_forward_workspace_size(int64_t B, int64_t N, int64_t D, int64_t H, int64_t cube_m);
+
+/* Forward. Replaces attention_forward_kernel_launcher (attention.cuh:28-31) and
+ * the launch part of morpho_forward (attention.cpp:15-57).
+ * Writes out [B, N, D] (float16) and lse [B*H, N] (float32, base 2;
+ * -FLT_MAX for a row without unmasked keys, which cannot occur for N >= 1). */
+int morpho_forward(const void* X, const void* W_phi, const void* gate_q, const void* gate_k, const void* W_V,
+                   void* out, float* lse, int64_t B, int64_t N, int64_t D, int64_t H, int64_t cube_m, float scale,
+                   int causal, void* workspace, size_t workspace_bytes, morpho_stream_t stream);
+
+/* Bytes of device workspace morpho_backward needs. With `have_forward_workspace`
+ * = 0 this includes room to recompute the projection. */
+size_t morpho_backward_workspace_size(int64_t B, int64_t N, int64_t D, int64_t H, int64_t cube_m,
+                                      int have_forward_workspace);
+
+/* Backward. Replaces attention_backward_kernel_launcher (attention.cuh:33-38)
+ * and the launch part of morpho_backward (attention.cpp:59-117).
+ * Writes dX, dW_phi, d_gate_q, d_gate_k, dW_V (float16, shaped like their
+ * inputs); every output is overwritten, none needs zeroing by the caller.
+ * `forward_workspace` is either NULL (the projection is recomputed from X) or
+ * the workspace of the morpho_forward call that produced `out` and `lse`,
+ * unchanged since. */
+int morpho_backward(const void* grad_out, const void* X, const void* W_phi, const void* gate_q, const void* gate_k,
+                    const void* W_V, const void* out, const float* lse, void* dX, void* dW_phi, void* d_gate_q,
+                    void* d_gate_k, void* dW_V, int64_t B, int64_t N, int64_t D, int64_t H, int64_t cube_m,
+                    float scale, int causal, const void* forward_workspace, void* workspace, size_t workspace_bytes,
+                    morpho_stream_t stream);
+
+/* Per-kernel timing for measurement harnesses. No reference counterpart.
+ * When enabled (process-wide), every kernel the library launches, from any
+ * thread, is bracketed by HIP events on its stream. morpho_timing_read
+ * synchronises on the recorded events and returns up to `max_entries`
+ * (name, milliseconds) pairs, oldest first, then clears the record; names
+ * point to static strings. */
+int morpho_timing_enable(int enable);
+int morpho_timing_read(const char** names, float* ms, int max_entries);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MORPHOTTENTION_H */

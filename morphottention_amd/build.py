@@ -1,0 +1,104 @@
+"""Build the native parts of morphottention_amd in-tree.
+
+* ``libmorphottention_hip.so`` -- the HIP kernels and the C ABI declared in
+  ``include/morphottention.h`` (hipcc, gfx950 only, no torch dependency).
+* ``_C.so`` -- the ``torch.ops.morphottention`` registrations, a thin C++ layer
+  that calls the C ABI (host code only, compiled with g++).
+
+Usage: ``python -m morphottention_amd.build`` (or ``__graft_entry__.build()``).
+"""
+
+from __future__ import annotations
+
+import concurrent.futures
+import glob
+import os
+import shutil
+import subprocess
+import sys
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+CSRC = os.path.join(PKG, "csrc")
+BUILD_DIR = os.path.join(PKG, "_build")
+HIP_LIB = os.path.join(PKG, "libmorphottention_hip.so")
+TORCH_OP = os.path.join(PKG, "_C.so")
+
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+HIPCC = os.path.join(ROCM, "bin", "hipcc")
+ARCH = "gfx950"
+
+HIP_FLAGS = [
+    "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-fvisibility=hidden",
+    "-munsafe-fp-atomics",
+    # packed fp32 VALU forms are disabled on this target
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def _run(cmd):
+    proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(line for line in proc.stdout.splitlines() if "is not a recognized feature" not in line)
+    if proc.returncode != 0:
+        raise RuntimeError(f"command failed ({proc.returncode}): {' '.join(cmd)}\n{out}")
+    return out
+
+
+def build_hip_lib(verbose: bool = False) -> str:
+    os.makedirs(BUILD_DIR, exist_ok=True)
+    sources = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+    objs = []
+
+    def compile_one(src):
+        obj = os.path.join(BUILD_DIR, os.path.basename(src) + ".o")
+        out = _run([HIPCC, *HIP_FLAGS, "-c", src, "-o", obj])
+        if verbose and out.strip():
+            print(out)
+        return obj
+
+    with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(sources))) as ex:
+        objs = list(ex.map(compile_one, sources))
+    tmp = HIP_LIB + ".tmp"
+    _run([HIPCC, "-shared", f"--offload-arch={ARCH}", "-fPIC", *objs, "-o", tmp,
+          f"-Wl,--version-script={os.path.join(CSRC, 'exports.map')}", f"-Wl,-rpath,{ROCM}/lib"])
+    os.replace(tmp, HIP_LIB)
+    return HIP_LIB
+
+
+def build_torch_op(verbose: bool = False) -> str:
+    import torch
+    from torch.utils import cpp_extension
+
+    incs = cpp_extension.include_paths(device_type="cuda")
+    libdirs = cpp_extension.library_paths(device_type="cuda")
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    cmd = [
+        "g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-fvisibility=hidden",
+        "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+        *[f"-I{p}" for p in incs],
+        os.path.join(CSRC, "torch_op.cpp"),
+        f"-L{PKG}", "-lmorphottention_hip",
+        *[f"-L{p}" for p in libdirs],
+        "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_hip",
+        "-Wl,-rpath,$ORIGIN",
+        *[f"-Wl,-rpath,{p}" for p in libdirs],
+        "-o", TORCH_OP + ".tmp",
+    ]
+    out = _run(cmd)
+    if verbose and out.strip():
+        print(out)
+    os.replace(TORCH_OP + ".tmp", TORCH_OP)
+    return TORCH_OP
+
+
+def build(verbose: bool = False) -> None:
+    if not os.path.exists(HIPCC):
+        raise RuntimeError(f"hipcc not found at {HIPCC}")
+    build_hip_lib(verbose)
+    build_torch_op(verbose)
+    shutil.rmtree(BUILD_DIR, ignore_errors=True)
+
+
+if __name__ == "__main__":
+    build(verbose="-v" in sys.argv)
+    print(f"built {HIP_LIB}\nbuilt {TORCH_OP}")

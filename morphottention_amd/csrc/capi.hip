@@ -1,0 +1,310 @@
+// C ABI of the MI355X morpho-attention library (declared in include/morphottention.h).
+//
+// Argument checks follow the reference's TORCH_CHECKs
+// (packages/morphottention/csrc/cuda/attention/attention.cpp:9-38,
+//  attention.cu:491-495,532-538) with the same messages, but return a status
+// code with the message available from morpho_last_error().
+#include <atomic>
+#include <climits>
+#include <cstdarg>
+#include <cstdio>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/morphottention.h"
+#include "internal.h"
+
+#define MORPHO_EXPORT extern "C" __attribute__((visibility("default")))
+
+namespace morpho {
+namespace {
+
+thread_local std::string g_last_error;
+
+struct TimingRec {
+  const char* name;
+  hipEvent_t start, stop;
+};
+// Timing state is process-wide: autograd runs the backward on its own thread.
+std::atomic<bool> g_timing{false};
+std::mutex g_timing_mu;
+std::vector<TimingRec> g_recs;     // guarded by g_timing_mu
+std::vector<hipEvent_t> g_pool;    // guarded by g_timing_mu
+thread_local int g_open_rec = -1;  // index of this thread's open record
+
+hipEvent_t take_event() {
+  if (!g_pool.empty()) {
+    hipEvent_t e = g_pool.back();
+    g_pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+size_t align_up(size_t x) { return (x + 255) & ~size_t(255); }
+
+// Validates sizes and fills Dims; returns MORPHO_OK or an error (message set).
+int make_dims(int64_t B, int64_t N, int64_t D, int64_t H, int64_t M, float scale, int causal, Dims& d) {
+  if (B <= 0 || N <= 0 || D <= 0 || H <= 0) return fail(MORPHO_ERR_INVALID_ARGUMENT, "Invalid dimensions");
+  if (D % H != 0) return fail(MORPHO_ERR_INVALID_ARGUMENT, "D must be divisible by H");
+  const int64_t DV = D / H;
+  if (M != 16 && M != 32 && M != 64)
+    return fail(MORPHO_ERR_UNSUPPORTED, "cube_m must be 16, 32 or 64 (got %lld)", (long long)M);
+  if (DV != 32 && DV != 64 && DV != 128)
+    return fail(MORPHO_ERR_UNSUPPORTED, "head_dim_v = D / H must be 32, 64 or 128 (got %lld)", (long long)DV);
+  const int64_t T = B * N;
+  if (T > (int64_t)1 << 30 || D > 65536 || H * M > 65536)
+    return fail(MORPHO_ERR_INVALID_ARGUMENT, "problem too large for 32-bit token indexing");
+  if (!(scale == scale)) return fail(MORPHO_ERR_INVALID_ARGUMENT, "scale must be a finite number");
+  d.B = (int)B;
+  d.N = (int)N;
+  d.D = (int)D;
+  d.H = (int)H;
+  d.M = (int)M;
+  d.DV = (int)DV;
+  d.T = T;
+  d.HM = (int)(H * M);
+  d.CW = 3 * (int)M + 8;
+  d.scale = scale;
+  d.causal = causal ? 1 : 0;
+  return MORPHO_OK;
+}
+
+size_t proj_bytes(const Dims& d) {
+  const size_t bhn = (size_t)d.B * d.H * d.N;
+  size_t s = 0;
+  s += align_up(bhn * d.CW * 2);         // qa
+  s += align_up(bhn * d.CW * 2);         // ka
+  s += align_up(bhn * d.DV * 4);         // v (hi | lo)
+  s += align_up(bhn * 16);               // tstat
+  s += align_up((size_t)(d.HM + d.D) * d.D * 2);  // wt
+  return s;
+}
+
+ProjBuffers carve_proj(void* base, const Dims& d) {
+  const size_t bhn = (size_t)d.B * d.H * d.N;
+  char* p = static_cast<char*>(base);
+  ProjBuffers b;
+  b.qa = reinterpret_cast<_Float16*>(p); p += align_up(bhn * d.CW * 2);
+  b.ka = reinterpret_cast<_Float16*>(p); p += align_up(bhn * d.CW * 2);
+  b.v = reinterpret_cast<_Float16*>(p); p += align_up(bhn * d.DV * 4);
+  b.tstat = reinterpret_cast<float4*>(p); p += align_up(bhn * 16);
+  b.wt = reinterpret_cast<_Float16*>(p);
+  return b;
+}
+
+size_t bwd_bytes(const Dims& d) {
+  const size_t bhn = (size_t)d.B * d.H * d.N;
+  const size_t nblk = (size_t)((d.T + kGateTokensPerBlock - 1) / kGateTokensPerBlock);
+  size_t s = 0;
+  s += align_up(bhn * 8);                              // qstat
+  s += align_up(bhn * d.M * 4);                        // dq
+  s += align_up(bhn * d.M * 4);                        // dk
+  s += align_up(bhn * 4);                              // dcb
+  s += align_up((size_t)d.T * (d.HM + d.D) * 2);       // dzv
+  s += align_up(nblk * d.HM * 4);                      // gpart
+  s += align_up((size_t)dw_splits(d) * d.D * (d.HM + d.D) * 4);  // wpart
+  return s;
+}
+
+BwdBuffers carve_bwd(void* base, const Dims& d) {
+  const size_t bhn = (size_t)d.B * d.H * d.N;
+  const size_t nblk = (size_t)((d.T + kGateTokensPerBlock - 1) / kGateTokensPerBlock);
+  char* p = static_cast<char*>(base);
+  BwdBuffers g;
+  g.qstat = reinterpret_cast<float2*>(p); p += align_up(bhn * 8);
+  g.dq = reinterpret_cast<float*>(p); p += align_up(bhn * d.M * 4);
+  g.dk = reinterpret_cast<float*>(p); p += align_up(bhn * d.M * 4);
+  g.dcb = reinterpret_cast<float*>(p); p += align_up(bhn * 4);
+  g.dzv = reinterpret_cast<_Float16*>(p); p += align_up((size_t)d.T * (d.HM + d.D) * 2);
+  g.gpart = reinterpret_cast<float*>(p); p += align_up(nblk * d.HM * 4);
+  g.wpart = reinterpret_cast<float*>(p);
+  g.splits = dw_splits(d);
+  return g;
+}
+
+bool misaligned(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) != 0; }
+
+#define MORPHO_LAUNCH(NAME, CALL)                                                       \
+  do {                                                                                  \
+    timing_begin(NAME, s);                                                              \
+    hipError_t e_ = (CALL);                                                             \
+    timing_end(s);                                                                      \
+    if (e_ != hipSuccess) return fail(MORPHO_ERR_HIP, "%s: %s", NAME, hipGetErrorString(e_)); \
+  } while (0)
+
+int run_projection(const Dims& d, const void* X, const void* W_phi, const void* gate_q, const void* gate_k,
+                   const void* W_V, const ProjBuffers& p, hipStream_t s) {
+  MORPHO_LAUNCH("transpose_weights", launch_transpose_weights(d, static_cast<const _Float16*>(W_phi),
+                                                              static_cast<const _Float16*>(W_V), p.wt, s));
+  MORPHO_LAUNCH("proj_fwd", launch_proj_fwd(d, static_cast<const _Float16*>(X), static_cast<const _Float16*>(gate_q),
+                                            static_cast<const _Float16*>(gate_k), p, s));
+  return MORPHO_OK;
+}
+
+}  // namespace
+
+void timing_begin(const char* name, hipStream_t s) {
+  g_open_rec = -1;
+  if (!g_timing.load(std::memory_order_relaxed)) return;
+  std::lock_guard<std::mutex> lock(g_timing_mu);
+  TimingRec r{name, take_event(), take_event()};
+  if (r.start) (void)hipEventRecord(r.start, s);
+  g_recs.push_back(r);
+  g_open_rec = (int)g_recs.size() - 1;
+}
+
+void timing_end(hipStream_t s) {
+  if (g_open_rec < 0) return;
+  std::lock_guard<std::mutex> lock(g_timing_mu);
+  if (g_open_rec < (int)g_recs.size() && g_recs[g_open_rec].stop) (void)hipEventRecord(g_recs[g_open_rec].stop, s);
+  g_open_rec = -1;
+}
+
+}  // namespace morpho
+
+using namespace morpho;
+
+MORPHO_EXPORT int morpho_version(void) { return 100; }
+
+MORPHO_EXPORT const char* morpho_status_string(int status) {
+  switch (status) {
+    case MORPHO_OK: return "ok";
+    case MORPHO_ERR_INVALID_ARGUMENT: return "invalid argument";
+    case MORPHO_ERR_UNSUPPORTED: return "unsupported";
+    case MORPHO_ERR_WORKSPACE: return "workspace missing or too small";
+    case MORPHO_ERR_HIP: return "HIP runtime error";
+    default: return "unknown status";
+  }
+}
+
+MORPHO_EXPORT const char* morpho_last_error(void) { return g_last_error.c_str(); }
+
+MORPHO_EXPORT size_t morpho_forward_workspace_size(int64_t B, int64_t N, int64_t D, int64_t H, int64_t cube_m) {
+  Dims d;
+  std::string keep = g_last_error;
+  const int st = make_dims(B, N, D, H, cube_m, 1.0f, 0, d);
+  g_last_error = keep;
+  return st == MORPHO_OK ? proj_bytes(d) : 0;
+}
+
+MORPHO_EXPORT size_t morpho_backward_workspace_size(int64_t B, int64_t N, int64_t D, int64_t H, int64_t cube_m,
+                                                    int have_forward_workspace) {
+  Dims d;
+  std::string keep = g_last_error;
+  const int st = make_dims(B, N, D, H, cube_m, 1.0f, 0, d);
+  g_last_error = keep;
+  if (st != MORPHO_OK) return 0;
+  return bwd_bytes(d) + (have_forward_workspace ? 0 : proj_bytes(d));
+}
+
+MORPHO_EXPORT int morpho_forward(const void* X, const void* W_phi, const void* gate_q, const void* gate_k,
+                                 const void* W_V, void* out, float* lse, int64_t B, int64_t N, int64_t D, int64_t H,
+                                 int64_t cube_m, float scale, int causal, void* workspace, size_t workspace_bytes,
+                                 morpho_stream_t stream) {
+  g_last_error.clear();
+  Dims d;
+  int st = make_dims(B, N, D, H, cube_m, scale, causal, d);
+  if (st != MORPHO_OK) return st;
+  if (!X || !W_phi || !gate_q || !gate_k || !W_V || !out || !lse) return fail(MORPHO_ERR_INVALID_ARGUMENT, "Null pointer");
+  if (misaligned(X) || misaligned(W_phi) || misaligned(W_V) || misaligned(out) || misaligned(lse))
+    return fail(MORPHO_ERR_INVALID_ARGUMENT, "tensor pointers must be 16-byte aligned");
+  const size_t need = proj_bytes(d);
+  if (!workspace || workspace_bytes < need)
+    return fail(MORPHO_ERR_WORKSPACE, "forward workspace needs %zu bytes (got %zu)", need, workspace_bytes);
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255) != 0)
+    return fail(MORPHO_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const ProjBuffers p = carve_proj(workspace, d);
+  st = run_projection(d, X, W_phi, gate_q, gate_k, W_V, p, s);
+  if (st != MORPHO_OK) return st;
+  MORPHO_LAUNCH("attn_fwd", launch_attn_fwd(d, p, static_cast<_Float16*>(out), lse, s));
+  return MORPHO_OK;
+}
+
+MORPHO_EXPORT int morpho_backward(const void* grad_out, const void* X, const void* W_phi, const void* gate_q,
+                                  const void* gate_k, const void* W_V, const void* out, const float* lse, void* dX,
+                                  void* dW_phi, void* d_gate_q, void* d_gate_k, void* dW_V, int64_t B, int64_t N,
+                                  int64_t D, int64_t H, int64_t cube_m, float scale, int causal,
+                                  const void* forward_workspace, void* workspace, size_t workspace_bytes,
+                                  morpho_stream_t stream) {
+  g_last_error.clear();
+  Dims d;
+  int st = make_dims(B, N, D, H, cube_m, scale, causal, d);
+  if (st != MORPHO_OK) return st;
+  if (!grad_out || !X || !W_phi || !gate_q || !gate_k || !W_V || !out || !lse)
+    return fail(MORPHO_ERR_INVALID_ARGUMENT, "Null input pointer");
+  if (!dX || !dW_phi || !d_gate_q || !d_gate_k || !dW_V) return fail(MORPHO_ERR_INVALID_ARGUMENT, "Null grad pointer");
+  if (misaligned(grad_out) || misaligned(X) || misaligned(W_phi) || misaligned(W_V) || misaligned(out) ||
+      misaligned(lse) || misaligned(dX) || misaligned(dW_phi) || misaligned(dW_V))
+    return fail(MORPHO_ERR_INVALID_ARGUMENT, "tensor pointers must be 16-byte aligned");
+  const bool have_fwd = forward_workspace != nullptr;
+  const size_t need = bwd_bytes(d) + (have_fwd ? 0 : proj_bytes(d));
+  if (!workspace || workspace_bytes < need)
+    return fail(MORPHO_ERR_WORKSPACE, "backward workspace needs %zu bytes (got %zu)", need, workspace_bytes);
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255) != 0 ||
+      (have_fwd && (reinterpret_cast<uintptr_t>(forward_workspace) & 255) != 0))
+    return fail(MORPHO_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  ProjBuffers p;
+  if (have_fwd) {
+    p = carve_proj(const_cast<void*>(forward_workspace), d);
+  } else {
+    p = carve_proj(ws, d);
+    st = run_projection(d, X, W_phi, gate_q, gate_k, W_V, p, s);
+    if (st != MORPHO_OK) return st;
+    ws += proj_bytes(d);
+  }
+  const BwdBuffers g = carve_bwd(ws, d);
+  const auto* go = static_cast<const _Float16*>(grad_out);
+  MORPHO_LAUNCH("bwd_prep", launch_bwd_prep(d, p, go, static_cast<const _Float16*>(out), lse, g, s));
+  MORPHO_LAUNCH("attn_bwd", launch_attn_bwd(d, p, go, g, s));
+  MORPHO_LAUNCH("proj_bwd_elem", launch_proj_bwd_elem(d, static_cast<const _Float16*>(gate_q),
+                                                      static_cast<const _Float16*>(gate_k), p, g, s));
+  MORPHO_LAUNCH("gate_reduce", launch_gate_reduce(d, g, static_cast<const _Float16*>(gate_q),
+                                                  static_cast<const _Float16*>(gate_k), static_cast<_Float16*>(d_gate_q),
+                                                  static_cast<_Float16*>(d_gate_k), s));
+  MORPHO_LAUNCH("dx_gemm", launch_dx_gemm(d, static_cast<const _Float16*>(W_phi), static_cast<const _Float16*>(W_V), g,
+                                          static_cast<_Float16*>(dX), s));
+  MORPHO_LAUNCH("dw_gemm", launch_dw_gemm(d, static_cast<const _Float16*>(X), g, s));
+  MORPHO_LAUNCH("dw_reduce", launch_dw_reduce(d, g, static_cast<_Float16*>(dW_phi), static_cast<_Float16*>(dW_V), s));
+  return MORPHO_OK;
+}
+
+MORPHO_EXPORT int morpho_timing_enable(int enable) {
+  g_timing.store(enable != 0);
+  return MORPHO_OK;
+}
+
+MORPHO_EXPORT int morpho_timing_read(const char** names, float* ms, int max_entries) {
+  std::lock_guard<std::mutex> lock(g_timing_mu);
+  int n = 0;
+  for (const TimingRec& r : g_recs) {
+    if (n < max_entries && r.start && r.stop) {
+      float t = 0.f;
+      if (hipEventSynchronize(r.stop) == hipSuccess && hipEventElapsedTime(&t, r.start, r.stop) == hipSuccess) {
+        if (names) names[n] = r.name;
+        if (ms) ms[n] = t;
+        ++n;
+      }
+    }
+    if (r.start) g_pool.push_back(r.start);
+    if (r.stop) g_pool.push_back(r.stop);
+  }
+  g_recs.clear();
+  return n;
+}

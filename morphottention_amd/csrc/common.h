@@ -1,0 +1,92 @@
+// Device-side building blocks for gfx950 (CDNA4, wave64).
+//
+// MFMA lane layouts used throughout (checked on MI355X):
+//   v_mfma_f32_32x32x16_f16  A: lane l holds A[l%32][8*(l/32) + j], j = 0..7
+//                            B: lane l holds B[8*(l/32) + j][l%32]
+//                            C: lane l, reg r holds C[8*(r/4) + 4*(l/32) + r%4][l%32]
+//   v_mfma_f32_32x32x8_f16   as above with 4 values per lane, k = 4*(l/32) + j.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace morpho {
+
+typedef _Float16 f16;
+typedef f16 f16x8 __attribute__((ext_vector_type(8)));
+typedef f16 f16x4 __attribute__((ext_vector_type(4)));
+typedef f16 f16x2 __attribute__((ext_vector_type(2)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kNegInf = -__builtin_inff();
+constexpr float kFltMax = 3.402823466e38f;
+
+__device__ __forceinline__ f32x16 mfma16(const f16x8& a, const f16x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mfma8(const f16x4& a, const f16x4& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x8f16(a, b, c, 0, 0, 0);
+}
+
+// Row (within a 32-row MFMA block) held in accumulator register r by lane l.
+__device__ __forceinline__ int acc_row(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
+
+// Swap bits 2 and 3 of a row index in 0..31. Loading the A-operand rows of a
+// 32x32 product in this order makes the accumulator registers 0..7 / 8..15 of
+// lane l hold rows 8*(l/32)+0..7 / 16+8*(l/32)+0..7 in natural order, which is
+// exactly the B-operand layout of the next product that contracts over them.
+__device__ __forceinline__ int swap23(int x) { return (x & ~12) | ((x & 4) << 1) | ((x & 8) >> 1); }
+
+__device__ __forceinline__ f16x4 lds_read_tr4(const f16* p) {
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
+  return __builtin_bit_cast(f16x4, v);
+}
+
+// MFMA 32x32x16 operand from an LDS tile whose contraction index runs along
+// its rows: value(mn, k) = tile[(k0 + k) * stride + mn0 + mn], mn = lane%32.
+// Two ds_read_b64_tr_b16 per lane; stride must be a multiple of 4 halves.
+__device__ __forceinline__ f16x8 frag_kmajor(const f16* tile, int stride, int k0, int mn0, int lane) {
+  const int g = lane >> 4;
+  const int row = k0 + 8 * (g >> 1) + ((lane & 15) >> 2);
+  const int col = mn0 + 16 * (g & 1) + 4 * (lane & 3);
+  const f16* p = tile + row * stride + col;
+  f16x4 lo = lds_read_tr4(p);
+  f16x4 hi = lds_read_tr4(p + 4 * stride);
+  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// MFMA 32x32x16 operand from an LDS tile whose contraction index is
+// contiguous: value(mn, k) = tile[row * stride + k0 + k] with `row` the tile
+// row this lane supplies. One 16-byte read.
+__device__ __forceinline__ f16x8 frag_kcontig(const f16* tile, int stride, int row, int k0, int lane) {
+  return *reinterpret_cast<const f16x8*>(tile + row * stride + k0 + 8 * (lane >> 5));
+}
+__device__ __forceinline__ f16x4 frag4_kcontig(const f16* tile, int stride, int row, int k0, int lane) {
+  return *reinterpret_cast<const f16x4*>(tile + row * stride + k0 + 4 * (lane >> 5));
+}
+
+// Split x into two halves with hi + lo == x to ~2^-22 relative; |x| is clamped
+// to 60000 so neither part overflows.
+__device__ __forceinline__ void split_hi_lo(float x, f16& hi, f16& lo) {
+  x = fminf(fmaxf(x, -60000.f), 60000.f);
+  hi = (f16)x;
+  lo = (f16)(x - (float)hi);
+}
+
+__device__ __forceinline__ f16x8 pack8(const f32x16& v, int base) {
+  f16x8 r;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) r[j] = (f16)v[base + j];
+  return r;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+
+__device__ __forceinline__ float sigmoidf_(float z) { return 1.0f / (1.0f + __expf(-z)); }
+
+}  // namespace morpho

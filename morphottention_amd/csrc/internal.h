@@ -1,0 +1,74 @@
+// Internal launcher interface shared by the kernel translation units and the
+// C ABI layer. Nothing here is exported from the shared library.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace morpho {
+
+struct Dims {
+  int B, N, D, H, M, DV;  // batch, tokens, model dim, heads, cube_m, head_dim_v
+  int64_t T;              // B * N tokens
+  int HM;                 // H * M projection columns
+  int CW;                 // 3 * M + 8: code row width (hi/lo split codes + affine augmentation)
+  float scale;
+  int causal;
+};
+
+// Products of the forward projection; the forward workspace holds exactly these.
+//
+// Code rows carry each code as an fp16 hi/lo pair laid out so that one MFMA
+// contraction over CW columns yields (to ~2^-22) the exact base-2 exponent:
+//   query row  [phi_hi | phi_lo | phi_hi | 1, 1, -R_hi, -R_lo, 0 x4]
+//   key row    [kc_hi  | kc_hi  | kc_lo  | b_hi, b_lo, 1, 1, 0 x4]
+// with kc = c1 * G * phi, c1 = 2 scale log2e, G = gate_q * gate_k, b the token
+// bias -scale log2e sum_c G_c phi_c and R the per-query softmax reference.
+struct ProjBuffers {
+  _Float16* qa;    // [B*H, N, CW] query rows (the first M columns are phi_hi, the next M phi_lo)
+  _Float16* ka;    // [B*H, N, CW] key rows
+  _Float16* v;     // [B*H, N, 2*DV] values X W_V per head: V_hi | V_lo
+  float4* tstat;   // [B*H, N] {b, R, gap, 0}: token bias, softmax reference, bound gap (base 2)
+  _Float16* wt;    // [H*M + D, D] transposed [W_phi | W_V]
+};
+
+struct BwdBuffers {
+  float2* qstat;   // [B*H, N] {-(lse - b), -delta}
+  float* dq;       // [B*H, N, M] sum_j dS_ij phi_j (query side), fp32 atomics
+  float* dk;       // [B*H, N, M] sum_i dS_ij phi_i (key side)
+  float* dcb;      // [B*H, N]    sum_i dS_ij
+  _Float16* dzv;   // [T, H*M + D] dZ | dV
+  float* gpart;    // [n_gate_blocks, H*M] partial sums of phi (2 dk - dcb), the gate factor dG
+  float* wpart;    // [splits, D, H*M + D] split-K partials of [dW_phi | dW_V]
+  int splits;
+};
+
+constexpr int kGateTokensPerBlock = 64;
+
+// kernels_proj.hip
+hipError_t launch_transpose_weights(const Dims& d, const _Float16* W_phi, const _Float16* W_V, _Float16* wt,
+                                    hipStream_t s);
+hipError_t launch_proj_fwd(const Dims& d, const _Float16* X, const _Float16* gate_q, const _Float16* gate_k,
+                           const ProjBuffers& p, hipStream_t s);
+hipError_t launch_proj_bwd_elem(const Dims& d, const _Float16* gate_q, const _Float16* gate_k, const ProjBuffers& p,
+                                const BwdBuffers& g, hipStream_t s);
+hipError_t launch_gate_reduce(const Dims& d, const BwdBuffers& g, const _Float16* gate_q, const _Float16* gate_k,
+                              _Float16* d_gate_q, _Float16* d_gate_k, hipStream_t s);
+hipError_t launch_dx_gemm(const Dims& d, const _Float16* W_phi, const _Float16* W_V, const BwdBuffers& g,
+                          _Float16* dX, hipStream_t s);
+hipError_t launch_dw_gemm(const Dims& d, const _Float16* X, const BwdBuffers& g, hipStream_t s);
+hipError_t launch_dw_reduce(const Dims& d, const BwdBuffers& g, _Float16* dW_phi, _Float16* dW_V, hipStream_t s);
+int dw_splits(const Dims& d);
+
+// kernels_attn.hip
+hipError_t launch_attn_fwd(const Dims& d, const ProjBuffers& p, _Float16* out, float* lse, hipStream_t s);
+hipError_t launch_bwd_prep(const Dims& d, const ProjBuffers& p, const _Float16* grad_out, const _Float16* out,
+                           const float* lse, const BwdBuffers& g, hipStream_t s);
+hipError_t launch_attn_bwd(const Dims& d, const ProjBuffers& p, const _Float16* grad_out, const BwdBuffers& g,
+                           hipStream_t s);
+
+// Timing hooks (capi.hip): bracket one launch with events when enabled.
+void timing_begin(const char* name, hipStream_t s);
+void timing_end(hipStream_t s);
+
+}  // namespace morpho

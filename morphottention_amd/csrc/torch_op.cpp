@@ -1,0 +1,161 @@
+// torch.ops.morphottention.{forward, backward}: the reference op schemas
+// (packages/morphottention/csrc/cuda/binder.cpp:6-15) registered on the CUDA
+// dispatch key, which PyTorch-ROCm uses for HIP tensors, plus two variants used
+// by the autograd Function that carry the forward projection to the backward.
+//
+// Checks and messages follow packages/morphottention/csrc/cuda/attention/attention.cpp:9-38,64-91.
+// Unlike the reference this layer sets a device guard (the reference launches
+// on whatever device is current) and honours `causal`.
+#include <ATen/ATen.h>
+#include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
+#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
+#include <torch/library.h>
+
+#include <vector>
+
+#include "../../include/morphottention.h"
+
+namespace {
+
+void check(const at::Tensor& t, const char* name) {
+  TORCH_CHECK(t.is_cuda(), name, " must be a CUDA tensor");
+  TORCH_CHECK(t.scalar_type() == at::kHalf, name, " must be float16");
+  TORCH_CHECK(t.is_contiguous(), name, " must be contiguous");
+}
+
+struct Shape {
+  int64_t B, N, D, H, M;
+};
+
+Shape check_inputs(const at::Tensor& X, const at::Tensor& W_phi, const at::Tensor& gate_q, const at::Tensor& gate_k,
+                   const at::Tensor& W_V, int64_t H, int64_t cube_m) {
+  check(X, "X");
+  check(W_phi, "W_phi");
+  check(gate_q, "gate_q");
+  check(gate_k, "gate_k");
+  check(W_V, "W_V");
+  TORCH_CHECK(X.dim() == 3, "X must be [B, N, D]");
+  const int64_t B = X.size(0), N = X.size(1), D = X.size(2);
+  TORCH_CHECK(H > 0 && D % H == 0, "D must be divisible by H");
+  const int64_t head_dim_v = D / H;
+  TORCH_CHECK(W_phi.dim() == 2 && W_phi.size(0) == D && W_phi.size(1) == H * cube_m, "W_phi must be [D, H*cube_m]");
+  TORCH_CHECK(W_V.dim() == 2 && W_V.size(0) == D && W_V.size(1) == H * head_dim_v, "W_V must be [D, H*head_dim_v]");
+  TORCH_CHECK(gate_q.dim() == 2 && gate_q.size(0) == H && gate_q.size(1) == cube_m, "gate_q must be [H, cube_m]");
+  TORCH_CHECK(gate_k.dim() == 2 && gate_k.size(0) == H && gate_k.size(1) == cube_m, "gate_k must be [H, cube_m]");
+  for (const at::Tensor* t : {&W_phi, &gate_q, &gate_k, &W_V})
+    TORCH_CHECK(t->device() == X.device(), "all tensors must be on the same device as X");
+  return {B, N, D, H, cube_m};
+}
+
+morpho_stream_t current_stream(const at::Tensor& X) {
+  return reinterpret_cast<morpho_stream_t>(c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(X.device().index()).stream());
+}
+
+void raise_on(int status, const char* what) {
+  TORCH_CHECK(status == MORPHO_OK, "morphottention ", what, " failed (", morpho_status_string(status),
+              "): ", morpho_last_error());
+}
+
+std::vector<at::Tensor> forward_impl(const at::Tensor& X, const at::Tensor& W_phi, const at::Tensor& gate_q,
+                                     const at::Tensor& gate_k, const at::Tensor& W_V, int64_t H, int64_t cube_m,
+                                     double scale, bool causal, bool keep_workspace) {
+  const Shape s = check_inputs(X, W_phi, gate_q, gate_k, W_V, H, cube_m);
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(X.device());
+  auto out = at::empty_like(X);
+  auto lse = at::empty({s.B * H, s.N}, X.options().dtype(at::kFloat));
+  const size_t ws_bytes = morpho_forward_workspace_size(s.B, s.N, s.D, s.H, s.M);
+  TORCH_CHECK(ws_bytes > 0, "morphottention forward: unsupported sizes (cube_m must be 16, 32 or 64; "
+              "D / H must be 32, 64 or 128)");
+  auto ws = at::empty({(int64_t)ws_bytes}, X.options().dtype(at::kByte));
+  raise_on(morpho_forward(X.data_ptr(), W_phi.data_ptr(), gate_q.data_ptr(), gate_k.data_ptr(), W_V.data_ptr(),
+                          out.data_ptr(), lse.data_ptr<float>(), s.B, s.N, s.D, s.H, s.M, (float)scale,
+                          causal ? 1 : 0, ws.data_ptr(), ws_bytes, current_stream(X)),
+           "forward");
+  if (keep_workspace) return {out, lse, ws};
+  return {out, lse};
+}
+
+std::vector<at::Tensor> backward_impl(const at::Tensor& grad_out, const at::Tensor& X, const at::Tensor& W_phi,
+                                      const at::Tensor& gate_q, const at::Tensor& gate_k, const at::Tensor& W_V,
+                                      const at::Tensor& out, const at::Tensor& lse, const at::Tensor* fwd_ws,
+                                      int64_t H, int64_t cube_m, double scale, bool causal) {
+  check(grad_out, "grad_out");
+  const Shape s = check_inputs(X, W_phi, gate_q, gate_k, W_V, H, cube_m);
+  check(out, "out");
+  TORCH_CHECK(lse.is_cuda(), "lse must be a CUDA tensor");
+  TORCH_CHECK(lse.scalar_type() == at::kFloat, "lse must be float32");
+  TORCH_CHECK(lse.is_contiguous(), "lse must be contiguous");
+  TORCH_CHECK(grad_out.sizes() == X.sizes(), "grad_out must match X shape [B, N, D]");
+  TORCH_CHECK(out.sizes() == X.sizes(), "out must match X shape [B, N, D]");
+  TORCH_CHECK(lse.dim() == 2 && lse.size(0) == s.B * H && lse.size(1) == s.N, "lse must be [B*H, N]");
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(X.device());
+  const void* fwd_ptr = nullptr;
+  if (fwd_ws) {
+    const size_t need = morpho_forward_workspace_size(s.B, s.N, s.D, s.H, s.M);
+    TORCH_CHECK(fwd_ws->is_cuda() && fwd_ws->scalar_type() == at::kByte && fwd_ws->is_contiguous() &&
+                    (size_t)fwd_ws->numel() >= need,
+                "workspace must be the uint8 CUDA tensor returned by forward_train for these sizes");
+    fwd_ptr = fwd_ws->data_ptr();
+  }
+  auto dX = at::empty_like(X);
+  auto dW_phi = at::empty_like(W_phi);
+  auto d_gate_q = at::empty_like(gate_q);
+  auto d_gate_k = at::empty_like(gate_k);
+  auto dW_V = at::empty_like(W_V);
+  const size_t ws_bytes = morpho_backward_workspace_size(s.B, s.N, s.D, s.H, s.M, fwd_ptr != nullptr);
+  TORCH_CHECK(ws_bytes > 0, "morphottention backward: unsupported sizes");
+  auto ws = at::empty({(int64_t)ws_bytes}, X.options().dtype(at::kByte));
+  raise_on(morpho_backward(grad_out.data_ptr(), X.data_ptr(), W_phi.data_ptr(), gate_q.data_ptr(), gate_k.data_ptr(),
+                           W_V.data_ptr(), out.data_ptr(), lse.data_ptr<float>(), dX.data_ptr(), dW_phi.data_ptr(),
+                           d_gate_q.data_ptr(), d_gate_k.data_ptr(), dW_V.data_ptr(), s.B, s.N, s.D, s.H, s.M,
+                           (float)scale, causal ? 1 : 0, fwd_ptr, ws.data_ptr(), ws_bytes, current_stream(X)),
+           "backward");
+  return {dX, dW_phi, d_gate_q, d_gate_k, dW_V};
+}
+
+std::vector<at::Tensor> op_forward(const at::Tensor& X, const at::Tensor& W_phi, const at::Tensor& gate_q,
+                                   const at::Tensor& gate_k, const at::Tensor& W_V, int64_t H, int64_t cube_m,
+                                   double scale, bool causal) {
+  return forward_impl(X, W_phi, gate_q, gate_k, W_V, H, cube_m, scale, causal, false);
+}
+
+std::vector<at::Tensor> op_forward_train(const at::Tensor& X, const at::Tensor& W_phi, const at::Tensor& gate_q,
+                                         const at::Tensor& gate_k, const at::Tensor& W_V, int64_t H, int64_t cube_m,
+                                         double scale, bool causal) {
+  return forward_impl(X, W_phi, gate_q, gate_k, W_V, H, cube_m, scale, causal, true);
+}
+
+std::vector<at::Tensor> op_backward(const at::Tensor& grad_out, const at::Tensor& X, const at::Tensor& W_phi,
+                                    const at::Tensor& gate_q, const at::Tensor& gate_k, const at::Tensor& W_V,
+                                    const at::Tensor& out, const at::Tensor& lse, int64_t H, int64_t cube_m,
+                                    double scale, bool causal) {
+  return backward_impl(grad_out, X, W_phi, gate_q, gate_k, W_V, out, lse, nullptr, H, cube_m, scale, causal);
+}
+
+std::vector<at::Tensor> op_backward_train(const at::Tensor& grad_out, const at::Tensor& X, const at::Tensor& W_phi,
+                                          const at::Tensor& gate_q, const at::Tensor& gate_k, const at::Tensor& W_V,
+                                          const at::Tensor& out, const at::Tensor& lse, const at::Tensor& workspace,
+                                          int64_t H, int64_t cube_m, double scale, bool causal) {
+  return backward_impl(grad_out, X, W_phi, gate_q, gate_k, W_V, out, lse, &workspace, H, cube_m, scale, causal);
+}
+
+}  // namespace
+
+TORCH_LIBRARY(morphottention, m) {
+  m.def("forward(Tensor X, Tensor W_phi, Tensor gate_q, Tensor gate_k, Tensor W_V, "
+        "int H, int cube_m, float scale, bool causal) -> Tensor[]");
+  m.def("backward(Tensor grad_out, Tensor X, Tensor W_phi, Tensor gate_q, Tensor gate_k, "
+        "Tensor W_V, Tensor out, Tensor lse, int H, int cube_m, float scale, bool causal) -> Tensor[]");
+  m.def("forward_train(Tensor X, Tensor W_phi, Tensor gate_q, Tensor gate_k, Tensor W_V, "
+        "int H, int cube_m, float scale, bool causal) -> Tensor[]");
+  m.def("backward_train(Tensor grad_out, Tensor X, Tensor W_phi, Tensor gate_q, Tensor gate_k, "
+        "Tensor W_V, Tensor out, Tensor lse, Tensor workspace, int H, int cube_m, float scale, bool causal) "
+        "-> Tensor[]");
+}
+
+TORCH_LIBRARY_IMPL(morphottention, CUDA, m) {
+  m.impl("forward", &op_forward);
+  m.impl("backward", &op_backward);
+  m.impl("forward_train", &op_forward_train);
+  m.impl("backward_train", &op_backward_train);
+}

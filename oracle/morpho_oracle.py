@@ -101,7 +101,7 @@ def morpho_attention_ref(x, W_phi, gate_q, gate_k, W_V, num_heads: int, cube_m: 
     """
     B, N, D = x.shape
     H, m = num_heads, cube_m
-    dv = D // H
+    dv = W_V.shape[1] // H          # D // H; a head slice of W_V is also accepted
     W_phi = W_phi.to(x.dtype)
     W_V = W_V.to(x.dtype)
     _, q, k, qb, cb = project(x, W_phi, gate_q, gate_k, H, m)
@@ -112,7 +112,7 @@ def morpho_attention_ref(x, W_phi, gate_q, gate_k, W_V, num_heads: int, cube_m: 
     P = torch.exp(s - lse_nat[..., None])
     V = (x @ W_V).view(B, N, H, dv).permute(0, 2, 1, 3)         # [B, H, N, dv]
     O = P @ V
-    out = O.permute(0, 2, 1, 3).reshape(B, N, D)
+    out = O.permute(0, 2, 1, 3).reshape(B, N, H * dv)
     if not return_lse:
         return out
     lse = (lse_nat * LOG2E).reshape(B * H, N)
@@ -121,30 +121,43 @@ def morpho_attention_ref(x, W_phi, gate_q, gate_k, W_V, num_heads: int, cube_m: 
 
 def morpho_attention_ref_grads(x, W_phi, gate_q, gate_k, W_V, num_heads: int, cube_m: int, *,
                                scale: float = 1.0, causal: bool = False, dout=None,
-                               dtype=torch.float32, batch_chunk: int | None = None):
-    """Forward + autograd backward of the restatement, chunked over the batch.
+                               dtype=torch.float32, batch_chunk: int | None = None,
+                               head_chunk: int | None = None):
+    """Forward + autograd backward of the restatement, chunked over batch and heads.
 
     Inputs are upcast to ``dtype``. ``dout`` defaults to ones (i.e. the
     gradient of ``out.sum()``). Returns ``out, lse, (dX, dW_phi, d_gate_q,
-    d_gate_k, dW_V)`` in ``dtype``. Chunking over the batch bounds the
-    ``[N, N]`` score memory; parameter gradients are summed over chunks, which
-    is exact because the batch rows never interact.
+    d_gate_k, dW_V)`` in ``dtype``. Chunking bounds the ``[N, N]`` score
+    memory and is exact: batch rows never interact, heads only meet in the
+    sum of their separate contributions to ``dX``, and the loss
+    ``sum(out * dout)`` is a sum over (batch, head) blocks, so the gradients of
+    the chunks add up to the full gradient.
     """
-    B = x.shape[0]
-    chunk = batch_chunk or B
+    B, N, D = x.shape
+    H, m = num_heads, cube_m
+    dv = D // H
+    bc = batch_chunk or B
+    hc = head_chunk or H
     params = [p.detach().to(dtype).clone().requires_grad_(True) for p in (W_phi, gate_q, gate_k, W_V)]
-    outs, lses, dxs = [], [], []
-    for b0 in range(0, B, chunk):
-        xb = x[b0:b0 + chunk].detach().to(dtype).clone().requires_grad_(True)
-        out, lse = morpho_attention_ref(xb, *params[:3], params[3], num_heads, cube_m,
+    out = torch.empty(B, N, D, dtype=dtype, device=x.device)
+    lse = torch.empty(B, H, N, dtype=dtype, device=x.device)
+    dX = torch.zeros(B, N, D, dtype=dtype, device=x.device)
+    for b0 in range(0, B, bc):
+        b1 = min(B, b0 + bc)
+        xb = x[b0:b1].detach().to(dtype).clone().requires_grad_(True)
+        g_full = torch.ones(b1 - b0, N, D, dtype=dtype, device=x.device) if dout is None \
+            else dout[b0:b1].to(dtype)
+        for h0 in range(0, H, hc):
+            h1 = min(H, h0 + hc)
+            o, l = morpho_attention_ref(xb, params[0][:, h0 * m:h1 * m], params[1][h0:h1], params[2][h0:h1],
+                                        params[3][:, h0 * dv:h1 * dv], h1 - h0, m,
                                         scale=scale, causal=causal, return_lse=True)
-        g = torch.ones_like(out) if dout is None else dout[b0:b0 + chunk].to(dtype)
-        out.backward(g)
-        outs.append(out.detach())
-        lses.append(lse.detach())
-        dxs.append(xb.grad.detach())
-    grads = (torch.cat(dxs), *(p.grad.detach() for p in params))
-    return torch.cat(outs), torch.cat(lses), grads
+            o.backward(g_full[:, :, h0 * dv:h1 * dv])
+            out[b0:b1, :, h0 * dv:h1 * dv] = o.detach()
+            lse[b0:b1, h0:h1] = l.detach().view(b1 - b0, h1 - h0, N)
+        dX[b0:b1] = xb.grad.detach()
+    grads = (dX, *(p.grad.detach() for p in params))
+    return out, lse.reshape(B * H, N), grads
 
 
 def brute_force_forward(x, W_phi, gate_q, gate_k, W_V, num_heads: int, cube_m: int, *,

@@ -1,0 +1,158 @@
+"""Host-side checks of the drop-in boundary (no GPU needed).
+
+* the C-ABI library loads and exports every function ``include/*.h`` declares;
+* argument validation returns the documented status codes and messages
+  without touching a device;
+* the torch op schemas equal the reference's
+  (``packages/morphottention/csrc/cuda/binder.cpp:7-11``);
+* fake (meta) kernels, module construction, init and errors mirror
+  ``packages/morphottention/torch-ext/morphottention/autograd.py``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import glob
+import os
+import re
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _header_functions():
+    names = []
+    for path in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        text = open(path).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names += re.findall(r"\b(morpho_[a-z_]+)\s*\(", text)
+    return sorted(set(names))
+
+
+def test_header_declares_the_entry_points():
+    names = _header_functions()
+    for required in ("morpho_forward", "morpho_backward", "morpho_forward_workspace_size",
+                     "morpho_backward_workspace_size", "morpho_last_error", "morpho_status_string"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol():
+    from morphottention_amd import capi
+    L = capi.lib()
+    for name in _header_functions():
+        assert hasattr(L, name), name
+        # and it is a real dynamic symbol of the library, not of a dependency
+        assert ctypes.cast(getattr(L, name), ctypes.c_void_p).value
+
+
+def test_status_strings_and_version():
+    from morphottention_amd import capi
+    L = capi.lib()
+    assert L.morpho_version() >= 100
+    assert L.morpho_status_string(0) == b"ok"
+    assert L.morpho_status_string(3).startswith(b"workspace")
+
+
+def test_workspace_sizes():
+    from morphottention_amd import capi
+    f = capi.forward_workspace_size(4, 4096, 1024, 16, 16)
+    assert f > 4 * 4096 * 1024 * 2  # holds at least the per-head values
+    b_with = capi.backward_workspace_size(4, 4096, 1024, 16, 16, True)
+    b_without = capi.backward_workspace_size(4, 4096, 1024, 16, 16, False)
+    assert b_without == b_with + f
+    assert capi.forward_workspace_size(4, 4096, 1024, 16, 24) == 0      # unsupported cube_m
+    assert capi.forward_workspace_size(4, 4096, 1000, 16, 16) == 0      # D % H != 0
+    assert capi.forward_workspace_size(4, 4096, 256, 16, 16) == 0       # head_dim_v 16 unsupported
+
+
+def _call_forward(L, ptr, *, M=16, D=64, H=2, ws=1 << 20):
+    vp = ctypes.c_void_p(ptr)
+    lse = ctypes.c_void_p(ptr)
+    return L.morpho_forward(vp, vp, vp, vp, vp, vp, lse, 2, 8, D, H, M, 1.0, 0, vp, ws, None)
+
+
+def test_forward_validation_never_reaches_the_device():
+    from morphottention_amd import capi
+    L = capi.lib()
+    vp = ctypes.c_void_p(0)
+    st = L.morpho_forward(vp, vp, vp, vp, vp, vp, vp, 2, 8, 64, 2, 16, 1.0, 0, vp, 0, None)
+    assert st == 1 and L.morpho_last_error() == b"Null pointer"
+    assert _call_forward(L, 4096, M=24) == 2
+    assert b"cube_m" in L.morpho_last_error()
+    assert _call_forward(L, 4096, D=63) == 1
+    assert L.morpho_last_error() == b"D must be divisible by H"
+    assert _call_forward(L, 4096, ws=16) == 3
+    assert b"workspace" in L.morpho_last_error()
+    assert _call_forward(L, 4100) == 1  # misaligned
+    st = L.morpho_backward(*([vp] * 13), 2, 8, 64, 2, 16, 1.0, 0, None, vp, 0, None)
+    assert st == 1 and L.morpho_last_error() == b"Null input pointer"
+
+
+REF_SCHEMAS = {
+    "forward": "morphottention::forward(Tensor X, Tensor W_phi, Tensor gate_q, Tensor gate_k, Tensor W_V, "
+               "int H, int cube_m, float scale, bool causal) -> Tensor[]",
+    "backward": "morphottention::backward(Tensor grad_out, Tensor X, Tensor W_phi, Tensor gate_q, Tensor gate_k, "
+                "Tensor W_V, Tensor out, Tensor lse, int H, int cube_m, float scale, bool causal) -> Tensor[]",
+}
+
+
+@pytest.mark.parametrize("name", sorted(REF_SCHEMAS))
+def test_op_schemas_match_reference(name):
+    import morphottention_amd  # noqa: F401
+    assert str(getattr(torch.ops.morphottention, name).default._schema) == REF_SCHEMAS[name]
+
+
+def test_fake_kernels():
+    import morphottention_amd  # noqa: F401
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    ops = torch.ops.morphottention
+    with FakeTensorMode():
+        X = torch.empty(2, 8, 64, dtype=torch.float16, device="cuda")
+        W = torch.empty(64, 32, dtype=torch.float16, device="cuda")
+        g = torch.empty(2, 16, dtype=torch.float16, device="cuda")
+        V = torch.empty(64, 64, dtype=torch.float16, device="cuda")
+        out, lse = ops.forward(X, W, g, g, V, 2, 16, 1.0, True)
+        assert out.shape == X.shape and lse.shape == (4, 8) and lse.dtype == torch.float32
+        out2, lse2, ws = ops.forward_train(X, W, g, g, V, 2, 16, 1.0, True)
+        assert ws.dtype == torch.uint8 and ws.numel() > 0
+        grads = ops.backward(out, X, W, g, g, V, out, lse, 2, 16, 1.0, True)
+        assert [t.shape for t in grads] == [X.shape, W.shape, g.shape, g.shape, V.shape]
+        grads = ops.backward_train(out, X, W, g, g, V, out, lse, ws, 2, 16, 1.0, True)
+        assert [t.shape for t in grads] == [X.shape, W.shape, g.shape, g.shape, V.shape]
+
+
+def test_module_construction_and_init_protocol():
+    from morphottention_amd import MorphoAttention
+    torch.manual_seed(0)
+    mod = MorphoAttention(256, 8, 16, scale=0.5, causal=True, dtype=torch.float32, device="cpu")
+    assert set(dict(mod.named_parameters())) == {"W_phi", "gate_q", "gate_k", "W_V"}
+    assert mod.W_phi.shape == (256, 128) and mod.W_V.shape == (256, 256)
+    assert mod.gate_q.shape == (8, 16) and torch.equal(mod.gate_k, torch.ones(8, 16))
+    torch.manual_seed(0)
+    a = torch.empty(256, 128).normal_(0.0, 256 ** -0.5)
+    b = torch.empty(256, 256).normal_(0.0, 256 ** -0.5)
+    assert torch.equal(mod.W_phi.detach(), a) and torch.equal(mod.W_V.detach(), b)
+    with pytest.raises(ValueError, match="divisible"):
+        MorphoAttention(250, 8, 16)
+
+
+def test_cpu_input_raises_value_error():
+    from morphottention_amd import MorphoAttention, morpho_attention
+    mod = MorphoAttention(64, 2, 16, dtype=torch.float16, device="cpu")
+    x = torch.randn(1, 4, 64, dtype=torch.float16)
+    with pytest.raises(ValueError, match="CUDA tensor"):
+        mod(x)
+    with pytest.raises(ValueError, match="CUDA tensor"):
+        morpho_attention(x, mod.W_phi, mod.gate_q, mod.gate_k, mod.W_V, 2, 16)
+
+
+def test_raw_op_on_cpu_tensors_is_not_silently_computed():
+    import morphottention_amd  # noqa: F401
+    X = torch.randn(1, 4, 64, dtype=torch.float16)
+    W = torch.randn(64, 32, dtype=torch.float16)
+    g = torch.ones(2, 16, dtype=torch.float16)
+    V = torch.randn(64, 64, dtype=torch.float16)
+    with pytest.raises((NotImplementedError, RuntimeError)):
+        torch.ops.morphottention.forward(X, W, g, g, V, 2, 16, 1.0, False)

@@ -174,10 +174,18 @@ def test_batch_chunking_is_exact():
     x, W_phi, gq, gk, W_V = _inputs(3, 9, 8, 2, 4, seed=12)
     a = mo.morpho_attention_ref_grads(x, W_phi, gq, gk, W_V, 2, 4, causal=True, dtype=torch.float64)
     b = mo.morpho_attention_ref_grads(x, W_phi, gq, gk, W_V, 2, 4, causal=True, dtype=torch.float64,
-                                      batch_chunk=1)
+                                      batch_chunk=1, head_chunk=1)
     assert torch.allclose(a[0], b[0], atol=1e-14)
+    assert torch.allclose(a[1], b[1], atol=1e-14)
     for ga, gb in zip(a[2], b[2]):
         assert torch.allclose(ga, gb, atol=1e-13)
+    # and the chunked driver agrees with a plain autograd pass
+    args = [t.clone().requires_grad_(True) for t in (x, W_phi, gq, gk, W_V)]
+    out = mo.morpho_attention_ref(*args, 2, 4, causal=True)
+    out.sum().backward()
+    assert torch.allclose(out.detach(), b[0], atol=1e-14)
+    for t, gb in zip(args, b[2]):
+        assert torch.allclose(t.grad, gb, atol=1e-13)
 
 
 def test_default_init_matches_module_protocol():
@@ -259,3 +267,20 @@ def test_gate_gradients_share_one_factor():
                                                 dout=torch.randn(2, 9, 8, dtype=torch.float64),
                                                 dtype=torch.float64)
     assert torch.allclose(grads[2] * gq, grads[3] * gk, atol=1e-13, rtol=0)
+
+
+def test_fp32_oracle_conditioning():
+    """Documents why the soft-hypercube gradients of the saturated, one-hot
+    regime are not held to a 1e-2 relative bar: even the fp32 evaluation of
+    the oracle misses its fp64 evaluation by far more than that, while the
+    value-path gradients agree to ~1e-6."""
+    d = np.load(os.path.join(GOLDEN, "wide_m64_x4.npz"))
+    t = {k: torch.from_numpy(d[k]) for k in ("x", "W_phi", "gate_q", "gate_k", "W_V", "dout")}
+    _, _, g = mo.morpho_attention_ref_grads(t["x"], t["W_phi"], t["gate_q"], t["gate_k"], t["W_V"], int(d["H"]),
+                                            int(d["cube_m"]), scale=float(d["scale"]), causal=bool(d["causal"]),
+                                            dout=t["dout"], dtype=torch.float32)
+    rel = {n: np.abs(x.numpy() - d[n]).max() / np.abs(d[n]).max()
+           for n, x in zip(("dX", "dW_phi", "d_gate_q", "d_gate_k", "dW_V"), g)}
+    assert rel["dX"] < 1e-5 and rel["dW_V"] < 1e-5
+    assert rel["dW_phi"] > 1e-2 and rel["d_gate_q"] > 1e-2
+    assert np.abs(d["dW_phi"]).max() < 1e-5 * np.abs(d["dW_V"]).max()
