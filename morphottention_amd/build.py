@@ -31,6 +31,8 @@ ARCH = "gfx950"
 HIP_FLAGS = [
     "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-fvisibility=hidden",
     "-munsafe-fp-atomics",
+    # keep MFMA accumulators in VGPRs (no AGPR round trips around the loops)
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     # packed fp32 VALU forms are disabled on this target
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]

@@ -30,6 +30,11 @@ __device__ __forceinline__ f32x16 mfma16(const f16x8& a, const f16x8& b, const f
 __device__ __forceinline__ f32x16 mfma8(const f16x4& a, const f16x4& b, const f32x16& c) {
   return __builtin_amdgcn_mfma_f32_32x32x8f16(a, b, c, 0, 0, 0);
 }
+// v_mfma_f32_16x16x32_f16: A lane l holds A[l%16][8*(l/16) + j], B lane l holds
+// B[8*(l/16) + j][l%16], C lane l reg r holds C[4*(l/16) + r][l%16].
+__device__ __forceinline__ f32x4 mfma16x16(const f16x8& a, const f16x8& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
 
 // Row (within a 32-row MFMA block) held in accumulator register r by lane l.
 __device__ __forceinline__ int acc_row(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
@@ -53,6 +58,19 @@ __device__ __forceinline__ f16x8 frag_kmajor(const f16* tile, int stride, int k0
   const int g = lane >> 4;
   const int row = k0 + 8 * (g >> 1) + ((lane & 15) >> 2);
   const int col = mn0 + 16 * (g & 1) + 4 * (lane & 3);
+  const f16* p = tile + row * stride + col;
+  f16x4 lo = lds_read_tr4(p);
+  f16x4 hi = lds_read_tr4(p + 4 * stride);
+  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// MFMA 16x16x32 operand from an LDS tile whose contraction index runs along
+// its rows: value(mn, k) = tile[(k0 + k) * stride + mn0 + mn], mn = lane%16,
+// k = 8*(lane/16) + j.
+__device__ __forceinline__ f16x8 frag16_kmajor(const f16* tile, int stride, int k0, int mn0, int lane) {
+  const int g = lane >> 4;
+  const int row = k0 + 8 * g + ((lane & 15) >> 2);
+  const int col = mn0 + 4 * (lane & 3);
   const f16* p = tile + row * stride + col;
   f16x4 lo = lds_read_tr4(p);
   f16x4 hi = lds_read_tr4(p + 4 * stride);

@@ -28,7 +28,9 @@ constexpr int kGemmBM = 128, kGemmBN = 128, kGemmBK = 32, kGemmThreads = 256;
 template <bool KCONTIG, int ROWS>
 struct GemmOperandTile {
   // LDS footprint (halves) of one buffer of this operand
-  static constexpr int kStride = KCONTIG ? (kGemmBK + 8) : (ROWS + 8);
+  // LDS row stride (halves): 20 dwords for b128 fragment reads (8 rows -> 8
+  // distinct bank groups), 16 (mod 64) halves for transposed reads.
+  static constexpr int kStride = KCONTIG ? (kGemmBK + 8) : (ROWS + 16);
   static constexpr int kElems = KCONTIG ? ROWS * kStride : kGemmBK * kStride;
 
   f16x8 reg[2];
@@ -86,7 +88,7 @@ struct GemmMainloop {
   // acc[i][j] holds C rows m0 + 64*wm + 32*i + acc_row(r), cols n0 + 64*wn + 32*j + lane%32
   __device__ __forceinline__ static void run(const OperandDesc& A, const OperandDesc& B, int M, int N, int m0, int n0,
                                              int kbeg, int kend, f16* lds, f32x16 acc[2][2]) {
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = w >> 1, wn = w & 1;
     f16* sA[2] = {lds, lds + TA::kElems};
     f16* sB[2] = {lds + 2 * TA::kElems, lds + 2 * TA::kElems + TB::kElems};

@@ -20,12 +20,16 @@ struct Dims {
 //
 // Code rows carry each code as an fp16 hi/lo pair laid out so that one MFMA
 // contraction over CW columns yields (to ~2^-22) the exact base-2 exponent:
-//   query row  [phi_hi | phi_lo | phi_hi | 1, 1, -R_hi, -R_lo, 0 x4]
-//   key row    [kc_hi  | kc_hi  | kc_lo  | b_hi, b_lo, 1, 1, 0 x4]
+//   query row  [phi_hi | 1, 1, -R_hi, -R_lo, 0 x4 | phi_lo | phi_hi]
+//   key row    [kc_hi  | b_hi, b_lo, 1, 1, 0 x4   | kc_hi  | kc_lo ]
+// (the 8-wide affine block sits right after the first M codes so that a
+// 32-row transposed read of the query row starting at column 32*floor(M/32)
+// sees the constant-1 column at row M, which the backward uses to form
+// column sums of dS in the same MFMA as the key-side code gradient).
 // with kc = c1 * G * phi, c1 = 2 scale log2e, G = gate_q * gate_k, b the token
 // bias -scale log2e sum_c G_c phi_c and R the per-query softmax reference.
 struct ProjBuffers {
-  _Float16* qa;    // [B*H, N, CW] query rows (the first M columns are phi_hi, the next M phi_lo)
+  _Float16* qa;    // [B*H, N, CW] query rows (columns 0..M-1 are phi_hi, M+8..2M+7 phi_lo)
   _Float16* ka;    // [B*H, N, CW] key rows
   _Float16* v;     // [B*H, N, 2*DV] values X W_V per head: V_hi | V_lo
   float4* tstat;   // [B*H, N] {b, R, gap, 0}: token bias, softmax reference, bound gap (base 2)

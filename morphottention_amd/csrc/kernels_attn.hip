@@ -13,8 +13,8 @@
 // MI355X design:
 //  * The exponent is produced by one MFMA contraction over a code row of
 //    width 3m + 8 (see ProjBuffers): fp16 hi/lo code pairs make the score exact
-//    to ~2^-22, and the 8-wide augmentation adds the key bias and subtracts
-//    the row reference, so exp2 reads the accumulator directly.
+//    to ~2^-22, and the 8-wide affine block adds the key bias and subtracts the
+//    row reference, so exp2 reads the accumulator directly.
 //  * Forward softmax uses a per-row reference R >= (row max - 15) computed by
 //    the projection from a closed-form bound on the soft Hamming score, so no
 //    running max or rescaling is needed; rows whose bound is loose (gap > 25,
@@ -23,6 +23,8 @@
 //    fp16 P; the row normaliser sums exactly those rounded P values.
 //  * Transposed operands (V^T, dO^T, phi^T, dS^T) are read from row-major LDS
 //    tiles with ds_read_b64_tr_b16.
+//  * Both loops are software-pipelined: the next tile's global loads are in
+//    flight while the current LDS tile is consumed, one barrier per tile.
 #include "common.h"
 #include "internal.h"
 
@@ -38,53 +40,111 @@ __device__ __forceinline__ float sum8(const f16x8& v) {
   return s;
 }
 
+// Column offset of the c-th 16-wide code chunk of a code row (the 8-wide
+// affine block sits at [M, M + 8)).
+template <int M>
+__device__ __forceinline__ constexpr int chunk_off(int c) {
+  return c < M / 16 ? 16 * c : 16 * c + 8;
+}
+
 // ============================================================ forward
 template <int M, int DV>
 struct FwdCfg {
-  static constexpr int CW = 3 * M + 8;  // code row width
+  static constexpr int CW = 3 * M + 8;    // code row width
   static constexpr int NCH = 3 * M / 16;  // 16-wide code chunks
-  static constexpr int KT = 64;         // keys per LDS tile
-  static constexpr int KS = CW + 8;     // key row stride (halves)
-  static constexpr int VS = 2 * DV + 8;  // value row stride (halves): V_hi | V_lo | pad
-  static constexpr int QW = 128;        // queries per workgroup (4 waves x 32)
+  static constexpr int KT = 64;           // keys per LDS tile
+  // LDS strides: rows read with ds_read_b128 want a stride = 8 (mod 16) halves
+  // (8 consecutive rows then hit 8 distinct 16-byte bank groups); rows read
+  // with ds_read_b64_tr_b16 want 16 (mod 64) halves (4 rows x 4 chunks of a
+  // 16-lane group hit distinct banks). CW = 3M + 8 is already 8 (mod 16).
+  static constexpr int KS = CW;           // key row stride (halves)
+  static constexpr int VS = 2 * DV + 16;  // value row stride (halves): V_hi | V_lo | pad
+  static constexpr int QW = 128;          // queries per workgroup (4 waves x 32)
+  static constexpr int KVEC = KT * CW / 8;
+  static constexpr int VVEC = KT * 2 * DV / 8;
+  static constexpr int NKR = (KVEC + 255) / 256;
+  static constexpr int NVR = (VVEC + 255) / 256;
+};
+
+template <int M, int DV>
+struct FwdPrefetch {
+  using C = FwdCfg<M, DV>;
+  f16x8 kr[C::NKR];
+  f16x8 vr[C::NVR];
+
+  __device__ __forceinline__ void load(const f16* __restrict__ ka, const f16* __restrict__ vv, int64_t rowbase, int N,
+                                       int k0, bool with_v, int tid) {
+#pragma unroll
+    for (int i = 0; i < C::NKR; ++i) {
+      const int v = tid + 256 * i;
+      const int r = v / (C::CW / 8), cv = (v % (C::CW / 8)) * 8;
+      // branch-free guard: read a clamped (valid) row, then zero it if out of range
+      const int row = min(k0 + r, N - 1);
+      const f16x8 x = *reinterpret_cast<const f16x8*>(ka + (rowbase + row) * C::CW + (v < C::KVEC ? cv : 0));
+      kr[i] = (v < C::KVEC && k0 + r < N) ? x : f16x8{};
+    }
+    if (with_v) {
+#pragma unroll
+      for (int i = 0; i < C::NVR; ++i) {
+        const int v = tid + 256 * i;
+        const int r = v / (DV / 4), cv = (v % (DV / 4)) * 8;
+        const int row = min(k0 + r, N - 1);
+        const f16x8 x = *reinterpret_cast<const f16x8*>(vv + (rowbase + row) * (2 * DV) + (v < C::VVEC ? cv : 0));
+        vr[i] = (v < C::VVEC && k0 + r < N) ? x : f16x8{};
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store(f16* sK, f16* sV, bool with_v, int tid) const {
+#pragma unroll
+    for (int i = 0; i < C::NKR; ++i) {
+      const int v = tid + 256 * i;
+      const int r = v / (C::CW / 8), cv = (v % (C::CW / 8)) * 8;
+      if (v < C::KVEC) *reinterpret_cast<f16x8*>(sK + r * C::KS + cv) = kr[i];
+    }
+    if (with_v) {
+#pragma unroll
+      for (int i = 0; i < C::NVR; ++i) {
+        const int v = tid + 256 * i;
+        const int r = v / (DV / 4), cv = (v % (DV / 4)) * 8;
+        if (v < C::VVEC) *reinterpret_cast<f16x8*>(sV + r * C::VS + cv) = vr[i];
+      }
+    }
+  }
 };
 
 template <int M, int DV, bool MAXPASS>
 __device__ __forceinline__ void fwd_tile_loop(const f16* __restrict__ ka, const f16* __restrict__ vv, int64_t rowbase,
-                                              int N, int causal, int kend, int qw0, int q, f16* sK, f16* sV,
+                                              int N, int causal, int kend, int qw0, int q, f16 (*sK)[FwdCfg<M, DV>::KT *
+                                                                                                    FwdCfg<M, DV>::KS],
+                                              f16 (*sV)[FwdCfg<M, DV>::KT * FwdCfg<M, DV>::VS],
                                               const f16x8 (&qf)[FwdCfg<M, DV>::NCH], const f16x4& qaug,
                                               f32x16 (&o)[DV / 32], float& lsum, float& rmax) {
   using C = FwdCfg<M, DV>;
   const int tid = threadIdx.x, lane = tid & 63, h32 = lane >> 5, l32 = lane & 31;
   const int nkt = (kend + C::KT - 1) / C::KT;
   const int wave_kend = causal ? min(N, qw0 + 32) : N;
+  FwdPrefetch<M, DV> pf;
+  pf.load(ka, vv, rowbase, N, 0, !MAXPASS, tid);
+  pf.store(sK[0], sV[0], !MAXPASS, tid);
+  __syncthreads();
   for (int kt = 0; kt < nkt; ++kt) {
     const int k0 = kt * C::KT;
-    __syncthreads();  // previous tile fully consumed
-    for (int v = tid; v < C::KT * (C::CW / 8); v += 256) {
-      const int r = v / (C::CW / 8), cv = (v % (C::CW / 8)) * 8;
-      f16x8 x = {};
-      if (k0 + r < N) x = *reinterpret_cast<const f16x8*>(ka + (rowbase + k0 + r) * C::CW + cv);
-      *reinterpret_cast<f16x8*>(sK + r * C::KS + cv) = x;
-    }
-    if (!MAXPASS) {
-      for (int v = tid; v < C::KT * (DV / 4); v += 256) {
-        const int r = v / (DV / 4), cv = (v % (DV / 4)) * 8;
-        f16x8 x = {};
-        if (k0 + r < N) x = *reinterpret_cast<const f16x8*>(vv + (rowbase + k0 + r) * (2 * DV) + cv);
-        *reinterpret_cast<f16x8*>(sV + r * C::VS + cv) = x;
-      }
-    }
-    __syncthreads();
+    const int buf = kt & 1;
+    const bool more = kt + 1 < nkt;
+    if (more) pf.load(ka, vv, rowbase, N, k0 + C::KT, !MAXPASS, tid);
+    const f16* tK = sK[buf];
+    const f16* tV = sV[buf];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       const int kbase = k0 + 32 * kb;
       if (kbase >= wave_kend) continue;  // wave-uniform
-      const f16* krow = sK + (32 * kb + swap23(l32)) * C::KS;
+      const f16* krow = tK + (32 * kb + swap23(l32)) * C::KS;
       f32x16 s = {};
 #pragma unroll
-      for (int c = 0; c < C::NCH; ++c) s = mfma16(*reinterpret_cast<const f16x8*>(krow + 16 * c + 8 * h32), qf[c], s);
-      s = mfma8(*reinterpret_cast<const f16x4*>(krow + 3 * M + 4 * h32), qaug, s);
+      for (int c = 0; c < C::NCH; ++c)
+        s = mfma16(*reinterpret_cast<const f16x8*>(krow + chunk_off<M>(c) + 8 * h32), qf[c], s);
+      s = mfma8(*reinterpret_cast<const f16x4*>(krow + M + 4 * h32), qaug, s);
       const bool need_mask = (kbase + 31 >= N) || (causal && kbase + 31 > qw0);
       if (need_mask) {
 #pragma unroll
@@ -108,13 +168,15 @@ __device__ __forceinline__ void fwd_tile_loop(const f16* __restrict__ ka, const 
 #pragma unroll
       for (int dvb = 0; dvb < DV / 32; ++dvb) {
         f32x16 acc = o[dvb];
-        acc = mfma16(frag_kmajor(sV, C::VS, 32 * kb, 32 * dvb, lane), p0, acc);
-        acc = mfma16(frag_kmajor(sV, C::VS, 32 * kb + 16, 32 * dvb, lane), p1, acc);
-        acc = mfma16(frag_kmajor(sV, C::VS, 32 * kb, DV + 32 * dvb, lane), p0, acc);
-        acc = mfma16(frag_kmajor(sV, C::VS, 32 * kb + 16, DV + 32 * dvb, lane), p1, acc);
+        acc = mfma16(frag_kmajor(tV, C::VS, 32 * kb, 32 * dvb, lane), p0, acc);
+        acc = mfma16(frag_kmajor(tV, C::VS, 32 * kb + 16, 32 * dvb, lane), p1, acc);
+        acc = mfma16(frag_kmajor(tV, C::VS, 32 * kb, DV + 32 * dvb, lane), p0, acc);
+        acc = mfma16(frag_kmajor(tV, C::VS, 32 * kb + 16, DV + 32 * dvb, lane), p1, acc);
         o[dvb] = acc;
       }
     }
+    if (more) pf.store(sK[buf ^ 1], sV[buf ^ 1], !MAXPASS, tid);
+    __syncthreads();
   }
 }
 
@@ -124,9 +186,10 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const f16* __restrict__ q
                                                        f16* __restrict__ out, float* __restrict__ lse, int N, int H,
                                                        int D, int causal) {
   using C = FwdCfg<M, DV>;
-  __shared__ __align__(16) f16 sK[C::KT * C::KS];
-  __shared__ __align__(16) f16 sV[C::KT * C::VS];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h32 = lane >> 5, l32 = lane & 31;
+  __shared__ __align__(16) f16 sK[2][C::KT * C::KS];
+  __shared__ __align__(16) f16 sV[2][C::KT * C::VS];
+  const int tid = threadIdx.x, lane = tid & 63, h32 = lane >> 5, l32 = lane & 31;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, scalar
   const int bh = blockIdx.y;
   const int qblk = causal ? (int)(gridDim.x - 1 - blockIdx.x) : (int)blockIdx.x;  // longest rows first
   const int q0 = qblk * C::QW, qw0 = q0 + 32 * w, q = qw0 + l32;
@@ -142,8 +205,8 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const f16* __restrict__ q
   if (qvalid) {
     const f16* qrow = qa + (rowbase + q) * C::CW;
 #pragma unroll
-    for (int c = 0; c < C::NCH; ++c) qf[c] = *reinterpret_cast<const f16x8*>(qrow + 16 * c + 8 * h32);
-    qaug = *reinterpret_cast<const f16x4*>(qrow + 3 * M + 4 * h32);
+    for (int c = 0; c < C::NCH; ++c) qf[c] = *reinterpret_cast<const f16x8*>(qrow + chunk_off<M>(c) + 8 * h32);
+    qaug = *reinterpret_cast<const f16x4*>(qrow + M + 4 * h32);
     ts = tstat[rowbase + q];
   }
   float R = ts.y;
@@ -212,39 +275,44 @@ hipError_t launch_attn_fwd(const Dims& d, const ProjBuffers& p, f16* out, float*
 }
 
 // ============================================================ backward prep
-// qstat = {-(lse - b), -delta} with delta_i = dO_i . O_i (fp32); zeroes dq.
+// qstat = {-(lse - b), -delta} with delta_i = dO_i . O_i (fp32), one thread per
+// (token, head), heads fastest so a wave reads whole contiguous rows; the same
+// grid zeroes the dq accumulator with contiguous stores.
 template <int M, int DV>
 __global__ __launch_bounds__(256) void bwd_prep_kernel(const f16* __restrict__ grad_out, const f16* __restrict__ out,
                                                        const float* __restrict__ lse,
                                                        const float4* __restrict__ tstat, float2* __restrict__ qstat,
-                                                       float* __restrict__ dq, int N, int H, int D) {
-  const int n = blockIdx.x * 256 + threadIdx.x;
-  const int bh = blockIdx.y;
-  if (n >= N) return;
-  const int b = bh / H, h = bh - b * H;
-  const int64_t bhn = (int64_t)bh * N + n;
-  const f16* go = grad_out + ((int64_t)b * N + n) * D + h * DV;
-  const f16* oo = out + ((int64_t)b * N + n) * D + h * DV;
-  float delta = 0.f;
+                                                       float* __restrict__ dq, int64_t T, int N, int H, int D) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx < T * H) {
+    const int h = (int)(idx % H);
+    const int64_t t = idx / H;
+    const int b = (int)(t / N), n = (int)(t - (int64_t)b * N);
+    const int64_t bhn = (int64_t)(b * H + h) * N + n;
+    const f16* go = grad_out + t * D + h * DV;
+    const f16* oo = out + t * D + h * DV;
+    float delta = 0.f;
 #pragma unroll
-  for (int c = 0; c < DV; c += 8) {
-    const f16x8 a = *reinterpret_cast<const f16x8*>(go + c);
-    const f16x8 o = *reinterpret_cast<const f16x8*>(oo + c);
+    for (int c = 0; c < DV; c += 8) {
+      const f16x8 a = *reinterpret_cast<const f16x8*>(go + c);
+      const f16x8 o = *reinterpret_cast<const f16x8*>(oo + c);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) delta += (float)a[e] * (float)o[e];
+      for (int e = 0; e < 8; ++e) delta += (float)a[e] * (float)o[e];
+    }
+    qstat[bhn] = make_float2(-(lse[bhn] - tstat[bhn].x), -delta);
   }
-  qstat[bhn] = make_float2(-(lse[bhn] - tstat[bhn].x), -delta);
-  float4* z = reinterpret_cast<float4*>(dq + bhn * M);
-#pragma unroll
-  for (int c = 0; c < M / 4; ++c) z[c] = make_float4(0.f, 0.f, 0.f, 0.f);
+  // zero dq: T * H * M floats, M / 4 float4 per (token, head)
+  float4* z = reinterpret_cast<float4*>(dq);
+  const int64_t nz = T * H * (M / 4);
+  for (int64_t i = idx; i < nz; i += (int64_t)gridDim.x * 256) z[i] = make_float4(0.f, 0.f, 0.f, 0.f);
 }
 
 template <int M, int DV>
 static hipError_t launch_bwd_prep_t(const Dims& d, const ProjBuffers& p, const f16* grad_out, const f16* out,
                                     const float* lse, const BwdBuffers& g, hipStream_t s) {
-  dim3 grid((d.N + 255) / 256, d.B * d.H);
-  hipLaunchKernelGGL((bwd_prep_kernel<M, DV>), grid, dim3(256), 0, s, grad_out, out, lse, p.tstat, g.qstat, g.dq, d.N,
-                     d.H, d.D);
+  const int64_t n = d.T * d.H;
+  hipLaunchKernelGGL((bwd_prep_kernel<M, DV>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, grad_out, out, lse,
+                     p.tstat, g.qstat, g.dq, d.T, d.N, d.H, d.D);
   return hipGetLastError();
 }
 
@@ -258,14 +326,78 @@ template <int M, int DV>
 struct BwdCfg {
   static constexpr int CW = 3 * M + 8;
   static constexpr int NCH = 3 * M / 16;
-  static constexpr int MB = (M + 1 + 31) / 32;  // 32-row blocks of dk^T (codes + the ones row)
+  static constexpr int MB = M / 32 + 1;         // 32-row blocks of dk^T (codes + the ones row at row M)
   static constexpr int MQ = (M + 31) / 32;      // 32-column blocks of dq
-  static constexpr int QT = 32;                 // queries per step
-  static constexpr int QS = CW + 8;             // score-operand query tile stride
-  static constexpr int PS = 32 * MB + 8;        // phi^T tile stride: phi_hi | 1 | zeros
-  static constexpr int OS = DV + 16;            // dO tile stride: DV values + 8 aug + pad
-  static constexpr int SS = 32 + 8;             // dS tile stride
+  static constexpr int QT = M <= 32 ? 64 : 32;  // queries per step
+  static constexpr int NSB = QT / 32;           // 32-query sub-blocks per step
+  // strides (halves): see FwdCfg; the query and dO tiles serve both b128 and
+  // transposed reads and are laid out for the b128 ones
+  static constexpr int QS = CW;                 // query tile stride
+  static constexpr int OS = DV + 8;             // dO tile stride: DV values + 8 aug
+  static constexpr int SS = QT + 16;            // dS^T tile stride (transposed reads only)
+  static constexpr int PKS = M + 16;            // key phi tile stride (transposed reads only)
   static constexpr int KW = 128;                // keys per workgroup (4 waves x 32)
+  static constexpr int DQT = (QT / 16) * (M / 16) / 4;  // 16x16 dq tiles per wave per step
+  // prefetch: data vectors of 8 halves per step (the affine blocks are built from qstat)
+  static constexpr int QDV = 3 * M / 8;         // code vectors per query row
+  static constexpr int ODV = DV / 8;            // dO vectors per query row
+  static constexpr int NDV = QT * (QDV + ODV);
+  static constexpr int NPR = (NDV + 255) / 256;
+};
+
+template <int M, int DV>
+struct BwdPrefetch {
+  using C = BwdCfg<M, DV>;
+  f16x8 r[C::NPR];
+  float2 st;  // qstat of query row tid (tid < QT)
+
+  __device__ __forceinline__ void load(const f16* __restrict__ qa, const f16* __restrict__ grad_out,
+                                       const float2* __restrict__ qstat, int64_t rowbase, int64_t tokbase, int hoff,
+                                       int N, int D, int qs, int tid) {
+#pragma unroll
+    for (int i = 0; i < C::NPR; ++i) {
+      const int v = tid + 256 * i;
+      f16x8 x = {};
+      if (v < C::QT * C::QDV) {
+        const int rr = v / C::QDV, j = v % C::QDV;
+        const int col = j < M / 8 ? 8 * j : 8 * j + 8;
+        if (qs + rr < N) x = *reinterpret_cast<const f16x8*>(qa + (rowbase + qs + rr) * C::CW + col);
+      } else if (v < C::NDV) {
+        const int u = v - C::QT * C::QDV;
+        const int rr = u / C::ODV, col = 8 * (u % C::ODV);
+        if (qs + rr < N) x = *reinterpret_cast<const f16x8*>(grad_out + (tokbase + qs + rr) * D + hoff + col);
+      }
+      r[i] = x;
+    }
+    st = make_float2(0.f, 0.f);
+    if (tid < C::QT && qs + tid < N) st = qstat[rowbase + qs + tid];
+  }
+
+  __device__ __forceinline__ void store(f16* sQ, f16* sO, int tid) const {
+#pragma unroll
+    for (int i = 0; i < C::NPR; ++i) {
+      const int v = tid + 256 * i;
+      if (v < C::QT * C::QDV) {
+        const int rr = v / C::QDV, j = v % C::QDV;
+        const int col = j < M / 8 ? 8 * j : 8 * j + 8;
+        *reinterpret_cast<f16x8*>(sQ + rr * C::QS + col) = r[i];
+      } else if (v < C::NDV) {
+        const int u = v - C::QT * C::QDV;
+        const int rr = u / C::ODV, col = 8 * (u % C::ODV);
+        *reinterpret_cast<f16x8*>(sO + rr * C::OS + col) = r[i];
+      }
+    }
+    if (tid < C::QT) {
+      // affine blocks (rows past N get st = 0; every score they touch is masked)
+      const f16 one = (f16)1.f;
+      f16 lh, ll, dh, dl;
+      split_hi_lo(st.x, lh, ll);
+      split_hi_lo(st.y, dh, dl);
+      const f16 zero = (f16)0.f;
+      *reinterpret_cast<f16x8*>(sQ + tid * C::QS + M) = f16x8{one, one, lh, ll, zero, zero, zero, zero};
+      *reinterpret_cast<f16x8*>(sO + tid * C::OS + DV) = f16x8{dh, dl, zero, zero, zero, zero, zero, zero};
+    }
+  }
 };
 
 template <int M, int DV>
@@ -277,12 +409,12 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ q
                                                        int causal) {
   using C = BwdCfg<M, DV>;
   __shared__ __align__(16) f16 sQ[2][C::QT * C::QS];
-  __shared__ __align__(16) f16 sP[2][C::QT * C::PS];
   __shared__ __align__(16) f16 sO[2][C::QT * C::OS];
-  __shared__ __align__(16) f16 sdS[4][32 * C::SS];
-  __shared__ __align__(16) float sdq[4][C::QT * M];
+  __shared__ __align__(16) f16 sdS[2][C::KW * C::SS];  // dS^T of the whole workgroup: row = key
+  __shared__ __align__(16) f16 sPk[C::KW * C::PKS];     // phi_hi of the workgroup's keys: row = key
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h32 = lane >> 5, l32 = lane & 31;
+  const int tid = threadIdx.x, lane = tid & 63, h32 = lane >> 5, l32 = lane & 31;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, scalar
   const int bh = blockIdx.y;
   const int k0 = blockIdx.x * C::KW;  // causal: low key blocks see the most queries; they start first
   const int kw0 = k0 + 32 * w;
@@ -290,13 +422,13 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ q
   const bool kvalid = key < N;
   const int b = bh / H, h = bh - b * H;
   const int64_t rowbase = (int64_t)bh * N;
+  const int64_t tokbase = (int64_t)b * N;
   const f16 one = (f16)1.f, zero = (f16)0.f;
 
   // ---- per-wave key-side operands, loaded once
   f16x8 kf[C::NCH];
   f16x4 kaug = {};
   f16x8 vf[DV / 16];
-  f16x8 kq[C::MQ][2];
 #pragma unroll
   for (int c = 0; c < C::NCH; ++c) kf[c] = f16x8{};
 #pragma unroll
@@ -304,27 +436,20 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ q
   if (kvalid) {
     const f16* krow = ka + (rowbase + key) * C::CW;
 #pragma unroll
-    for (int c = 0; c < C::NCH; ++c) kf[c] = *reinterpret_cast<const f16x8*>(krow + 16 * c + 8 * h32);
-    kaug = *reinterpret_cast<const f16x4*>(krow + 3 * M + 4 * h32);
+    for (int c = 0; c < C::NCH; ++c) kf[c] = *reinterpret_cast<const f16x8*>(krow + chunk_off<M>(c) + 8 * h32);
+    kaug = *reinterpret_cast<const f16x4*>(krow + M + 4 * h32);
     const f16* vrow = vv + (rowbase + key) * (2 * DV);
 #pragma unroll
     for (int c = 0; c < DV / 16; ++c) vf[c] = *reinterpret_cast<const f16x8*>(vrow + 16 * c + 8 * h32);
   }
   const f16x4 vaug = h32 == 0 ? f16x4{one, one, zero, zero} : f16x4{zero, zero, zero, zero};
-  // B operand of dq = dS phi_keys: lane supplies phi_hi[kw0 + 16 c + 8 h32 + j][32 cb + l32]
-#pragma unroll
-  for (int cb = 0; cb < C::MQ; ++cb)
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      f16x8 x = {};
-      const int code = 32 * cb + l32;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int kk = kw0 + 16 * c + 8 * h32 + j;
-        if (code < M && kk < N) x[j] = qa[(rowbase + kk) * C::CW + code];
-      }
-      kq[cb][c] = x;
-    }
+  // phi_hi of the workgroup's keys for the dq product (zero past N)
+  for (int v = tid; v < C::KW * (M / 8); v += 256) {
+    const int r = v / (M / 8), cv = (v % (M / 8)) * 8;
+    f16x8 x = {};
+    if (k0 + r < N) x = *reinterpret_cast<const f16x8*>(qa + (rowbase + k0 + r) * C::CW + cv);
+    *reinterpret_cast<f16x8*>(sPk + r * C::PKS + cv) = x;
+  }
 
   f32x16 dva[DV / 32], dka[C::MB];
 #pragma unroll
@@ -334,137 +459,91 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ q
 
   const int qstart = causal ? k0 : 0;
   const int nsteps = qstart < N ? (N - qstart + C::QT - 1) / C::QT : 0;
+  // keys of this workgroup that exist: dq contracts over [0, kw_valid) only
+  const int nkey = min(C::KW, N - k0);
 
-  auto stage = [&](int step, int buf) {
-    const int qs = qstart + step * C::QT;
-    // score operand rows: codes (3M) | 1, 1, -L_hi, -L_lo, 0 x4
-    for (int v = tid; v < C::QT * (C::CW / 8); v += 256) {
-      const int r = v / (C::CW / 8), cv = (v % (C::CW / 8)) * 8;
-      const int qq = qs + r;
-      f16x8 x = {};
-      if (qq < N) {
-        if (cv < 3 * M) {
-          x = *reinterpret_cast<const f16x8*>(qa + (rowbase + qq) * C::CW + cv);
-        } else {
-          f16 lh, ll;
-          split_hi_lo(qstat[rowbase + qq].x, lh, ll);
-          x = f16x8{one, one, lh, ll, zero, zero, zero, zero};
-        }
-      }
-      *reinterpret_cast<f16x8*>(&sQ[buf][r * C::QS + cv]) = x;
-    }
-    // key-gradient operand rows: phi_hi (M) | 1 | zeros to 32 MB
-    for (int v = tid; v < C::QT * (32 * C::MB / 8); v += 256) {
-      const int r = v / (32 * C::MB / 8), cv = (v % (32 * C::MB / 8)) * 8;
-      const int qq = qs + r;
-      f16x8 x = {};
-      if (qq < N) {
-        if (cv < M) x = *reinterpret_cast<const f16x8*>(qa + (rowbase + qq) * C::CW + cv);
-        else if (cv == M) x[0] = one;
-      }
-      *reinterpret_cast<f16x8*>(&sP[buf][r * C::PS + cv]) = x;
-    }
-    // dO rows: dO_h | -delta_hi, -delta_lo, 0.. | zero pad to OS
-    for (int v = tid; v < C::QT * (C::OS / 8); v += 256) {
-      const int r = v / (C::OS / 8), cv = (v % (C::OS / 8)) * 8;
-      const int qq = qs + r;
-      f16x8 x = {};
-      if (qq < N) {
-        if (cv < DV) {
-          x = *reinterpret_cast<const f16x8*>(grad_out + ((int64_t)b * N + qq) * D + h * DV + cv);
-        } else if (cv == DV) {
-          f16 dh, dl;
-          split_hi_lo(qstat[rowbase + qq].y, dh, dl);
-          x = f16x8{dh, dl, zero, zero, zero, zero, zero, zero};
-        }
-      }
-      *reinterpret_cast<f16x8*>(&sO[buf][r * C::OS + cv]) = x;
-    }
-  };
+  BwdPrefetch<M, DV> pf;
+  if (nsteps > 0) {
+    pf.load(qa, grad_out, qstat, rowbase, tokbase, h * DV, N, D, qstart, tid);
+    pf.store(sQ[0], sO[0], tid);
+  }
+  __syncthreads();
 
-  // Sum the per-wave dq partials of one step and add them to global memory.
-  auto flush_dq = [&](int step) {
-    const int qs = qstart + step * C::QT;
-    int nact = 0;
-#pragma unroll
-    for (int ww = 0; ww < 4; ++ww)
-      if (!(causal && k0 + 32 * ww > qs + C::QT - 1) && k0 + 32 * ww < N) nact = ww + 1;
-    for (int idx = tid; idx < C::QT * M; idx += 256) {
-      const int r = idx / M, c = idx - r * M;
-      const int qq = qs + r;
-      if (qq >= N) continue;
-      float s = 0.f;
-      for (int ww = 0; ww < nact; ++ww) s += sdq[ww][idx];
-      unsafeAtomicAdd(dq + (rowbase + qq) * M + c, s);
-    }
-  };
-
-  if (nsteps > 0) stage(0, 0);
   for (int step = 0; step < nsteps; ++step) {
     const int buf = step & 1;
     const int qs = qstart + step * C::QT;
-    __syncthreads();  // staging of `step` visible; sdq of step-1 complete
-    if (step > 0) flush_dq(step - 1);
-    const bool active = !(causal && kw0 > qs + C::QT - 1) && kw0 < N;  // wave-uniform
-    if (active) {
-      // S = Q~ K~^T (rows: queries in swap23 order; lane: key)
-      const f16* qrow = &sQ[buf][swap23(l32) * C::QS];
-      f32x16 s = {};
+    const bool more = step + 1 < nsteps;
+    if (more) pf.load(qa, grad_out, qstat, rowbase, tokbase, h * DV, N, D, qs + C::QT, tid);
+    const f16* tQ = sQ[buf];
+    const f16* tO = sO[buf];
+    f16* tS = sdS[buf] + (32 * w + l32) * C::SS;  // this lane's key row
 #pragma unroll
-      for (int c = 0; c < C::NCH; ++c) s = mfma16(*reinterpret_cast<const f16x8*>(qrow + 16 * c + 8 * h32), kf[c], s);
-      s = mfma8(*reinterpret_cast<const f16x4*>(qrow + 3 * M + 4 * h32), kaug, s);
-      // dP - delta = dO~ V~^T
-      const f16* orow = &sO[buf][swap23(l32) * C::OS];
-      f32x16 dp = {};
+    for (int sb = 0; sb < C::NSB; ++sb) {
+      const int q0 = qs + 32 * sb;
+      f16x8 ds16[2] = {f16x8{}, f16x8{}};
+      if (!((causal && kw0 > q0 + 31) || kw0 >= N || q0 >= N)) {  // wave-uniform: something unmasked
+        // S = Q~ K~^T (rows: queries in swap23 order; lane: key)
+        const f16* qrow = tQ + (32 * sb + swap23(l32)) * C::QS;
+        f32x16 s = {};
 #pragma unroll
-      for (int c = 0; c < DV / 16; ++c) dp = mfma16(*reinterpret_cast<const f16x8*>(orow + 16 * c + 8 * h32), vf[c], dp);
-      dp = mfma8(*reinterpret_cast<const f16x4*>(orow + DV + 4 * h32), vaug, dp);
-      const bool need_mask = (qs + C::QT > N) || (kw0 + 31 >= N) || (causal && kw0 + 31 > qs);
-      f16x8 p16[2], ds16[2];
+        for (int c = 0; c < C::NCH; ++c)
+          s = mfma16(*reinterpret_cast<const f16x8*>(qrow + chunk_off<M>(c) + 8 * h32), kf[c], s);
+        s = mfma8(*reinterpret_cast<const f16x4*>(qrow + M + 4 * h32), kaug, s);
+        // dP - delta = dO~ V~^T
+        const f16* orow = tO + (32 * sb + swap23(l32)) * C::OS;
+        f32x16 dp = {};
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float pr = fast_exp2(s[r]);
-        if (need_mask) {
-          const int qq = qs + swap23(acc_row(r, lane));
-          if (qq >= N || !kvalid || (causal && key > qq)) pr = 0.f;
+        for (int c = 0; c < DV / 16; ++c)
+          dp = mfma16(*reinterpret_cast<const f16x8*>(orow + 16 * c + 8 * h32), vf[c], dp);
+        dp = mfma8(*reinterpret_cast<const f16x4*>(orow + DV + 4 * h32), vaug, dp);
+        const bool need_mask = (q0 + 32 > N) || (kw0 + 31 >= N) || (causal && kw0 + 31 > q0);
+        f16x8 p16[2];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float pr = fast_exp2(s[r]);
+          if (need_mask) {
+            const int qq = q0 + swap23(acc_row(r, lane));
+            if (qq >= N || !kvalid || (causal && key > qq)) pr = 0.f;
+          }
+          p16[r >> 3][r & 7] = (f16)pr;
+          ds16[r >> 3][r & 7] = (f16)(pr * dp[r]);
         }
-        p16[r >> 3][r & 7] = (f16)pr;
-        ds16[r >> 3][r & 7] = (f16)(pr * dp[r]);
-      }
-      // dV^T += dO^T P ; dk^T += phi^T dS  (rows: dv / code; lane: key)
+        // dV^T += dO^T P ; dk^T += phi^T dS  (rows: dv / code; lane: key)
 #pragma unroll
-      for (int c = 0; c < 2; ++c) {
+        for (int c = 0; c < 2; ++c) {
 #pragma unroll
-        for (int dvb = 0; dvb < DV / 32; ++dvb)
-          dva[dvb] = mfma16(frag_kmajor(sO[buf], C::OS, 16 * c, 32 * dvb, lane), p16[c], dva[dvb]);
+          for (int dvb = 0; dvb < DV / 32; ++dvb)
+            dva[dvb] = mfma16(frag_kmajor(tO, C::OS, 32 * sb + 16 * c, 32 * dvb, lane), p16[c], dva[dvb]);
 #pragma unroll
-        for (int mb = 0; mb < C::MB; ++mb)
-          dka[mb] = mfma16(frag_kmajor(sP[buf], C::PS, 16 * c, 32 * mb, lane), ds16[c], dka[mb]);
-      }
-      // dS^T to LDS: row = key, 32 query columns
-#pragma unroll
-      for (int c = 0; c < 2; ++c) *reinterpret_cast<f16x8*>(&sdS[w][l32 * C::SS + 16 * c + 8 * h32]) = ds16[c];
-    }
-    if (step + 1 < nsteps) stage(step + 1, buf ^ 1);
-    __syncthreads();  // dS tiles visible
-    if (active) {
-      // dq[q][code] = sum_key dS[q][key] phi[key][code] (rows: q natural; lane: code)
-#pragma unroll
-      for (int cb = 0; cb < C::MQ; ++cb) {
-        f32x16 acc = {};
-#pragma unroll
-        for (int c = 0; c < 2; ++c) acc = mfma16(frag_kmajor(sdS[w], C::SS, 16 * c, 0, lane), kq[cb][c], acc);
-        const int code = 32 * cb + l32;
-        if (code < M) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) sdq[w][acc_row(r, lane) * M + code] = acc[r];
+          for (int mb = 0; mb < C::MB; ++mb)
+            dka[mb] = mfma16(frag_kmajor(tQ, C::QS, 32 * sb + 16 * c, 32 * mb, lane), ds16[c], dka[mb]);
         }
       }
+      // dS^T row of this key (zeros where nothing was computed)
+#pragma unroll
+      for (int c = 0; c < 2; ++c) *reinterpret_cast<f16x8*>(tS + 32 * sb + 16 * c + 8 * h32) = ds16[c];
     }
-  }
-  if (nsteps > 0) {
-    __syncthreads();
-    flush_dq(nsteps - 1);
+    if (more) pf.store(sQ[buf ^ 1], sO[buf ^ 1], tid);
+    __syncthreads();  // dS^T of all four waves complete; next tiles visible
+    // dq[q][code] += sum_key dS[q][key] phi[key][code]: 16 x 16 output tiles
+    // split over the waves, contraction over the workgroup's keys.
+#pragma unroll
+    for (int t = 0; t < C::DQT; ++t) {
+      const int tile = w + 4 * t;
+      const int qt = tile % (C::QT / 16), ct = tile / (C::QT / 16);
+      const int qrow0 = qs + 16 * qt;
+      if (qrow0 >= N) continue;  // uniform
+      f32x4 acc = {};
+      for (int kc = 0; kc < nkey; kc += 32)
+        acc = mfma16x16(frag16_kmajor(sdS[buf], C::SS, kc, 16 * qt, lane),
+                        frag16_kmajor(sPk, C::PKS, kc, 16 * ct, lane), acc);
+      const int code = 16 * ct + (lane & 15);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int qq = qrow0 + 4 * (lane >> 4) + r;
+        if (qq < N && acc[r] != 0.f) unsafeAtomicAdd(dq + (rowbase + qq) * M + code, acc[r]);
+      }
+    }
   }
 
   // ---- epilogue: dk, dcb (fp32, per key) and dV (fp16 into the dZ|dV buffer)
@@ -478,7 +557,7 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ q
         if (code == M) dcb[rowbase + key] = dka[mb][r];
       }
     const int NC = HM + D;
-    f16* drow = dzv + ((int64_t)b * N + key) * NC + HM + h * DV;
+    f16* drow = dzv + (tokbase + key) * NC + HM + h * DV;
 #pragma unroll
     for (int dvb = 0; dvb < DV / 32; ++dvb)
 #pragma unroll

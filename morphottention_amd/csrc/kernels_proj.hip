@@ -113,12 +113,13 @@ __global__ __launch_bounds__(256) void proj_fwd_kernel(const f16* __restrict__ X
           tii += wgt * phi * (2.f * phi - 1.f);
           U += fmaxf(0.f, wgt * (2.f * phi - 1.f));
         }
+        // rows: [phi_hi | aug | phi_lo | phi_hi] and [kc_hi | aug | kc_hi | kc_lo]
         *reinterpret_cast<f16x8*>(qrow + c8) = phh;
-        *reinterpret_cast<f16x8*>(qrow + M + c8) = phl;
-        *reinterpret_cast<f16x8*>(qrow + 2 * M + c8) = phh;
+        *reinterpret_cast<f16x8*>(qrow + M + 8 + c8) = phl;
+        *reinterpret_cast<f16x8*>(qrow + 2 * M + 8 + c8) = phh;
         *reinterpret_cast<f16x8*>(krow + c8) = kch;
-        *reinterpret_cast<f16x8*>(krow + M + c8) = kch;
-        *reinterpret_cast<f16x8*>(krow + 2 * M + c8) = kcl;
+        *reinterpret_cast<f16x8*>(krow + M + 8 + c8) = kch;
+        *reinterpret_cast<f16x8*>(krow + 2 * M + 8 + c8) = kcl;
       }
       // base-2 quantities: token bias b = -log2e * sum_c w_c phi_c; self score
       // t_ii and the upper bound U of any score in this query's row (without
@@ -131,8 +132,8 @@ __global__ __launch_bounds__(256) void proj_fwd_kernel(const f16* __restrict__ X
       split_hi_lo(-R, rh, rl);
       split_hi_lo(bias, bh_, bl_);
       const f16 one = (f16)1.f, zero = (f16)0.f;
-      *reinterpret_cast<f16x8*>(qrow + 3 * M) = f16x8{one, one, rh, rl, zero, zero, zero, zero};
-      *reinterpret_cast<f16x8*>(krow + 3 * M) = f16x8{bh_, bl_, one, one, zero, zero, zero, zero};
+      *reinterpret_cast<f16x8*>(qrow + M) = f16x8{one, one, rh, rl, zero, zero, zero, zero};
+      *reinterpret_cast<f16x8*>(krow + M) = f16x8{bh_, bl_, one, one, zero, zero, zero, zero};
       p.tstat[bhn] = make_float4(bias, R, Ub - t_ii, 0.f);
     }
     // values: 8 columns per item
@@ -200,7 +201,7 @@ __global__ __launch_bounds__(256) void proj_bwd_elem_kernel(const f16* __restric
     const int b = (int)(t / d.N), n = (int)(t - (int64_t)b * d.N);
     const int64_t bhn = (int64_t)(b * d.H + h) * d.N + n;
     const f16* qrow = p.qa + bhn * d.CW;
-    const float phi = (float)qrow[c] + (float)qrow[d.M + c];
+    const float phi = (float)qrow[c] + (float)qrow[d.M + 8 + c];
     const float dq = g.dq[bhn * d.M + c];
     const float dk = g.dk[bhn * d.M + c];
     const float dcb = g.dcb[bhn];
@@ -222,19 +223,34 @@ __global__ __launch_bounds__(256) void gate_reduce_kernel(const float* __restric
                                                           float scale, const f16* __restrict__ gate_q,
                                                           const f16* __restrict__ gate_k, f16* __restrict__ d_gate_q,
                                                           f16* __restrict__ d_gate_k) {
-  const int col = blockIdx.x * 256 + threadIdx.x;
-  if (col >= HM) return;
-  float s = 0.f;
-  for (int i = 0; i < nblk; ++i) s += gpart[(int64_t)i * HM + col];
-  const float dG = scale * s;
-  d_gate_q[col] = (f16)(dG * (float)gate_k[col]);
-  d_gate_k[col] = (f16)(dG * (float)gate_q[col]);
+  // 64 columns x 4 row groups per block; fixed summation order (deterministic)
+  __shared__ float part[4][64];
+  const int cl = threadIdx.x & 63, grp = threadIdx.x >> 6;
+  const int col = blockIdx.x * 64 + cl;
+  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+  if (col < HM) {
+    int i = grp;
+    for (; i + 12 < nblk; i += 16) {
+      s0 += gpart[(int64_t)i * HM + col];
+      s1 += gpart[(int64_t)(i + 4) * HM + col];
+      s2 += gpart[(int64_t)(i + 8) * HM + col];
+      s3 += gpart[(int64_t)(i + 12) * HM + col];
+    }
+    for (; i < nblk; i += 4) s0 += gpart[(int64_t)i * HM + col];
+  }
+  part[grp][cl] = (s0 + s1) + (s2 + s3);
+  __syncthreads();
+  if (grp == 0 && col < HM) {
+    const float dG = scale * ((part[0][cl] + part[1][cl]) + (part[2][cl] + part[3][cl]));
+    d_gate_q[col] = (f16)(dG * (float)gate_k[col]);
+    d_gate_k[col] = (f16)(dG * (float)gate_q[col]);
+  }
 }
 
 hipError_t launch_gate_reduce(const Dims& d, const BwdBuffers& g, const f16* gq, const f16* gk, f16* dgq, f16* dgk,
                               hipStream_t s) {
   const int nblk = (int)((d.T + kGateTokensPerBlock - 1) / kGateTokensPerBlock);
-  hipLaunchKernelGGL(gate_reduce_kernel, dim3((d.HM + 255) / 256), dim3(256), 0, s, g.gpart, nblk, d.HM, d.scale, gq,
+  hipLaunchKernelGGL(gate_reduce_kernel, dim3((d.HM + 63) / 64), dim3(256), 0, s, g.gpart, nblk, d.HM, d.scale, gq,
                      gk, dgq, dgk);
   return hipGetLastError();
 }
