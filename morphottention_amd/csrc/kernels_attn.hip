@@ -47,6 +47,18 @@ __device__ __forceinline__ constexpr int chunk_off(int c) {
   return c < M / 16 ? 16 * c : 16 * c + 8;
 }
 
+// Workgroups are dispatched round-robin over the 8 XCDs (id % 8), each with
+// its own L2. Map a 1-D grid of 8 * ceil(BH / 8) * nblk workgroups so that all
+// blocks of one (batch, head) run on the same XCD and share its L2: XCD x
+// serves heads x, x + 8, ... in turn. Returns false for the padding slots.
+__device__ __forceinline__ bool xcd_map(int nblk, int BH, int& bh, int& blk) {
+  const int i = blockIdx.x, xcd = i & 7, slot = i >> 3;
+  bh = 8 * (slot / nblk) + xcd;
+  blk = slot % nblk;
+  return bh < BH;
+}
+__host__ inline unsigned xcd_grid(int nblk, int BH) { return 8u * (unsigned)((BH + 7) / 8) * (unsigned)nblk; }
+
 // ============================================================ forward
 template <int M, int DV>
 struct FwdCfg {
@@ -184,14 +196,16 @@ template <int M, int DV>
 __global__ __launch_bounds__(256) void attn_fwd_kernel(const f16* __restrict__ qa, const f16* __restrict__ ka,
                                                        const f16* __restrict__ vv, const float4* __restrict__ tstat,
                                                        f16* __restrict__ out, float* __restrict__ lse, int N, int H,
-                                                       int D, int causal) {
+                                                       int D, int BH, int causal) {
   using C = FwdCfg<M, DV>;
   __shared__ __align__(16) f16 sK[2][C::KT * C::KS];
   __shared__ __align__(16) f16 sV[2][C::KT * C::VS];
   const int tid = threadIdx.x, lane = tid & 63, h32 = lane >> 5, l32 = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, scalar
-  const int bh = blockIdx.y;
-  const int qblk = causal ? (int)(gridDim.x - 1 - blockIdx.x) : (int)blockIdx.x;  // longest rows first
+  const int nqb = (N + C::QW - 1) / C::QW;
+  int bh, blk;
+  if (!xcd_map(nqb, BH, bh, blk)) return;
+  const int qblk = causal ? nqb - 1 - blk : blk;  // longest rows first
   const int q0 = qblk * C::QW, qw0 = q0 + 32 * w, q = qw0 + l32;
   const bool qvalid = q < N;
   const int b = bh / H, h = bh - b * H;
@@ -250,9 +264,9 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const f16* __restrict__ q
 template <int M, int DV>
 static hipError_t launch_attn_fwd_t(const Dims& d, const ProjBuffers& p, f16* out, float* lse, hipStream_t s) {
   using C = FwdCfg<M, DV>;
-  dim3 grid((d.N + C::QW - 1) / C::QW, d.B * d.H);
+  const dim3 grid(xcd_grid((d.N + C::QW - 1) / C::QW, d.B * d.H));
   hipLaunchKernelGGL((attn_fwd_kernel<M, DV>), grid, dim3(256), 0, s, p.qa, p.ka, p.v, p.tstat, out, lse, d.N, d.H,
-                     d.D, d.causal);
+                     d.D, d.B * d.H, d.causal);
   return hipGetLastError();
 }
 
@@ -405,7 +419,7 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ q
                                                        const f16* __restrict__ vv, const float2* __restrict__ qstat,
                                                        const f16* __restrict__ grad_out, float* __restrict__ dq,
                                                        float* __restrict__ dk, float* __restrict__ dcb,
-                                                       f16* __restrict__ dzv, int N, int H, int D, int HM,
+                                                       f16* __restrict__ dzv, int N, int H, int D, int HM, int BH,
                                                        int causal) {
   using C = BwdCfg<M, DV>;
   __shared__ __align__(16) f16 sQ[2][C::QT * C::QS];
@@ -415,8 +429,9 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ q
 
   const int tid = threadIdx.x, lane = tid & 63, h32 = lane >> 5, l32 = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, scalar
-  const int bh = blockIdx.y;
-  const int k0 = blockIdx.x * C::KW;  // causal: low key blocks see the most queries; they start first
+  int bh, kblk;
+  if (!xcd_map((N + C::KW - 1) / C::KW, BH, bh, kblk)) return;
+  const int k0 = kblk * C::KW;  // causal: low key blocks see the most queries; they start first
   const int kw0 = k0 + 32 * w;
   const int key = kw0 + l32;
   const bool kvalid = key < N;
@@ -574,9 +589,9 @@ template <int M, int DV>
 static hipError_t launch_attn_bwd_t(const Dims& d, const ProjBuffers& p, const f16* grad_out, const BwdBuffers& g,
                                     hipStream_t s) {
   using C = BwdCfg<M, DV>;
-  dim3 grid((d.N + C::KW - 1) / C::KW, d.B * d.H);
+  const dim3 grid(xcd_grid((d.N + C::KW - 1) / C::KW, d.B * d.H));
   hipLaunchKernelGGL((attn_bwd_kernel<M, DV>), grid, dim3(256), 0, s, p.qa, p.ka, p.v, g.qstat, grad_out, g.dq, g.dk,
-                     g.dcb, g.dzv, d.N, d.H, d.D, d.HM, d.causal);
+                     g.dcb, g.dzv, d.N, d.H, d.D, d.HM, d.B * d.H, d.causal);
   return hipGetLastError();
 }
 
