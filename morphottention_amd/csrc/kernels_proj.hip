@@ -57,10 +57,13 @@ __global__ __launch_bounds__(256) void proj_fwd_kernel(const f16* __restrict__ X
   __shared__ __align__(16) unsigned char smem[kMainBytes > kStageBytes ? kMainBytes : kStageBytes];
   constexpr int CW = 3 * M + 8;
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, wm = w >> 1, wn = w & 1;
-  const int n0 = blockIdx.x * kGemmBN, m0 = blockIdx.y * kGemmBM;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = w >> 1, wn = w & 1;
   const int NC = d.HM + d.D;
   const int T = (int)d.T;
+  int tm, tn;
+  if (!gemm_tile_map((T + kGemmBM - 1) / kGemmBM, (NC + kGemmBN - 1) / kGemmBN, tm, tn)) return;
+  const int n0 = tn * kGemmBN, m0 = tm * kGemmBM;
   OperandDesc A{X, d.D, nullptr, 0, INT_MAX};
   OperandDesc B{p.wt, d.D, nullptr, 0, INT_MAX};
   f32x16 acc[2][2];
@@ -160,7 +163,7 @@ __global__ __launch_bounds__(256) void proj_fwd_kernel(const f16* __restrict__ X
 template <int M, int DV>
 static hipError_t launch_proj_fwd_t(const Dims& d, const f16* X, const f16* gq, const f16* gk, const ProjBuffers& p,
                                     hipStream_t s) {
-  dim3 grid((d.HM + d.D + kGemmBN - 1) / kGemmBN, (unsigned)((d.T + kGemmBM - 1) / kGemmBM));
+  const dim3 grid(gemm_tile_grid((int)((d.T + kGemmBM - 1) / kGemmBM), (d.HM + d.D + kGemmBN - 1) / kGemmBN));
   hipLaunchKernelGGL((proj_fwd_kernel<M, DV>), grid, dim3(256), 0, s, X, gq, gk, d, p);
   return hipGetLastError();
 }
@@ -260,9 +263,12 @@ __global__ __launch_bounds__(256) void dx_gemm_kernel(const f16* __restrict__ W_
                                                       const f16* __restrict__ dzv, f16* __restrict__ dX, Dims d) {
   using ML = GemmMainloop<true, true>;
   __shared__ __align__(16) f16 smem[ML::kLdsHalves];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, wm = w >> 1, wn = w & 1;
-  const int n0 = blockIdx.x * kGemmBN, m0 = blockIdx.y * kGemmBM;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = w >> 1, wn = w & 1;
   const int T = (int)d.T, NC = d.HM + d.D;
+  int tm, tn;
+  if (!gemm_tile_map((T + kGemmBM - 1) / kGemmBM, (d.D + kGemmBN - 1) / kGemmBN, tm, tn)) return;
+  const int n0 = tn * kGemmBN, m0 = tm * kGemmBM;
   OperandDesc A{dzv, NC, nullptr, 0, INT_MAX};
   OperandDesc B{W_phi, d.HM, W_V, d.D, d.HM};
   f32x16 acc[2][2];
@@ -282,7 +288,7 @@ __global__ __launch_bounds__(256) void dx_gemm_kernel(const f16* __restrict__ W_
 
 hipError_t launch_dx_gemm(const Dims& d, const f16* W_phi, const f16* W_V, const BwdBuffers& g, f16* dX,
                           hipStream_t s) {
-  dim3 grid((d.D + kGemmBN - 1) / kGemmBN, (unsigned)((d.T + kGemmBM - 1) / kGemmBM));
+  const dim3 grid(gemm_tile_grid((int)((d.T + kGemmBM - 1) / kGemmBM), (d.D + kGemmBN - 1) / kGemmBN));
   hipLaunchKernelGGL(dx_gemm_kernel, grid, dim3(256), 0, s, W_phi, W_V, g.dzv, dX, d);
   return hipGetLastError();
 }
@@ -301,7 +307,8 @@ __global__ __launch_bounds__(256) void dw_gemm_kernel(const f16* __restrict__ X,
                                                       float* __restrict__ wpart, Dims d, int kchunk) {
   using ML = GemmMainloop<false, false>;
   __shared__ __align__(16) f16 smem[ML::kLdsHalves];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, wm = w >> 1, wn = w & 1;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = w >> 1, wn = w & 1;
   const int n0 = blockIdx.x * kGemmBN, m0 = blockIdx.y * kGemmBM, z = blockIdx.z;
   const int NC = d.HM + d.D;
   const int T = (int)d.T;
