@@ -71,6 +71,7 @@ int make_dims(int64_t B, int64_t N, int64_t D, int64_t H, int64_t M, float scale
   if (!(scale == scale)) return fail(MORPHO_ERR_INVALID_ARGUMENT, "scale must be a finite number");
   d.B = (int)B;
   d.N = (int)N;
+  d.NP = (int)((N + 63) / 64 * 64);
   d.D = (int)D;
   d.H = (int)H;
   d.M = (int)M;
@@ -88,7 +89,7 @@ size_t proj_bytes(const Dims& d) {
   size_t s = 0;
   s += align_up(bhn * d.CW * 2);         // qa
   s += align_up(bhn * d.CW * 2);         // ka
-  s += align_up(bhn * d.DV * 4);         // v (hi | lo)
+  s += align_up((size_t)d.B * d.H * d.NP * d.DV * 4);  // vt (hi | lo rows)
   s += align_up(bhn * 16);               // tstat
   s += align_up((size_t)(d.HM + d.D) * d.D * 2);  // wt
   return s;
@@ -100,7 +101,7 @@ ProjBuffers carve_proj(void* base, const Dims& d) {
   ProjBuffers b;
   b.qa = reinterpret_cast<_Float16*>(p); p += align_up(bhn * d.CW * 2);
   b.ka = reinterpret_cast<_Float16*>(p); p += align_up(bhn * d.CW * 2);
-  b.v = reinterpret_cast<_Float16*>(p); p += align_up(bhn * d.DV * 4);
+  b.vt = reinterpret_cast<_Float16*>(p); p += align_up((size_t)d.B * d.H * d.NP * d.DV * 4);
   b.tstat = reinterpret_cast<float4*>(p); p += align_up(bhn * 16);
   b.wt = reinterpret_cast<_Float16*>(p);
   return b;

@@ -9,6 +9,7 @@ namespace morpho {
 
 struct Dims {
   int B, N, D, H, M, DV;  // batch, tokens, model dim, heads, cube_m, head_dim_v
+  int NP;                 // N rounded up to a multiple of 64: row length of the V^T layout
   int64_t T;              // B * N tokens
   int HM;                 // H * M projection columns
   int CW;                 // 3 * M + 8: code row width (hi/lo split codes + affine augmentation)
@@ -31,7 +32,8 @@ struct Dims {
 struct ProjBuffers {
   _Float16* qa;    // [B*H, N, CW] query rows (columns 0..M-1 are phi_hi, M+8..2M+7 phi_lo)
   _Float16* ka;    // [B*H, N, CW] key rows
-  _Float16* v;     // [B*H, N, 2*DV] values X W_V per head: V_hi | V_lo
+  _Float16* vt;    // [B*H, 2*DV, NP] values X W_V per head, transposed: rows V_hi^T then V_lo^T,
+                   // zero for tokens N..NP-1
   float4* tstat;   // [B*H, N] {b, R, gap, 0}: token bias, softmax reference, bound gap (base 2)
   _Float16* wt;    // [H*M + D, D] transposed [W_phi | W_V]
 };

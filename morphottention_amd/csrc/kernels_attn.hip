@@ -70,10 +70,10 @@ struct FwdCfg {
   // with ds_read_b64_tr_b16 want 16 (mod 64) halves (4 rows x 4 chunks of a
   // 16-lane group hit distinct banks). CW = 3M + 8 is already 8 (mod 16).
   static constexpr int KS = CW;           // key row stride (halves)
-  static constexpr int VS = 2 * DV + 16;  // value row stride (halves): V_hi | V_lo | pad
+  static constexpr int VS = KT + 8;       // V^T tile row stride (halves): row = value column, 64 keys + pad
   static constexpr int QW = 128;          // queries per workgroup (4 waves x 32)
   static constexpr int KVEC = KT * CW / 8;
-  static constexpr int VVEC = KT * 2 * DV / 8;
+  static constexpr int VVEC = 2 * DV * KT / 8;
   static constexpr int NKR = (KVEC + 255) / 256;
   static constexpr int NVR = (VVEC + 255) / 256;
 };
@@ -84,74 +84,79 @@ struct FwdPrefetch {
   f16x8 kr[C::NKR];
   f16x8 vr[C::NVR];
 
-  __device__ __forceinline__ void load(const f16* __restrict__ ka, const f16* __restrict__ vv, int64_t rowbase, int N,
-                                       int k0, bool with_v, int tid) {
+  __device__ __forceinline__ void load_k(const f16* __restrict__ ka, int64_t rowbase, int N, int k0, int tid) {
 #pragma unroll
     for (int i = 0; i < C::NKR; ++i) {
       const int v = tid + 256 * i;
       const int r = v / (C::CW / 8), cv = (v % (C::CW / 8)) * 8;
-      // branch-free guard: read a clamped (valid) row, then zero it if out of range
+      // rows past N read the (finite) last row instead; every score they feed
+      // is masked. No select here: it would wait for the load to land.
       const int row = min(k0 + r, N - 1);
-      const f16x8 x = *reinterpret_cast<const f16x8*>(ka + (rowbase + row) * C::CW + (v < C::KVEC ? cv : 0));
-      kr[i] = (v < C::KVEC && k0 + r < N) ? x : f16x8{};
-    }
-    if (with_v) {
-#pragma unroll
-      for (int i = 0; i < C::NVR; ++i) {
-        const int v = tid + 256 * i;
-        const int r = v / (DV / 4), cv = (v % (DV / 4)) * 8;
-        const int row = min(k0 + r, N - 1);
-        const f16x8 x = *reinterpret_cast<const f16x8*>(vv + (rowbase + row) * (2 * DV) + (v < C::VVEC ? cv : 0));
-        vr[i] = (v < C::VVEC && k0 + r < N) ? x : f16x8{};
-      }
+      kr[i] = *reinterpret_cast<const f16x8*>(ka + (rowbase + row) * C::CW + (v < C::KVEC ? cv : 0));
     }
   }
+  // V^T rows are NP >= N + pad long and zero past N, so a 64-key tile never
+  // needs a guard.
+  __device__ __forceinline__ void load_v(const f16* __restrict__ vt, int64_t vbase, int NP, int k0, int tid) {
+#pragma unroll
+    for (int i = 0; i < C::NVR; ++i) {
+      const int v = tid + 256 * i;
+      const int r = v / (C::KT / 8), g = v % (C::KT / 8);
+      vr[i] = *reinterpret_cast<const f16x8*>(vt + vbase + (int64_t)r * NP + k0 + 8 * g);
+    }
+  }
+  __device__ __forceinline__ void load(const f16* __restrict__ ka, const f16* __restrict__ vt, int64_t vbase,
+                                       int64_t rowbase, int NP, int N, int k0, bool with_v, int tid) {
+    load_k(ka, rowbase, N, k0, tid);
+    if (with_v) load_v(vt, vbase, NP, k0, tid);
+  }
 
-  __device__ __forceinline__ void store(f16* sK, f16* sV, bool with_v, int tid) const {
+  // Key rows are stored in swap23 order within each 32-row block, so the lanes
+  // that read them in score order touch consecutive LDS rows (conflict-free
+  // 16-byte reads).
+  __device__ __forceinline__ void store_k(f16* sK, int tid) const {
 #pragma unroll
     for (int i = 0; i < C::NKR; ++i) {
       const int v = tid + 256 * i;
       const int r = v / (C::CW / 8), cv = (v % (C::CW / 8)) * 8;
-      if (v < C::KVEC) *reinterpret_cast<f16x8*>(sK + r * C::KS + cv) = kr[i];
+      const int lr = (r & ~31) | swap23(r & 31);
+      if (v < C::KVEC) *reinterpret_cast<f16x8*>(sK + lr * C::KS + cv) = kr[i];
     }
-    if (with_v) {
+  }
+  __device__ __forceinline__ void store_v(f16* sV, int tid) const {
 #pragma unroll
-      for (int i = 0; i < C::NVR; ++i) {
-        const int v = tid + 256 * i;
-        const int r = v / (DV / 4), cv = (v % (DV / 4)) * 8;
-        if (v < C::VVEC) *reinterpret_cast<f16x8*>(sV + r * C::VS + cv) = vr[i];
-      }
+    for (int i = 0; i < C::NVR; ++i) {
+      const int v = tid + 256 * i;
+      const int r = v / (C::KT / 8), g = v % (C::KT / 8);
+      *reinterpret_cast<f16x8*>(sV + r * C::VS + 8 * g) = vr[i];
     }
+  }
+  __device__ __forceinline__ void store(f16* sK, f16* sV, bool with_v, int tid) const {
+    store_k(sK, tid);
+    if (with_v) store_v(sV, tid);
   }
 };
 
 template <int M, int DV, bool MAXPASS>
-__device__ __forceinline__ void fwd_tile_loop(const f16* __restrict__ ka, const f16* __restrict__ vv, int64_t rowbase,
-                                              int N, int causal, int kend, int qw0, int q, f16 (*sK)[FwdCfg<M, DV>::KT *
-                                                                                                    FwdCfg<M, DV>::KS],
-                                              f16 (*sV)[FwdCfg<M, DV>::KT * FwdCfg<M, DV>::VS],
+__device__ __forceinline__ void fwd_tile_loop(const f16* __restrict__ ka, const f16* __restrict__ vt, int64_t vbase,
+                                              int64_t rowbase, int NP, int N, int causal, int t0, int kend, int qw0,
+                                              int q,
+                                              f16 (*sK)[FwdCfg<M, DV>::KT * FwdCfg<M, DV>::KS],
+                                              f16 (*sV)[2 * DV * FwdCfg<M, DV>::VS],
                                               const f16x8 (&qf)[FwdCfg<M, DV>::NCH], const f16x4& qaug,
                                               f32x16 (&o)[DV / 32], float& lsum, float& rmax) {
   using C = FwdCfg<M, DV>;
   const int tid = threadIdx.x, lane = tid & 63, h32 = lane >> 5, l32 = lane & 31;
-  const int nkt = (kend + C::KT - 1) / C::KT;
+  const int nkt = (kend + C::KT - 1) / C::KT - t0;
+  if (nkt <= 0) return;
   const int wave_kend = causal ? min(N, qw0 + 32) : N;
-  FwdPrefetch<M, DV> pf;
-  pf.load(ka, vv, rowbase, N, 0, !MAXPASS, tid);
-  pf.store(sK[0], sV[0], !MAXPASS, tid);
-  __syncthreads();
-  for (int kt = 0; kt < nkt; ++kt) {
-    const int k0 = kt * C::KT;
-    const int buf = kt & 1;
-    const bool more = kt + 1 < nkt;
-    if (more) pf.load(ka, vv, rowbase, N, k0 + C::KT, !MAXPASS, tid);
-    const f16* tK = sK[buf];
-    const f16* tV = sV[buf];
+
+  auto compute = [&](const f16* tK, const f16* tV, int k0) {
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       const int kbase = k0 + 32 * kb;
       if (kbase >= wave_kend) continue;  // wave-uniform
-      const f16* krow = tK + (32 * kb + swap23(l32)) * C::KS;
+      const f16* krow = tK + (32 * kb + l32) * C::KS;
       f32x16 s = {};
 #pragma unroll
       for (int c = 0; c < C::NCH; ++c)
@@ -177,29 +182,52 @@ __device__ __forceinline__ void fwd_tile_loop(const f16* __restrict__ ka, const 
         p1[r] = (f16)fast_exp2(s[r + 8]);
       }
       lsum += sum8(p0) + sum8(p1);
+      // O^T += V^T P: A rows are value columns (hi, then lo), k = key
 #pragma unroll
       for (int dvb = 0; dvb < DV / 32; ++dvb) {
+        const f16* vh = tV + (32 * dvb + l32) * C::VS + 32 * kb + 8 * h32;
+        const f16* vl = vh + DV * C::VS;
         f32x16 acc = o[dvb];
-        acc = mfma16(frag_kmajor(tV, C::VS, 32 * kb, 32 * dvb, lane), p0, acc);
-        acc = mfma16(frag_kmajor(tV, C::VS, 32 * kb + 16, 32 * dvb, lane), p1, acc);
-        acc = mfma16(frag_kmajor(tV, C::VS, 32 * kb, DV + 32 * dvb, lane), p0, acc);
-        acc = mfma16(frag_kmajor(tV, C::VS, 32 * kb + 16, DV + 32 * dvb, lane), p1, acc);
+        acc = mfma16(*reinterpret_cast<const f16x8*>(vh), p0, acc);
+        acc = mfma16(*reinterpret_cast<const f16x8*>(vh + 16), p1, acc);
+        acc = mfma16(*reinterpret_cast<const f16x8*>(vl), p0, acc);
+        acc = mfma16(*reinterpret_cast<const f16x8*>(vl + 16), p1, acc);
         o[dvb] = acc;
       }
     }
-    if (more) pf.store(sK[buf ^ 1], sV[buf ^ 1], !MAXPASS, tid);
+  };
+
+  // Two register stages: while tile kt is consumed from LDS, the loads of
+  // tiles kt+1 and kt+2 are in flight; unrolled by two so a stage never
+  // changes registers while its loads are outstanding.
+  FwdPrefetch<M, DV> pf0, pf1;
+  const int kb0 = t0 * C::KT;
+  pf0.load(ka, vt, vbase, rowbase, NP, N, kb0, !MAXPASS, tid);
+  pf0.store(sK[0], sV[0], !MAXPASS, tid);
+  if (nkt > 1) pf1.load(ka, vt, vbase, rowbase, NP, N, kb0 + C::KT, !MAXPASS, tid);
+  if (nkt > 2) pf0.load(ka, vt, vbase, rowbase, NP, N, kb0 + 2 * C::KT, !MAXPASS, tid);
+  __syncthreads();
+  for (int kt = 0; kt < nkt; kt += 2) {
+    compute(sK[0], sV[0], kb0 + kt * C::KT);
+    if (kt + 1 < nkt) pf1.store(sK[1], sV[1], !MAXPASS, tid);
     __syncthreads();
+    if (kt + 3 < nkt) pf1.load(ka, vt, vbase, rowbase, NP, N, kb0 + (kt + 3) * C::KT, !MAXPASS, tid);
+    if (kt + 1 >= nkt) break;
+    compute(sK[1], sV[1], kb0 + (kt + 1) * C::KT);
+    if (kt + 2 < nkt) pf0.store(sK[0], sV[0], !MAXPASS, tid);
+    __syncthreads();
+    if (kt + 4 < nkt) pf0.load(ka, vt, vbase, rowbase, NP, N, kb0 + (kt + 4) * C::KT, !MAXPASS, tid);
   }
 }
 
 template <int M, int DV>
 __global__ __launch_bounds__(256) void attn_fwd_kernel(const f16* __restrict__ qa, const f16* __restrict__ ka,
-                                                       const f16* __restrict__ vv, const float4* __restrict__ tstat,
-                                                       f16* __restrict__ out, float* __restrict__ lse, int N, int H,
-                                                       int D, int BH, int causal) {
+                                                       const f16* __restrict__ vt, const float4* __restrict__ tstat,
+                                                       f16* __restrict__ out, float* __restrict__ lse, int N, int NP,
+                                                       int H, int D, int BH, int causal) {
   using C = FwdCfg<M, DV>;
   __shared__ __align__(16) f16 sK[2][C::KT * C::KS];
-  __shared__ __align__(16) f16 sV[2][C::KT * C::VS];
+  __shared__ __align__(16) f16 sV[2][2 * DV * C::VS];
   const int tid = threadIdx.x, lane = tid & 63, h32 = lane >> 5, l32 = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, scalar
   const int nqb = (N + C::QW - 1) / C::QW;
@@ -210,6 +238,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const f16* __restrict__ q
   const bool qvalid = q < N;
   const int b = bh / H, h = bh - b * H;
   const int64_t rowbase = (int64_t)bh * N;
+  const int64_t vbase = (int64_t)bh * 2 * DV * NP;
 
   f16x8 qf[C::NCH];
   f16x4 qaug = {};
@@ -235,14 +264,14 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const f16* __restrict__ q
     // pass 1: exact row max of the base-2 exponent without the reference
     f16x4 qa0 = qaug;
     if (h32 == 0) { qa0[2] = (f16)0.f; qa0[3] = (f16)0.f; }
-    fwd_tile_loop<M, DV, true>(ka, vv, rowbase, N, causal, kend, qw0, q, sK, sV, qf, qa0, o, lsum, rmax);
+    fwd_tile_loop<M, DV, true>(ka, vt, vbase, rowbase, NP, N, causal, 0, kend, qw0, q, sK, sV, qf, qa0, o, lsum, rmax);
     rmax = fmaxf(rmax, __shfl_xor(rmax, 32));
     R = qvalid ? rmax : 0.f;
     f16 rh, rl;
     split_hi_lo(-R, rh, rl);
     if (h32 == 0) { qaug[2] = rh; qaug[3] = rl; }
   }
-  fwd_tile_loop<M, DV, false>(ka, vv, rowbase, N, causal, kend, qw0, q, sK, sV, qf, qaug, o, lsum, rmax);
+  fwd_tile_loop<M, DV, false>(ka, vt, vbase, rowbase, NP, N, causal, 0, kend, qw0, q, sK, sV, qf, qaug, o, lsum, rmax);
 
   const float ltot = lsum + __shfl_xor(lsum, 32);
   if (qvalid) {
@@ -265,8 +294,8 @@ template <int M, int DV>
 static hipError_t launch_attn_fwd_t(const Dims& d, const ProjBuffers& p, f16* out, float* lse, hipStream_t s) {
   using C = FwdCfg<M, DV>;
   const dim3 grid(xcd_grid((d.N + C::QW - 1) / C::QW, d.B * d.H));
-  hipLaunchKernelGGL((attn_fwd_kernel<M, DV>), grid, dim3(256), 0, s, p.qa, p.ka, p.v, p.tstat, out, lse, d.N, d.H,
-                     d.D, d.B * d.H, d.causal);
+  hipLaunchKernelGGL((attn_fwd_kernel<M, DV>), grid, dim3(256), 0, s, p.qa, p.ka, p.vt, p.tstat, out, lse, d.N, d.NP,
+                     d.H, d.D, d.B * d.H, d.causal);
   return hipGetLastError();
 }
 
@@ -416,10 +445,10 @@ struct BwdPrefetch {
 
 template <int M, int DV>
 __global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ qa, const f16* __restrict__ ka,
-                                                       const f16* __restrict__ vv, const float2* __restrict__ qstat,
+                                                       const f16* __restrict__ vt, const float2* __restrict__ qstat,
                                                        const f16* __restrict__ grad_out, float* __restrict__ dq,
                                                        float* __restrict__ dk, float* __restrict__ dcb,
-                                                       f16* __restrict__ dzv, int N, int H, int D, int HM, int BH,
+                                                       f16* __restrict__ dzv, int N, int NP, int H, int D, int HM, int BH,
                                                        int causal) {
   using C = BwdCfg<M, DV>;
   __shared__ __align__(16) f16 sQ[2][C::QT * C::QS];
@@ -453,9 +482,13 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ q
 #pragma unroll
     for (int c = 0; c < C::NCH; ++c) kf[c] = *reinterpret_cast<const f16x8*>(krow + chunk_off<M>(c) + 8 * h32);
     kaug = *reinterpret_cast<const f16x4*>(krow + M + 4 * h32);
-    const f16* vrow = vv + (rowbase + key) * (2 * DV);
+    // V_hi[key][16c + 8 h32 + j] from the transposed layout (a wave reads 32
+    // consecutive keys of each value column)
+    const f16* vcol = vt + (int64_t)bh * 2 * DV * NP + key;
 #pragma unroll
-    for (int c = 0; c < DV / 16; ++c) vf[c] = *reinterpret_cast<const f16x8*>(vrow + 16 * c + 8 * h32);
+    for (int c = 0; c < DV / 16; ++c)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) vf[c][j] = vcol[(int64_t)(16 * c + 8 * h32 + j) * NP];
   }
   const f16x4 vaug = h32 == 0 ? f16x4{one, one, zero, zero} : f16x4{zero, zero, zero, zero};
   // phi_hi of the workgroup's keys for the dq product (zero past N)
@@ -477,18 +510,24 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ q
   // keys of this workgroup that exist: dq contracts over [0, kw_valid) only
   const int nkey = min(C::KW, N - k0);
 
-  BwdPrefetch<M, DV> pf;
+  // Two register stages (see the forward): step s computes from LDS buffer
+  // s & 1 while the loads of steps s+1 and s+2 are in flight.
+  BwdPrefetch<M, DV> pf0, pf1;
+  auto pf_load = [&](BwdPrefetch<M, DV>& pf, int step) {
+    pf.load(qa, grad_out, qstat, rowbase, tokbase, h * DV, N, D, qstart + step * C::QT, tid);
+  };
   if (nsteps > 0) {
-    pf.load(qa, grad_out, qstat, rowbase, tokbase, h * DV, N, D, qstart, tid);
-    pf.store(sQ[0], sO[0], tid);
+    pf_load(pf0, 0);
+    pf0.store(sQ[0], sO[0], tid);
   }
+  if (nsteps > 1) pf_load(pf1, 1);
+  if (nsteps > 2) pf_load(pf0, 2);
   __syncthreads();
 
   for (int step = 0; step < nsteps; ++step) {
     const int buf = step & 1;
     const int qs = qstart + step * C::QT;
     const bool more = step + 1 < nsteps;
-    if (more) pf.load(qa, grad_out, qstat, rowbase, tokbase, h * DV, N, D, qs + C::QT, tid);
     const f16* tQ = sQ[buf];
     const f16* tO = sO[buf];
     f16* tS = sdS[buf] + (32 * w + l32) * C::SS;  // this lane's key row
@@ -538,8 +577,15 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ q
 #pragma unroll
       for (int c = 0; c < 2; ++c) *reinterpret_cast<f16x8*>(tS + 32 * sb + 16 * c + 8 * h32) = ds16[c];
     }
-    if (more) pf.store(sQ[buf ^ 1], sO[buf ^ 1], tid);
+    if (more) {
+      if (buf == 0) pf1.store(sQ[1], sO[1], tid);
+      else pf0.store(sQ[0], sO[0], tid);
+    }
     __syncthreads();  // dS^T of all four waves complete; next tiles visible
+    if (step + 3 < nsteps) {
+      if (buf == 0) pf_load(pf1, step + 3);
+      else pf_load(pf0, step + 3);
+    }
     // dq[q][code] += sum_key dS[q][key] phi[key][code]: 16 x 16 output tiles
     // split over the waves, contraction over the workgroup's keys.
 #pragma unroll
@@ -590,8 +636,8 @@ static hipError_t launch_attn_bwd_t(const Dims& d, const ProjBuffers& p, const f
                                     hipStream_t s) {
   using C = BwdCfg<M, DV>;
   const dim3 grid(xcd_grid((d.N + C::KW - 1) / C::KW, d.B * d.H));
-  hipLaunchKernelGGL((attn_bwd_kernel<M, DV>), grid, dim3(256), 0, s, p.qa, p.ka, p.v, g.qstat, grad_out, g.dq, g.dk,
-                     g.dcb, g.dzv, d.N, d.H, d.D, d.HM, d.B * d.H, d.causal);
+  hipLaunchKernelGGL((attn_bwd_kernel<M, DV>), grid, dim3(256), 0, s, p.qa, p.ka, p.vt, g.qstat, grad_out, g.dq, g.dk,
+                     g.dcb, g.dzv, d.N, d.NP, d.H, d.D, d.HM, d.B * d.H, d.causal);
   return hipGetLastError();
 }
 

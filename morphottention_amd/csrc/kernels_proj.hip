@@ -139,23 +139,53 @@ __global__ __launch_bounds__(256) void proj_fwd_kernel(const f16* __restrict__ X
       *reinterpret_cast<f16x8*>(krow + M) = f16x8{bh_, bl_, one, one, zero, zero, zero, zero};
       p.tstat[bhn] = make_float4(bias, R, Ub - t_ii, 0.f);
     }
-    // values: 8 columns per item
-    for (int idx = tid; idx < 64 * (kGemmBN / 8); idx += 256) {
-      const int r = idx / (kGemmBN / 8), cv = (idx % (kGemmBN / 8)) * 8;
-      const int col = n0 + cv, t = row0 + r;
-      if (col < d.HM || col >= NC || t >= T) continue;
-      const int vcol = col - d.HM, h = vcol / DV, dd = vcol % DV;
-      const int b = t / d.N, n = t - b * d.N;
-      const float* src = stage + r * kStageStride + cv;
-      f16x8 vh, vl;
+    // values, transposed: vt[bh][dd][n] = V_hi, vt[bh][DV + dd][n] = V_lo.
+    // One item = one column x 8 consecutive tokens; 8 neighbouring threads
+    // cover 64 consecutive tokens of a column (128 contiguous bytes).
+    if (n0 + kGemmBN > d.HM) {  // the tile has value columns (uniform)
+      const bool vec = d.N % 8 == 0;
+      for (int idx = tid; idx < 8 * kGemmBN; idx += 256) {
+        const int rg = idx & 7, cc = idx >> 3;
+        const int col = n0 + cc, tb = row0 + 8 * rg;
+        if (col < d.HM || col >= NC || tb >= T) continue;
+        const int vcol = col - d.HM, h = vcol / DV, dd = vcol % DV;
+        const float* src = stage + 8 * rg * kStageStride + cc;
+        if (vec) {
+          // N % 8 == 0 and tb % 8 == 0: the 8 tokens share one batch row
+          const int b = tb / d.N, n = tb - b * d.N;
+          f16x8 vh, vl;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        vh[e] = (f16)src[e];
-        vl[e] = (f16)(src[e] - (float)vh[e]);
+          for (int e = 0; e < 8; ++e) {
+            const float x = src[e * kStageStride];
+            vh[e] = (f16)x;
+            vl[e] = (f16)(x - (float)vh[e]);
+          }
+          f16* dst = p.vt + ((int64_t)(b * d.H + h) * 2 * DV + dd) * d.NP + n;
+          const int64_t lo = (int64_t)DV * d.NP;
+          *reinterpret_cast<f16x8*>(dst) = vh;
+          *reinterpret_cast<f16x8*>(dst + lo) = vl;
+          if (n + 8 == d.N)
+            for (int z = 8; n + z < d.NP; z += 8) {
+              *reinterpret_cast<f16x8*>(dst + z) = f16x8{};
+              *reinterpret_cast<f16x8*>(dst + lo + z) = f16x8{};
+            }
+        } else {
+          for (int e = 0; e < 8 && tb + e < T; ++e) {
+            const int t = tb + e, b = t / d.N, n = t - b * d.N;
+            const float x = src[e * kStageStride];
+            const f16 vh = (f16)x, vl = (f16)(x - (float)vh);
+            f16* dst = p.vt + ((int64_t)(b * d.H + h) * 2 * DV + dd) * d.NP + n;
+            const int64_t lo = (int64_t)DV * d.NP;
+            dst[0] = vh;
+            dst[lo] = vl;
+            if (n == d.N - 1)
+              for (int z = 1; n + z < d.NP; ++z) {
+                dst[z] = (f16)0.f;
+                dst[lo + z] = (f16)0.f;
+              }
+          }
+        }
       }
-      f16* dst = p.v + ((int64_t)(b * d.H + h) * d.N + n) * (2 * DV) + dd;
-      *reinterpret_cast<f16x8*>(dst) = vh;
-      *reinterpret_cast<f16x8*>(dst + DV) = vl;
     }
   }
 }
