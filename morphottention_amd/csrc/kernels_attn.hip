@@ -60,103 +60,149 @@ __device__ __forceinline__ bool xcd_map(int nblk, int BH, int& bh, int& blk) {
 __host__ inline unsigned xcd_grid(int nblk, int BH) { return 8u * (unsigned)((BH + 7) / 8) * (unsigned)nblk; }
 
 // ============================================================ forward
+// s_waitcnt on the vector-memory counter only (gfx9 encoding: vmcnt[3:0],
+// expcnt[6:4] = 7 and lgkmcnt[11:8] = 15 mean "no wait", vmcnt[5:4] at [15:14]).
+template <int CNT>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(CNT >= 0 && CNT < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((CNT & 15) | (7 << 4) | (15 << 8) | ((CNT >> 4) << 14));
+}
+
+// 16 bytes per lane from global memory straight into LDS: lane l of the wave
+// writes LDS byte address lds_addr + 16 l (lds_addr wave-uniform). Issued as
+// inline asm so that the compiler does not order every later LDS read after
+// it: the callers wait for these loads explicitly (wait_vmcnt) before the
+// barrier that publishes a stage.
+__device__ __forceinline__ void lds_dma16(const f16* g, unsigned lds_addr) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds_addr))
+               : "memory", "m0");
+}
+
+// XOR swizzle of the 16-byte chunk index within a 128-byte V^T tile row: the
+// 16 rows one b128 read phase touches land on distinct bank groups.
+__device__ __forceinline__ int vswz(int r) { return (r ^ (r >> 3)) & 7; }
+
 template <int M, int DV>
 struct FwdCfg {
   static constexpr int CW = 3 * M + 8;    // code row width
   static constexpr int NCH = 3 * M / 16;  // 16-wide code chunks
-  static constexpr int KT = 64;           // keys per LDS tile
-  // LDS strides: rows read with ds_read_b128 want a stride = 8 (mod 16) halves
-  // (8 consecutive rows then hit 8 distinct 16-byte bank groups); rows read
-  // with ds_read_b64_tr_b16 want 16 (mod 64) halves (4 rows x 4 chunks of a
-  // 16-lane group hit distinct banks). CW = 3M + 8 is already 8 (mod 16).
-  static constexpr int KS = CW;           // key row stride (halves)
-  static constexpr int VS = KT + 8;       // V^T tile row stride (halves): row = value column, 64 keys + pad
-  static constexpr int QW = 128;          // queries per workgroup (4 waves x 32)
-  static constexpr int KVEC = KT * CW / 8;
-  static constexpr int VVEC = 2 * DV * KT / 8;
-  static constexpr int NKR = (KVEC + 255) / 256;
-  static constexpr int NVR = (VVEC + 255) / 256;
+  static constexpr int KT = 64;           // keys per tile
+  static constexpr int WAVES = 8;
+  static constexpr int QW = 32 * WAVES;   // queries per workgroup
+  // A stage holds one key tile [KT][CW] (rows in swap23 order within each 32,
+  // unpadded: CW = 8 (mod 16) halves keeps b128 reads conflict-free) and one
+  // V^T tile [2 DV][KT] (V_hi^T rows, then V_lo^T rows, chunk-swizzled), both
+  // filled by 1 KiB DMA chunks spread evenly over the waves.
+  static constexpr int KCH = CW / 8;      // key tile chunks
+  static constexpr int VCH = DV / 4;      // V^T tile chunks
+  static constexpr int NPW = (KCH + VCH + WAVES - 1) / WAVES;  // chunks per wave per tile
+  static constexpr int NPW_K = (KCH + WAVES - 1) / WAVES;      // key-only tiles (exact-max pass)
+  static constexpr int VOFF = KCH * 512;  // V^T offset in a stage (halves)
+  static constexpr int STAGE = WAVES * NPW * 512;              // halves, incl. padding chunks
+  // Two workgroups per CU (4 waves per SIMD, <= 128 VGPRs) when the code is
+  // narrow and two stages fit in half the 160 KiB LDS (less 1 KiB for the
+  // rest); otherwise one workgroup with the registers and LDS to itself.
+  // PIPE: software-pipelined main loop (steps S(j+1) | E(j) | PV(j-1)), which
+  // needs the registers of two waves per SIMD; otherwise tile-at-a-time code
+  // with four waves per SIMD. The latter measures faster on MI355X.
+  static constexpr bool PIPE = false;
+  static constexpr bool TWO = !PIPE && M == 16 && 2 * STAGE * 2 <= 79 * 1024;
+  static constexpr int WG_PER_CU = TWO ? 2 : 1;
+  static constexpr int LDS_BUDGET = (TWO ? 79 : 158) * 1024;
+  static constexpr int NSTAGE = 3 * STAGE * 2 <= LDS_BUDGET ? 3 : 2;
 };
 
-template <int M, int DV>
-struct FwdPrefetch {
-  using C = FwdCfg<M, DV>;
-  f16x8 kr[C::NKR];
-  f16x8 vr[C::NVR];
-
-  __device__ __forceinline__ void load_k(const f16* __restrict__ ka, int64_t rowbase, int N, int k0, int tid) {
-#pragma unroll
-    for (int i = 0; i < C::NKR; ++i) {
-      const int v = tid + 256 * i;
-      const int r = v / (C::CW / 8), cv = (v % (C::CW / 8)) * 8;
-      // rows past N read the (finite) last row instead; every score they feed
-      // is masked. No select here: it would wait for the load to land.
-      const int row = min(k0 + r, N - 1);
-      kr[i] = *reinterpret_cast<const f16x8*>(ka + (rowbase + row) * C::CW + (v < C::KVEC ? cv : 0));
-    }
-  }
-  // V^T rows are NP >= N + pad long and zero past N, so a 64-key tile never
-  // needs a guard.
-  __device__ __forceinline__ void load_v(const f16* __restrict__ vt, int64_t vbase, int NP, int k0, int tid) {
-#pragma unroll
-    for (int i = 0; i < C::NVR; ++i) {
-      const int v = tid + 256 * i;
-      const int r = v / (C::KT / 8), g = v % (C::KT / 8);
-      vr[i] = *reinterpret_cast<const f16x8*>(vt + vbase + (int64_t)r * NP + k0 + 8 * g);
-    }
-  }
-  __device__ __forceinline__ void load(const f16* __restrict__ ka, const f16* __restrict__ vt, int64_t vbase,
-                                       int64_t rowbase, int NP, int N, int k0, bool with_v, int tid) {
-    load_k(ka, rowbase, N, k0, tid);
-    if (with_v) load_v(vt, vbase, NP, k0, tid);
-  }
-
-  // Key rows are stored in swap23 order within each 32-row block, so the lanes
-  // that read them in score order touch consecutive LDS rows (conflict-free
-  // 16-byte reads).
-  __device__ __forceinline__ void store_k(f16* sK, int tid) const {
-#pragma unroll
-    for (int i = 0; i < C::NKR; ++i) {
-      const int v = tid + 256 * i;
-      const int r = v / (C::CW / 8), cv = (v % (C::CW / 8)) * 8;
-      const int lr = (r & ~31) | swap23(r & 31);
-      if (v < C::KVEC) *reinterpret_cast<f16x8*>(sK + lr * C::KS + cv) = kr[i];
-    }
-  }
-  __device__ __forceinline__ void store_v(f16* sV, int tid) const {
-#pragma unroll
-    for (int i = 0; i < C::NVR; ++i) {
-      const int v = tid + 256 * i;
-      const int r = v / (C::KT / 8), g = v % (C::KT / 8);
-      *reinterpret_cast<f16x8*>(sV + r * C::VS + 8 * g) = vr[i];
-    }
-  }
-  __device__ __forceinline__ void store(f16* sK, f16* sV, bool with_v, int tid) const {
-    store_k(sK, tid);
-    if (with_v) store_v(sV, tid);
-  }
-};
-
+// One pass over the key tiles [0, kend) of a workgroup. Tiles stream through
+// NSTAGE LDS stages by DMA: tile t + NSTAGE - 1 is issued right after the
+// barrier that opens tile t (its stage last served tile t - 1, which every wave
+// finished before that barrier), so each tile has NSTAGE - 1 tiles of compute
+// to arrive; one barrier per tile.
+// MAXPASS: key tiles only, track the row max of the exponent (exact path).
 template <int M, int DV, bool MAXPASS>
-__device__ __forceinline__ void fwd_tile_loop(const f16* __restrict__ ka, const f16* __restrict__ vt, int64_t vbase,
-                                              int64_t rowbase, int NP, int N, int causal, int t0, int kend, int qw0,
-                                              int q,
-                                              f16 (*sK)[FwdCfg<M, DV>::KT * FwdCfg<M, DV>::KS],
-                                              f16 (*sV)[2 * DV * FwdCfg<M, DV>::VS],
-                                              const f16x8 (&qf)[FwdCfg<M, DV>::NCH], const f16x4& qaug,
-                                              f32x16 (&o)[DV / 32], float& lsum, float& rmax) {
+__device__ __forceinline__ void fwd_pass(const f16* __restrict__ ka, const f16* __restrict__ vt, int64_t rowbase,
+                                         int64_t vbase, int N, int NP, int causal, int kend, int q0, int qw0,
+                                         int q, f16* smem, const f16x8 (&qf)[FwdCfg<M, DV>::NCH], const f16x4& qaug,
+                                         f32x16 (&o)[DV / 32], float& lsum, float& rmax) {
   using C = FwdCfg<M, DV>;
+  constexpr int NPWX = MAXPASS ? C::NPW_K : C::NPW;
   const int tid = threadIdx.x, lane = tid & 63, h32 = lane >> 5, l32 = lane & 31;
-  const int nkt = (kend + C::KT - 1) / C::KT - t0;
-  if (nkt <= 0) return;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nkt = (kend + C::KT - 1) / C::KT;
   const int wave_kend = causal ? min(N, qw0 + 32) : N;
 
-  auto compute = [&](const f16* tK, const f16* tV, int k0) {
+  // LDS byte address of the stage area (the DMA takes raw LDS addresses)
+  const unsigned sbase = (unsigned)(uintptr_t)(__attribute__((address_space(3))) f16*)smem;
+  auto issue = [&](int t) {
+    const unsigned st = sbase + 2u * (unsigned)((t % C::NSTAGE) * C::STAGE);
+    const int k0 = t * C::KT;
+#pragma unroll
+    for (int i = 0; i < NPWX; ++i) {
+      const int c = w + C::WAVES * i;  // wave-uniform chunk id
+      const f16* src;
+      if (c < C::KCH) {
+        const int p = 64 * c + lane;
+        const int row = p / (C::CW / 8), col = 8 * (p % (C::CW / 8));
+        // rows past N read the (finite) last row; every score they feed is masked
+        const int key = min(k0 + ((row & ~31) | swap23(row & 31)), N - 1);
+        src = ka + (rowbase + key) * C::CW + col;
+      } else if (!MAXPASS && c < C::KCH + C::VCH) {
+        const int pv = 64 * (c - C::KCH) + lane;
+        const int r = pv >> 3, lc = (pv & 7) ^ vswz(r);
+        src = vt + vbase + (int64_t)r * NP + k0 + 8 * lc;  // V^T rows are zero past N
+      } else {
+        src = ka + (rowbase + min(k0 + lane, N - 1)) * C::CW;  // padding chunk: any in-bounds bytes
+      }
+      lds_dma16(src, st + 1024u * (unsigned)c);
+    }
+  };
+
+  // This lane's V^T fragment offsets within a stage. Row 32 j + l32 has
+  // swizzle vswz(l32) ^ 4 (j & 1), so the chunk of key half p of block kb is
+  //   4 (kb ^ z2 ^ (j & 1)) + 2 (p ^ z1) + (h32 ^ z0)   (z = vswz(l32) bits),
+  // i.e. four per-lane offsets cover every (kb, p, j) up to a constant.
+  int vofs[2][2];
+  {
+    const int z = vswz(l32);
+#pragma unroll
+    for (int x = 0; x < 2; ++x)
+#pragma unroll
+      for (int p = 0; p < 2; ++p)
+        vofs[x][p] = C::VOFF + l32 * C::KT + 8 * (4 * (x ^ (z >> 2)) + 2 * (p ^ ((z >> 1) & 1)) + (h32 ^ (z & 1)));
+  }
+  // O^T += V^T P for the 32 keys of block kb: A rows are value columns (hi,
+  // then lo), k = key. The DV / 32 accumulators are independent and are
+  // interleaved, so consecutive MFMAs never wait on each other.
+  auto pv = [&](const f16* tile, int kb, const f16x8& p0, const f16x8& p1) {
+#pragma unroll
+    for (int part = 0; part < 4; ++part) {  // (hi, k 0-15), (hi, k 16-31), (lo, ...), (lo, ...)
+#pragma unroll
+      for (int dvb = 0; dvb < DV / 32; ++dvb) {
+        const int j = (part >= 2 ? DV / 32 : 0) + dvb;  // 32-row block of the V^T tile
+        const f16* src = tile + vofs[kb ^ (j & 1)][part & 1] + 32 * C::KT * j;
+        o[dvb] = mfma16(*reinterpret_cast<const f16x8*>(src), (part & 1) ? p1 : p0, o[dvb]);
+      }
+    }
+  };
+  auto expo = [&](const f32x16& s, f16x8& p0, f16x8& p1) {
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      p0[r] = (f16)fast_exp2(s[r]);
+      p1[r] = (f16)fast_exp2(s[r + 8]);
+    }
+    lsum += sum8(p0) + sum8(p1);
+  };
+
+  auto stage = [&](int t) { return smem + (t % C::NSTAGE) * C::STAGE; };
+
+  // Any tile: per 32-key block, with masks where needed.
+  auto compute = [&](const f16* tile, int k0) {
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       const int kbase = k0 + 32 * kb;
       if (kbase >= wave_kend) continue;  // wave-uniform
-      const f16* krow = tK + (32 * kb + l32) * C::KS;
+      const f16* krow = tile + (32 * kb + l32) * C::CW;
       f32x16 s = {};
 #pragma unroll
       for (int c = 0; c < C::NCH; ++c)
@@ -176,58 +222,147 @@ __device__ __forceinline__ void fwd_tile_loop(const f16* __restrict__ ka, const 
         continue;
       }
       f16x8 p0, p1;
-#pragma unroll
-      for (int r = 0; r < 8; ++r) {
-        p0[r] = (f16)fast_exp2(s[r]);
-        p1[r] = (f16)fast_exp2(s[r + 8]);
-      }
-      lsum += sum8(p0) + sum8(p1);
-      // O^T += V^T P: A rows are value columns (hi, then lo), k = key
-#pragma unroll
-      for (int dvb = 0; dvb < DV / 32; ++dvb) {
-        const f16* vh = tV + (32 * dvb + l32) * C::VS + 32 * kb + 8 * h32;
-        const f16* vl = vh + DV * C::VS;
-        f32x16 acc = o[dvb];
-        acc = mfma16(*reinterpret_cast<const f16x8*>(vh), p0, acc);
-        acc = mfma16(*reinterpret_cast<const f16x8*>(vh + 16), p1, acc);
-        acc = mfma16(*reinterpret_cast<const f16x8*>(vl), p0, acc);
-        acc = mfma16(*reinterpret_cast<const f16x8*>(vl + 16), p1, acc);
-        o[dvb] = acc;
-      }
+      expo(s, p0, p1);
+      pv(tile, kb, p0, p1);
     }
   };
 
-  // Two register stages: while tile kt is consumed from LDS, the loads of
-  // tiles kt+1 and kt+2 are in flight; unrolled by two so a stage never
-  // changes registers while its loads are outstanding.
-  FwdPrefetch<M, DV> pf0, pf1;
-  const int kb0 = t0 * C::KT;
-  pf0.load(ka, vt, vbase, rowbase, NP, N, kb0, !MAXPASS, tid);
-  pf0.store(sK[0], sV[0], !MAXPASS, tid);
-  if (nkt > 1) pf1.load(ka, vt, vbase, rowbase, NP, N, kb0 + C::KT, !MAXPASS, tid);
-  if (nkt > 2) pf0.load(ka, vt, vbase, rowbase, NP, N, kb0 + 2 * C::KT, !MAXPASS, tid);
-  __syncthreads();
-  for (int kt = 0; kt < nkt; kt += 2) {
-    compute(sK[0], sV[0], kb0 + kt * C::KT);
-    if (kt + 1 < nkt) pf1.store(sK[1], sV[1], !MAXPASS, tid);
-    __syncthreads();
-    if (kt + 3 < nkt) pf1.load(ka, vt, vbase, rowbase, NP, N, kb0 + (kt + 3) * C::KT, !MAXPASS, tid);
-    if (kt + 1 >= nkt) break;
-    compute(sK[1], sV[1], kb0 + (kt + 1) * C::KT);
-    if (kt + 2 < nkt) pf0.store(sK[0], sV[0], !MAXPASS, tid);
-    __syncthreads();
-    if (kt + 4 < nkt) pf0.load(ka, vt, vbase, rowbase, NP, N, kb0 + (kt + 4) * C::KT, !MAXPASS, tid);
+  int next_issue = 0;  // tiles [0, next_issue) have been issued
+  auto issue_upto = [&](int t) {
+    for (; next_issue <= t && next_issue < nkt; ++next_issue) issue(next_issue);
+  };
+  // wait until tile t has landed in every wave's share, then publish it
+  auto publish = [&](int t) {
+    if (next_issue > t + 1)
+      wait_vmcnt<NPWX>();  // tile t + 1 may stay in flight (never more than one tile beyond t)
+    else
+      wait_vmcnt<0>();
+    __builtin_amdgcn_s_barrier();
+  };
+
+  int t = 0;
+  issue_upto(1);
+  if (!MAXPASS && !C::PIPE) {
+    // ---- tiles whose 64 keys are unmasked for every wave, one at a time. In
+    // program order [S0 chain] [S1 chain, exp S0] [P0.V, exp S1] [P1.V]: the
+    // exponentials of one block sit next to the MFMAs of another.
+    const int nfull = min(nkt, (causal ? q0 : N) / C::KT);
+    for (; t < nfull; ++t) {
+      publish(t);
+      issue_upto(t + C::NSTAGE - 1);
+      const f16* tile = stage(t);
+      const f16* k0row = tile + l32 * C::CW;
+      const f16* k1row = k0row + 32 * C::CW;
+      f32x16 s0 = {}, s1 = {};
+#pragma unroll
+      for (int c = 0; c < C::NCH; ++c)
+        s0 = mfma16(*reinterpret_cast<const f16x8*>(k0row + chunk_off<M>(c) + 8 * h32), qf[c], s0);
+      s0 = mfma8(*reinterpret_cast<const f16x4*>(k0row + M + 4 * h32), qaug, s0);
+#pragma unroll
+      for (int c = 0; c < C::NCH; ++c)
+        s1 = mfma16(*reinterpret_cast<const f16x8*>(k1row + chunk_off<M>(c) + 8 * h32), qf[c], s1);
+      s1 = mfma8(*reinterpret_cast<const f16x4*>(k1row + M + 4 * h32), qaug, s1);
+      f16x8 a0, a1, b0, b1;
+      expo(s0, a0, a1);
+      pv(tile, 0, a0, a1);
+      expo(s1, b0, b1);
+      pv(tile, 1, b0, b1);
+    }
+  }
+  if (!MAXPASS && C::PIPE) {
+    // ---- software-pipelined main loop over the tiles [0, nfull), whose keys
+    // are unmasked for every wave. Block j (32 keys; tile j / 2) passes through
+    // S(j) score MFMAs, E(j) exponentials and PV(j) value MFMAs in three
+    // successive steps; step j issues S(j + 1), E(j) and PV(j - 1), which are
+    // independent, so the matrix pipe and the VALU overlap inside a wave.
+    // Barrier B_k sits between steps 2k and 2k + 1: it publishes tile k + 1
+    // (needed by S(2k + 2)) and then refills the stage of tile k - 1, whose
+    // last reader, PV(2k - 1), ran in step 2k.
+    const int nfull = min(nkt, (causal ? q0 : N) / C::KT);
+    if (nfull > 0) {
+      f32x16 s_cur;
+      f16x8 pp0 = {}, pp1 = {};
+      auto kfrags = [&](const f16* tile, int kb, f16x8 (&kf)[C::NCH], f16x4& kx) {
+        const f16* krow = tile + (32 * kb + l32) * C::CW;
+#pragma unroll
+        for (int c = 0; c < C::NCH; ++c) kf[c] = *reinterpret_cast<const f16x8*>(krow + chunk_off<M>(c) + 8 * h32);
+        kx = *reinterpret_cast<const f16x4*>(krow + M + 4 * h32);
+      };
+      auto vfrags = [&](const f16* tile, int kb, f16x8 (&vf)[4][DV / 32]) {
+#pragma unroll
+        for (int part = 0; part < 4; ++part)
+#pragma unroll
+          for (int dvb = 0; dvb < DV / 32; ++dvb) {
+            const int j = (part >= 2 ? DV / 32 : 0) + dvb;
+            vf[part][dvb] = *reinterpret_cast<const f16x8*>(tile + vofs[kb ^ (j & 1)][part & 1] + 32 * C::KT * j);
+          }
+      };
+      auto score = [&](const f16x8 (&kf)[C::NCH], const f16x4& kx) {
+        f32x16 sc = {};
+#pragma unroll
+        for (int c = 0; c < C::NCH; ++c) sc = mfma16(kf[c], qf[c], sc);
+        return mfma8(kx, qaug, sc);
+      };
+      // one step: S of (tS, kbS) if do_s; E of s_cur; PV of (tV, kbV) with the
+      // previous P if do_pv
+      auto step = [&](bool do_s, const f16* tS, int kbS, bool do_pv, const f16* tV, int kbV) {
+        f16x8 kf[C::NCH];
+        f16x4 kx;
+        f16x8 vf[4][DV / 32];
+        if (do_s) kfrags(tS, kbS, kf, kx);
+        if (do_pv) vfrags(tV, kbV, vf);
+        __builtin_amdgcn_sched_barrier(0);  // all fragment reads in flight before the math
+        f32x16 s_nxt;
+        if (do_s) s_nxt = score(kf, kx);
+        f16x8 c0, c1;
+        expo(s_cur, c0, c1);
+        if (do_pv) {
+#pragma unroll
+          for (int part = 0; part < 4; ++part)
+#pragma unroll
+            for (int dvb = 0; dvb < DV / 32; ++dvb)
+              o[dvb] = mfma16(vf[part][dvb], (part & 1) ? pp1 : pp0, o[dvb]);
+        }
+        if (do_s) s_cur = s_nxt;
+        pp0 = c0;
+        pp1 = c1;
+      };
+
+      publish(0);  // B_-1: tile 0
+      {
+        f16x8 kf[C::NCH];
+        f16x4 kx;
+        kfrags(stage(0), 0, kf, kx);
+        s_cur = score(kf, kx);
+      }
+      step(true, stage(0), 1, false, nullptr, 0);  // step 0
+      for (int k = 0; k + 1 < nfull; ++k) {
+        publish(k + 1);  // B_k
+        issue_upto(k + 2);
+        step(true, stage(k + 1), 0, true, stage(k), 0);  // step 2k + 1
+        step(true, stage(k + 1), 1, true, stage(k), 1);  // step 2k + 2
+      }
+      const int L = nfull - 1;
+      step(false, nullptr, 0, true, stage(L), 0);  // step 2L + 1
+      pv(stage(L), 1, pp0, pp1);                   // PV(2L + 1)
+      t = nfull;
+    }
+  }
+  // ---- remaining tiles (masked ones; all of them in the exact-max pass)
+  for (; t < nkt; ++t) {
+    publish(t);
+    issue_upto(t + C::NSTAGE - 1);
+    compute(stage(t), t * C::KT);
   }
 }
 
 template <int M, int DV>
-__global__ __launch_bounds__(256) void attn_fwd_kernel(const f16* __restrict__ qa, const f16* __restrict__ ka,
-                                                       const f16* __restrict__ vt, const float4* __restrict__ tstat,
-                                                       f16* __restrict__ out, float* __restrict__ lse, int N, int NP,
-                                                       int H, int D, int BH, int causal) {
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2 * FwdCfg<M, DV>::WG_PER_CU)))
+void attn_fwd_kernel(const f16* __restrict__ qa, const f16* __restrict__ ka, const f16* __restrict__ vt,
+                     const float4* __restrict__ tstat, f16* __restrict__ out, float* __restrict__ lse, int N, int NP,
+                     int H, int D, int BH, int causal) {
   using C = FwdCfg<M, DV>;
-  __shared__ __align__(16) f16 sK[2][C::KT * C::KS];
-  __shared__ __align__(16) f16 sV[2][2 * DV * C::VS];
+  __shared__ __align__(16) f16 smem[C::NSTAGE * C::STAGE];
   const int tid = threadIdx.x, lane = tid & 63, h32 = lane >> 5, l32 = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, scalar
   const int nqb = (N + C::QW - 1) / C::QW;
@@ -264,14 +399,15 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const f16* __restrict__ q
     // pass 1: exact row max of the base-2 exponent without the reference
     f16x4 qa0 = qaug;
     if (h32 == 0) { qa0[2] = (f16)0.f; qa0[3] = (f16)0.f; }
-    fwd_tile_loop<M, DV, true>(ka, vt, vbase, rowbase, NP, N, causal, 0, kend, qw0, q, sK, sV, qf, qa0, o, lsum, rmax);
+    fwd_pass<M, DV, true>(ka, vt, rowbase, vbase, N, NP, causal, kend, q0, qw0, q, smem, qf, qa0, o, lsum, rmax);
     rmax = fmaxf(rmax, __shfl_xor(rmax, 32));
     R = qvalid ? rmax : 0.f;
     f16 rh, rl;
     split_hi_lo(-R, rh, rl);
     if (h32 == 0) { qaug[2] = rh; qaug[3] = rl; }
+    __syncthreads();  // every wave is done with the stages before they are refilled
   }
-  fwd_tile_loop<M, DV, false>(ka, vt, vbase, rowbase, NP, N, causal, 0, kend, qw0, q, sK, sV, qf, qaug, o, lsum, rmax);
+  fwd_pass<M, DV, false>(ka, vt, rowbase, vbase, N, NP, causal, kend, q0, qw0, q, smem, qf, qaug, o, lsum, rmax);
 
   const float ltot = lsum + __shfl_xor(lsum, 32);
   if (qvalid) {
@@ -294,8 +430,8 @@ template <int M, int DV>
 static hipError_t launch_attn_fwd_t(const Dims& d, const ProjBuffers& p, f16* out, float* lse, hipStream_t s) {
   using C = FwdCfg<M, DV>;
   const dim3 grid(xcd_grid((d.N + C::QW - 1) / C::QW, d.B * d.H));
-  hipLaunchKernelGGL((attn_fwd_kernel<M, DV>), grid, dim3(256), 0, s, p.qa, p.ka, p.vt, p.tstat, out, lse, d.N, d.NP,
-                     d.H, d.D, d.B * d.H, d.causal);
+  hipLaunchKernelGGL((attn_fwd_kernel<M, DV>), grid, dim3(64 * C::WAVES), 0, s, p.qa, p.ka, p.vt, p.tstat, out, lse,
+                     d.N, d.NP, d.H, d.D, d.B * d.H, d.causal);
   return hipGetLastError();
 }
 
