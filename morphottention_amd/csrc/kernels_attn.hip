@@ -530,28 +530,30 @@ struct BwdPrefetch {
   f16x8 r[C::NPR];
   float2 st;  // qstat of query row tid (tid < QT)
 
+  // Rows past N read row N - 1 (finite data): every score of such a query is
+  // masked, so it contributes nothing. No guards or selects, so the loads stay
+  // in flight until the stores need them.
   __device__ __forceinline__ void load(const f16* __restrict__ qa, const f16* __restrict__ grad_out,
                                        const float2* __restrict__ qstat, int64_t rowbase, int64_t tokbase, int hoff,
                                        int N, int D, int qs, int tid) {
 #pragma unroll
     for (int i = 0; i < C::NPR; ++i) {
-      const int v = tid + 256 * i;
-      f16x8 x = {};
+      const int v = tid + 256 * i;  // the Q / dO split falls on wave boundaries
       if (v < C::QT * C::QDV) {
         const int rr = v / C::QDV, j = v % C::QDV;
         const int col = j < M / 8 ? 8 * j : 8 * j + 8;
-        if (qs + rr < N) x = *reinterpret_cast<const f16x8*>(qa + (rowbase + qs + rr) * C::CW + col);
+        r[i] = *reinterpret_cast<const f16x8*>(qa + (rowbase + min(qs + rr, N - 1)) * C::CW + col);
       } else if (v < C::NDV) {
         const int u = v - C::QT * C::QDV;
         const int rr = u / C::ODV, col = 8 * (u % C::ODV);
-        if (qs + rr < N) x = *reinterpret_cast<const f16x8*>(grad_out + (tokbase + qs + rr) * D + hoff + col);
+        r[i] = *reinterpret_cast<const f16x8*>(grad_out + (tokbase + min(qs + rr, N - 1)) * D + hoff + col);
       }
-      r[i] = x;
     }
-    st = make_float2(0.f, 0.f);
-    if (tid < C::QT && qs + tid < N) st = qstat[rowbase + qs + tid];
+    if (tid < C::QT) st = qstat[rowbase + min(qs + tid, N - 1)];
   }
 
+  // Rows are stored in swap23 order within each 32-row block, so the b128
+  // operand reads (lane l32 reads row l32) touch consecutive rows.
   __device__ __forceinline__ void store(f16* sQ, f16* sO, int tid) const {
 #pragma unroll
     for (int i = 0; i < C::NPR; ++i) {
@@ -559,25 +561,39 @@ struct BwdPrefetch {
       if (v < C::QT * C::QDV) {
         const int rr = v / C::QDV, j = v % C::QDV;
         const int col = j < M / 8 ? 8 * j : 8 * j + 8;
-        *reinterpret_cast<f16x8*>(sQ + rr * C::QS + col) = r[i];
+        *reinterpret_cast<f16x8*>(sQ + lds_row(rr) * C::QS + col) = r[i];
       } else if (v < C::NDV) {
         const int u = v - C::QT * C::QDV;
         const int rr = u / C::ODV, col = 8 * (u % C::ODV);
-        *reinterpret_cast<f16x8*>(sO + rr * C::OS + col) = r[i];
+        *reinterpret_cast<f16x8*>(sO + lds_row(rr) * C::OS + col) = r[i];
       }
     }
     if (tid < C::QT) {
-      // affine blocks (rows past N get st = 0; every score they touch is masked)
       const f16 one = (f16)1.f;
       f16 lh, ll, dh, dl;
       split_hi_lo(st.x, lh, ll);
       split_hi_lo(st.y, dh, dl);
       const f16 zero = (f16)0.f;
-      *reinterpret_cast<f16x8*>(sQ + tid * C::QS + M) = f16x8{one, one, lh, ll, zero, zero, zero, zero};
-      *reinterpret_cast<f16x8*>(sO + tid * C::OS + DV) = f16x8{dh, dl, zero, zero, zero, zero, zero, zero};
+      *reinterpret_cast<f16x8*>(sQ + lds_row(tid) * C::QS + M) = f16x8{one, one, lh, ll, zero, zero, zero, zero};
+      *reinterpret_cast<f16x8*>(sO + lds_row(tid) * C::OS + DV) = f16x8{dh, dl, zero, zero, zero, zero, zero, zero};
     }
   }
+  __device__ __forceinline__ static int lds_row(int rr) { return (rr & ~31) | swap23(rr & 31); }
 };
+
+// MFMA 32x32x16 operand from a row-major LDS tile whose rows (the contraction
+// index) are stored in swap23 order within each 32-row block: value(mn, k) =
+// logical row k0 + k, column mn0 + mn. Each of the two transposed reads still
+// covers 4 consecutive stored rows.
+__device__ __forceinline__ f16x8 frag_kmajor_swz(const f16* tile, int stride, int k0, int mn0, int lane) {
+  const int g = lane >> 4;
+  const int row = k0 + 8 * (g >> 1) + ((lane & 15) >> 2);
+  const int col = mn0 + 16 * (g & 1) + 4 * (lane & 3);
+  const int rlo = (row & ~31) | swap23(row & 31), rhi = ((row + 4) & ~31) | swap23((row + 4) & 31);
+  f16x4 lo = lds_read_tr4(tile + rlo * stride + col);
+  f16x4 hi = lds_read_tr4(tile + rhi * stride + col);
+  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
 
 template <int M, int DV>
 __global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ qa, const f16* __restrict__ ka,
@@ -673,28 +689,31 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ q
       f16x8 ds16[2] = {f16x8{}, f16x8{}};
       if (!((causal && kw0 > q0 + 31) || kw0 >= N || q0 >= N)) {  // wave-uniform: something unmasked
         // S = Q~ K~^T (rows: queries in swap23 order; lane: key)
-        const f16* qrow = tQ + (32 * sb + swap23(l32)) * C::QS;
+        const f16* qrow = tQ + (32 * sb + l32) * C::QS;
         f32x16 s = {};
 #pragma unroll
         for (int c = 0; c < C::NCH; ++c)
           s = mfma16(*reinterpret_cast<const f16x8*>(qrow + chunk_off<M>(c) + 8 * h32), kf[c], s);
         s = mfma8(*reinterpret_cast<const f16x4*>(qrow + M + 4 * h32), kaug, s);
         // dP - delta = dO~ V~^T
-        const f16* orow = tO + (32 * sb + swap23(l32)) * C::OS;
+        const f16* orow = tO + (32 * sb + l32) * C::OS;
         f32x16 dp = {};
 #pragma unroll
         for (int c = 0; c < DV / 16; ++c)
           dp = mfma16(*reinterpret_cast<const f16x8*>(orow + 16 * c + 8 * h32), vf[c], dp);
         dp = mfma8(*reinterpret_cast<const f16x4*>(orow + DV + 4 * h32), vaug, dp);
         const bool need_mask = (q0 + 32 > N) || (kw0 + 31 >= N) || (causal && kw0 + 31 > q0);
+        if (need_mask) {  // wave-uniform; masked scores become -inf (P = 0)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int qq = q0 + swap23(acc_row(r, lane));
+            if (qq >= N || !kvalid || (causal && key > qq)) s[r] = kNegInf;
+          }
+        }
         f16x8 p16[2];
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          float pr = fast_exp2(s[r]);
-          if (need_mask) {
-            const int qq = q0 + swap23(acc_row(r, lane));
-            if (qq >= N || !kvalid || (causal && key > qq)) pr = 0.f;
-          }
+          const float pr = fast_exp2(s[r]);
           p16[r >> 3][r & 7] = (f16)pr;
           ds16[r >> 3][r & 7] = (f16)(pr * dp[r]);
         }
@@ -703,10 +722,10 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ q
         for (int c = 0; c < 2; ++c) {
 #pragma unroll
           for (int dvb = 0; dvb < DV / 32; ++dvb)
-            dva[dvb] = mfma16(frag_kmajor(tO, C::OS, 32 * sb + 16 * c, 32 * dvb, lane), p16[c], dva[dvb]);
+            dva[dvb] = mfma16(frag_kmajor_swz(tO, C::OS, 32 * sb + 16 * c, 32 * dvb, lane), p16[c], dva[dvb]);
 #pragma unroll
           for (int mb = 0; mb < C::MB; ++mb)
-            dka[mb] = mfma16(frag_kmajor(tQ, C::QS, 32 * sb + 16 * c, 32 * mb, lane), ds16[c], dka[mb]);
+            dka[mb] = mfma16(frag_kmajor_swz(tQ, C::QS, 32 * sb + 16 * c, 32 * mb, lane), ds16[c], dka[mb]);
         }
       }
       // dS^T row of this key (zeros where nothing was computed)
