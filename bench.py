@@ -76,6 +76,31 @@ def make_inputs(cfg, device):
     return x, params, dout
 
 
+def load_traffic(kernel, config):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary
+    (profiles/hbm_traffic_<config>.json: FETCH_SIZE and WRITE_SIZE per dispatch,
+    each scaled by the same counter's reading for a plain copy of known size).
+    Offline numbers: PMC passes cannot run inside this timed process."""
+    path = os.path.join(ROOT, "profiles", f"hbm_traffic_{config}.json")
+    try:
+        with open(path) as f:
+            data = json.load(f)
+        return data["kernels"][kernel]["hbm_bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def calib_copy(device, nbytes=256 << 20):
+    """One plain device-to-device copy of a known size (PMC calibration)."""
+    src = torch.ones(nbytes, dtype=torch.uint8, device=device)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"calibration copy: {nbytes} bytes read, {nbytes} bytes written")
+    del src, dst
+
+
 def cpu_baseline(cfg, budget_s=20.0):
     """Time the eager fp32 oracle (oracle/morpho_oracle.py) on the host CPU on a
     bounded sample of the workload: one batch row (all heads, full sequence)."""
@@ -112,6 +137,7 @@ def main():
     ap.add_argument("--config", default="C3", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--timing-steps", type=int, default=5, help="steps re-run with per-kernel HIP events")
+    ap.add_argument("--calib-copy", action="store_true", help="run one 256 MiB copy first (PMC calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; the path is sharded over "
@@ -126,6 +152,8 @@ def main():
     cfg = CONFIGS[args.config]
     B, N, D, H, m, scale, causal, seed, xm = cfg
     dev = torch.device("cuda:0")
+    if args.calib_copy:
+        calib_copy(dev)
     x, params, dout = make_inputs(cfg, dev)
     leaves = [x, *params]
 
@@ -209,7 +237,7 @@ def main():
         "step_roofline_frac": round((f_fwd + f_bwd) / 2.5e15 / (ms_step * 1e-3), 4),
         "roofline": {"bound": "mfma", "kernel": dominant, "achieved": round(achieved, 2),
                      "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
-                     "traffic": None},
+                     "traffic": load_traffic(dominant, args.config)},
         "kernels": kernels,
     }
     if not args.no_cpu_baseline:

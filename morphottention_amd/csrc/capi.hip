@@ -111,7 +111,7 @@ size_t bwd_bytes(const Dims& d) {
   const size_t bhn = (size_t)d.B * d.H * d.N;
   const size_t nblk = (size_t)((d.T + kGateTokensPerBlock - 1) / kGateTokensPerBlock);
   size_t s = 0;
-  s += align_up(bhn * 8);                              // qstat
+  s += align_up(bhn * 32);                             // aug
   s += align_up(bhn * d.M * 4);                        // dq
   s += align_up(bhn * d.M * 4);                        // dk
   s += align_up(bhn * 4);                              // dcb
@@ -126,7 +126,7 @@ BwdBuffers carve_bwd(void* base, const Dims& d) {
   const size_t nblk = (size_t)((d.T + kGateTokensPerBlock - 1) / kGateTokensPerBlock);
   char* p = static_cast<char*>(base);
   BwdBuffers g;
-  g.qstat = reinterpret_cast<float2*>(p); p += align_up(bhn * 8);
+  g.aug = reinterpret_cast<_Float16*>(p); p += align_up(bhn * 32);
   g.dq = reinterpret_cast<float*>(p); p += align_up(bhn * d.M * 4);
   g.dk = reinterpret_cast<float*>(p); p += align_up(bhn * d.M * 4);
   g.dcb = reinterpret_cast<float*>(p); p += align_up(bhn * 4);

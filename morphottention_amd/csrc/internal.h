@@ -39,7 +39,7 @@ struct ProjBuffers {
 };
 
 struct BwdBuffers {
-  float2* qstat;   // [B*H, N] {-(lse - b), -delta}
+  _Float16* aug;   // [B*H, N, 16] per query: {1, 1, -(lse - b) hi, lo, 0 x4} then {-delta hi, lo, 0 x6}
   float* dq;       // [B*H, N, M] sum_j dS_ij phi_j (query side), fp32 atomics
   float* dk;       // [B*H, N, M] sum_i dS_ij phi_i (key side)
   float* dcb;      // [B*H, N]    sum_i dS_ij

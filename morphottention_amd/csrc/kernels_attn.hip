@@ -454,13 +454,13 @@ hipError_t launch_attn_fwd(const Dims& d, const ProjBuffers& p, f16* out, float*
 }
 
 // ============================================================ backward prep
-// qstat = {-(lse - b), -delta} with delta_i = dO_i . O_i (fp32), one thread per
+// Backward affine blocks from lse and delta_i = dO_i . O_i (fp32), one thread per
 // (token, head), heads fastest so a wave reads whole contiguous rows; the same
 // grid zeroes the dq accumulator with contiguous stores.
 template <int M, int DV>
 __global__ __launch_bounds__(256) void bwd_prep_kernel(const f16* __restrict__ grad_out, const f16* __restrict__ out,
                                                        const float* __restrict__ lse,
-                                                       const float4* __restrict__ tstat, float2* __restrict__ qstat,
+                                                       const float4* __restrict__ tstat, f16* __restrict__ aug,
                                                        float* __restrict__ dq, int64_t T, int N, int H, int D) {
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (idx < T * H) {
@@ -478,7 +478,14 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(const f16* __restrict__ g
 #pragma unroll
       for (int e = 0; e < 8; ++e) delta += (float)a[e] * (float)o[e];
     }
-    qstat[bhn] = make_float2(-(lse[bhn] - tstat[bhn].x), -delta);
+    // affine blocks of the backward code rows: query side {1, 1, -(lse - b)},
+    // dO side {-delta}, as fp16 hi/lo pairs
+    f16 lh, ll, dh, dl;
+    split_hi_lo(-(lse[bhn] - tstat[bhn].x), lh, ll);
+    split_hi_lo(-delta, dh, dl);
+    const f16 one = (f16)1.f, zero = (f16)0.f;
+    *reinterpret_cast<f16x8*>(aug + bhn * 16) = f16x8{one, one, lh, ll, zero, zero, zero, zero};
+    *reinterpret_cast<f16x8*>(aug + bhn * 16 + 8) = f16x8{dh, dl, zero, zero, zero, zero, zero, zero};
   }
   // zero dq: T * H * M floats, M / 4 float4 per (token, head)
   float4* z = reinterpret_cast<float4*>(dq);
@@ -491,7 +498,7 @@ static hipError_t launch_bwd_prep_t(const Dims& d, const ProjBuffers& p, const f
                                     const float* lse, const BwdBuffers& g, hipStream_t s) {
   const int64_t n = d.T * d.H;
   hipLaunchKernelGGL((bwd_prep_kernel<M, DV>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, grad_out, out, lse,
-                     p.tstat, g.qstat, g.dq, d.T, d.N, d.H, d.D);
+                     p.tstat, g.aug, g.dq, d.T, d.N, d.H, d.D);
   return hipGetLastError();
 }
 
@@ -506,79 +513,23 @@ struct BwdCfg {
   static constexpr int CW = 3 * M + 8;
   static constexpr int NCH = 3 * M / 16;
   static constexpr int MB = M / 32 + 1;         // 32-row blocks of dk^T (codes + the ones row at row M)
-  static constexpr int MQ = (M + 31) / 32;      // 32-column blocks of dq
   static constexpr int QT = M <= 32 ? 64 : 32;  // queries per step
   static constexpr int NSB = QT / 32;           // 32-query sub-blocks per step
-  // strides (halves): see FwdCfg; the query and dO tiles serve both b128 and
-  // transposed reads and are laid out for the b128 ones
-  static constexpr int QS = CW;                 // query tile stride
-  static constexpr int OS = DV + 8;             // dO tile stride: DV values + 8 aug
+  // Query tile [QT][CW] and dO tile [QT][DV + 8] (values, then the affine
+  // block), rows in swap23 order within each 32; row strides CW and DV + 8 are
+  // 8 (mod 16) halves, conflict-free for the b128 operand reads.
+  static constexpr int QS = CW;
+  static constexpr int OS = DV + 8;
   static constexpr int SS = QT + 16;            // dS^T tile stride (transposed reads only)
   static constexpr int PKS = M + 16;            // key phi tile stride (transposed reads only)
   static constexpr int KW = 128;                // keys per workgroup (4 waves x 32)
   static constexpr int DQT = (QT / 16) * (M / 16) / 4;  // 16x16 dq tiles per wave per step
-  // prefetch: data vectors of 8 halves per step (the affine blocks are built from qstat)
-  static constexpr int QDV = 3 * M / 8;         // code vectors per query row
-  static constexpr int ODV = DV / 8;            // dO vectors per query row
-  static constexpr int NDV = QT * (QDV + ODV);
-  static constexpr int NPR = (NDV + 255) / 256;
-};
-
-template <int M, int DV>
-struct BwdPrefetch {
-  using C = BwdCfg<M, DV>;
-  f16x8 r[C::NPR];
-  float2 st;  // qstat of query row tid (tid < QT)
-
-  // Rows past N read row N - 1 (finite data): every score of such a query is
-  // masked, so it contributes nothing. No guards or selects, so the loads stay
-  // in flight until the stores need them.
-  __device__ __forceinline__ void load(const f16* __restrict__ qa, const f16* __restrict__ grad_out,
-                                       const float2* __restrict__ qstat, int64_t rowbase, int64_t tokbase, int hoff,
-                                       int N, int D, int qs, int tid) {
-#pragma unroll
-    for (int i = 0; i < C::NPR; ++i) {
-      const int v = tid + 256 * i;  // the Q / dO split falls on wave boundaries
-      if (v < C::QT * C::QDV) {
-        const int rr = v / C::QDV, j = v % C::QDV;
-        const int col = j < M / 8 ? 8 * j : 8 * j + 8;
-        r[i] = *reinterpret_cast<const f16x8*>(qa + (rowbase + min(qs + rr, N - 1)) * C::CW + col);
-      } else if (v < C::NDV) {
-        const int u = v - C::QT * C::QDV;
-        const int rr = u / C::ODV, col = 8 * (u % C::ODV);
-        r[i] = *reinterpret_cast<const f16x8*>(grad_out + (tokbase + min(qs + rr, N - 1)) * D + hoff + col);
-      }
-    }
-    if (tid < C::QT) st = qstat[rowbase + min(qs + tid, N - 1)];
-  }
-
-  // Rows are stored in swap23 order within each 32-row block, so the b128
-  // operand reads (lane l32 reads row l32) touch consecutive rows.
-  __device__ __forceinline__ void store(f16* sQ, f16* sO, int tid) const {
-#pragma unroll
-    for (int i = 0; i < C::NPR; ++i) {
-      const int v = tid + 256 * i;
-      if (v < C::QT * C::QDV) {
-        const int rr = v / C::QDV, j = v % C::QDV;
-        const int col = j < M / 8 ? 8 * j : 8 * j + 8;
-        *reinterpret_cast<f16x8*>(sQ + lds_row(rr) * C::QS + col) = r[i];
-      } else if (v < C::NDV) {
-        const int u = v - C::QT * C::QDV;
-        const int rr = u / C::ODV, col = 8 * (u % C::ODV);
-        *reinterpret_cast<f16x8*>(sO + lds_row(rr) * C::OS + col) = r[i];
-      }
-    }
-    if (tid < C::QT) {
-      const f16 one = (f16)1.f;
-      f16 lh, ll, dh, dl;
-      split_hi_lo(st.x, lh, ll);
-      split_hi_lo(st.y, dh, dl);
-      const f16 zero = (f16)0.f;
-      *reinterpret_cast<f16x8*>(sQ + lds_row(tid) * C::QS + M) = f16x8{one, one, lh, ll, zero, zero, zero, zero};
-      *reinterpret_cast<f16x8*>(sO + lds_row(tid) * C::OS + DV) = f16x8{dh, dl, zero, zero, zero, zero, zero, zero};
-    }
-  }
-  __device__ __forceinline__ static int lds_row(int rr) { return (rr & ~31) | swap23(rr & 31); }
+  // a stage = both tiles, filled by 1 KiB DMA chunks spread over the 4 waves
+  static constexpr int QCH = (QT * CW + 511) / 512;
+  static constexpr int OCH = (QT * OS + 511) / 512;
+  static constexpr int NPW = (QCH + OCH + 3) / 4;
+  static constexpr int OOFF = QCH * 512;        // dO tile offset in a stage (halves)
+  static constexpr int STAGE = 4 * NPW * 512;   // halves, incl. padding chunks
 };
 
 // MFMA 32x32x16 operand from a row-major LDS tile whose rows (the contraction
@@ -595,16 +546,32 @@ __device__ __forceinline__ f16x8 frag_kmajor_swz(const f16* tile, int stride, in
   return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
+// s_waitcnt: vector-memory count CNT and LDS count 0 (gfx9 encoding).
+template <int CNT>
+__device__ __forceinline__ void wait_vmcnt_lgkm0() {
+  static_assert(CNT >= 0 && CNT < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((CNT & 15) | (7 << 4) | (0 << 8) | ((CNT >> 4) << 14));
+}
+
+// Key-side (KV-outer) backward. A workgroup owns 128 keys (32 per wave, kept in
+// registers: codes, V_hi, dk / dV accumulators) and streams the query steps
+// of QT queries through two LDS stages filled by DMA. Step s:
+//   wait for its tiles, barrier (also publishes dS^T of step s - 1), DMA the
+//   tiles of step s + 1, read the dq fragments of step s - 1, compute step s
+//   (S, dP, P, dS, dV += dO^T P, dk^T += phi^T dS, dS^T -> LDS), then finish
+//   dq of step s - 1 (MFMA over the workgroup's keys, fp32 atomics).
+// Every wave issues exactly 4 DQT atomics per step (masked lanes add 0.0 to a
+// valid address), so the tile wait can leave the latest step's atomics in
+// flight: vector-memory operations complete in issue order.
 template <int M, int DV>
 __global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ qa, const f16* __restrict__ ka,
-                                                       const f16* __restrict__ vt, const float2* __restrict__ qstat,
+                                                       const f16* __restrict__ vt, const f16* __restrict__ aug,
                                                        const f16* __restrict__ grad_out, float* __restrict__ dq,
                                                        float* __restrict__ dk, float* __restrict__ dcb,
                                                        f16* __restrict__ dzv, int N, int NP, int H, int D, int HM, int BH,
                                                        int causal) {
   using C = BwdCfg<M, DV>;
-  __shared__ __align__(16) f16 sQ[2][C::QT * C::QS];
-  __shared__ __align__(16) f16 sO[2][C::QT * C::OS];
+  __shared__ __align__(16) f16 stg[2 * C::STAGE];
   __shared__ __align__(16) f16 sdS[2][C::KW * C::SS];  // dS^T of the whole workgroup: row = key
   __shared__ __align__(16) f16 sPk[C::KW * C::PKS];     // phi_hi of the workgroup's keys: row = key
 
@@ -659,30 +626,96 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ q
 
   const int qstart = causal ? k0 : 0;
   const int nsteps = qstart < N ? (N - qstart + C::QT - 1) / C::QT : 0;
-  // keys of this workgroup that exist: dq contracts over [0, kw_valid) only
-  const int nkey = min(C::KW, N - k0);
 
-  // Two register stages (see the forward): step s computes from LDS buffer
-  // s & 1 while the loads of steps s+1 and s+2 are in flight.
-  BwdPrefetch<M, DV> pf0, pf1;
-  auto pf_load = [&](BwdPrefetch<M, DV>& pf, int step) {
-    pf.load(qa, grad_out, qstat, rowbase, tokbase, h * DV, N, D, qstart + step * C::QT, tid);
+  // ---- DMA of the query and dO tiles of a step (rows clamped to N - 1: every
+  // score of a query past N is masked)
+  const unsigned sbase = (unsigned)(uintptr_t)(__attribute__((address_space(3))) f16*)stg;
+  auto issue = [&](int st) {
+    const unsigned dst = sbase + 2u * (unsigned)((st & 1) * C::STAGE);
+    const int qs = qstart + st * C::QT;
+#pragma unroll
+    for (int i = 0; i < C::NPW; ++i) {
+      const int c = w + 4 * i;  // wave-uniform chunk id
+      const f16* src;
+      if (c < C::QCH) {
+        const int p = 64 * c + lane;
+        const int r = p / (C::CW / 8), col = p % (C::CW / 8);
+        const int qrow = min(qs + ((r & ~31) | swap23(r & 31)), N - 1);
+        if (p >= C::QT * C::CW / 8)
+          src = qa + (rowbase + qs % N) * C::CW;  // padding piece: any in-bounds bytes
+        else if (col == M / 8)
+          src = aug + (rowbase + qrow) * 16;  // affine block of the backward
+        else
+          src = qa + (rowbase + qrow) * C::CW + 8 * col;
+      } else if (c < C::QCH + C::OCH) {
+        const int p = 64 * (c - C::QCH) + lane;
+        const int r = p / (C::OS / 8), col = p % (C::OS / 8);
+        const int qrow = min(qs + ((r & ~31) | swap23(r & 31)), N - 1);
+        if (p >= C::QT * C::OS / 8)
+          src = qa + (rowbase + qs % N) * C::CW;
+        else if (col == DV / 8)
+          src = aug + (rowbase + qrow) * 16 + 8;
+        else
+          src = grad_out + (tokbase + qrow) * D + h * DV + 8 * col;
+      } else {
+        src = qa + (rowbase + qs % N) * C::CW;
+      }
+      lds_dma16(src, dst + 1024u * (unsigned)c);
+    }
   };
-  if (nsteps > 0) {
-    pf_load(pf0, 0);
-    pf0.store(sQ[0], sO[0], tid);
-  }
-  if (nsteps > 1) pf_load(pf1, 1);
-  if (nsteps > 2) pf_load(pf0, 2);
-  __syncthreads();
 
+  // ---- dq[q][code] += sum_key dS[q][key] phi[key][code]: 16 x 16 output
+  // tiles split over the waves, contraction over all 128 keys of the workgroup
+  // (rows past N are zero in both operands)
+  f16x8 dqa[C::DQT][C::KW / 32], dqb[C::DQT][C::KW / 32];
+  auto dq_load = [&](int st) {
+#pragma unroll
+    for (int t = 0; t < C::DQT; ++t) {
+      const int tile = w + 4 * t;
+      const int qt = tile % (C::QT / 16), ct = tile / (C::QT / 16);
+#pragma unroll
+      for (int kc = 0; kc < C::KW / 32; ++kc) {
+        dqa[t][kc] = frag16_kmajor(sdS[st & 1], C::SS, 32 * kc, 16 * qt, lane);
+        dqb[t][kc] = frag16_kmajor(sPk, C::PKS, 32 * kc, 16 * ct, lane);
+      }
+    }
+  };
+  auto dq_finish = [&](int st) {
+    const int qs = qstart + st * C::QT;
+#pragma unroll
+    for (int t = 0; t < C::DQT; ++t) {
+      const int tile = w + 4 * t;
+      const int qt = tile % (C::QT / 16), ct = tile / (C::QT / 16);
+      f32x4 acc = {};
+#pragma unroll
+      for (int kc = 0; kc < C::KW / 32; ++kc) acc = mfma16x16(dqa[t][kc], dqb[t][kc], acc);
+      const int code = 16 * ct + (lane & 15);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int qq = qs + 16 * qt + 4 * (lane >> 4) + r;
+        const bool ok = qq < N;
+        // always issued (a fixed count per step); rows past N add 0 to row N - 1
+        unsafeAtomicAdd(dq + (rowbase + (ok ? qq : N - 1)) * M + code, ok ? acc[r] : 0.f);
+      }
+    }
+  };
+
+  if (nsteps > 0) issue(0);
   for (int step = 0; step < nsteps; ++step) {
-    const int buf = step & 1;
+    // this step's tiles have landed (the atomics of step - 2, issued after
+    // them, may still be in flight) and this wave's dS^T writes are done
+    if (step >= 2)
+      wait_vmcnt_lgkm0<4 * C::DQT>();
+    else
+      wait_vmcnt_lgkm0<0>();
+    __builtin_amdgcn_s_barrier();
+    if (step + 1 < nsteps) issue(step + 1);  // its stage last served step - 1
+    if (step >= 1) dq_load(step - 1);
+
     const int qs = qstart + step * C::QT;
-    const bool more = step + 1 < nsteps;
-    const f16* tQ = sQ[buf];
-    const f16* tO = sO[buf];
-    f16* tS = sdS[buf] + (32 * w + l32) * C::SS;  // this lane's key row
+    const f16* tQ = stg + (step & 1) * C::STAGE;
+    const f16* tO = tQ + C::OOFF;
+    f16* tS = sdS[step & 1] + (32 * w + l32) * C::SS;  // this lane's key row
 #pragma unroll
     for (int sb = 0; sb < C::NSB; ++sb) {
       const int q0 = qs + 32 * sb;
@@ -732,34 +765,13 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ q
 #pragma unroll
       for (int c = 0; c < 2; ++c) *reinterpret_cast<f16x8*>(tS + 32 * sb + 16 * c + 8 * h32) = ds16[c];
     }
-    if (more) {
-      if (buf == 0) pf1.store(sQ[1], sO[1], tid);
-      else pf0.store(sQ[0], sO[0], tid);
-    }
-    __syncthreads();  // dS^T of all four waves complete; next tiles visible
-    if (step + 3 < nsteps) {
-      if (buf == 0) pf_load(pf1, step + 3);
-      else pf_load(pf0, step + 3);
-    }
-    // dq[q][code] += sum_key dS[q][key] phi[key][code]: 16 x 16 output tiles
-    // split over the waves, contraction over the workgroup's keys.
-#pragma unroll
-    for (int t = 0; t < C::DQT; ++t) {
-      const int tile = w + 4 * t;
-      const int qt = tile % (C::QT / 16), ct = tile / (C::QT / 16);
-      const int qrow0 = qs + 16 * qt;
-      if (qrow0 >= N) continue;  // uniform
-      f32x4 acc = {};
-      for (int kc = 0; kc < nkey; kc += 32)
-        acc = mfma16x16(frag16_kmajor(sdS[buf], C::SS, kc, 16 * qt, lane),
-                        frag16_kmajor(sPk, C::PKS, kc, 16 * ct, lane), acc);
-      const int code = 16 * ct + (lane & 15);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int qq = qrow0 + 4 * (lane >> 4) + r;
-        if (qq < N && acc[r] != 0.f) unsafeAtomicAdd(dq + (rowbase + qq) * M + code, acc[r]);
-      }
-    }
+    if (step >= 1) dq_finish(step - 1);
+  }
+  if (nsteps > 0) {
+    wait_vmcnt_lgkm0<4 * C::DQT>();
+    __builtin_amdgcn_s_barrier();  // dS^T of the last step from every wave
+    dq_load(nsteps - 1);
+    dq_finish(nsteps - 1);
   }
 
   // ---- epilogue: dk, dcb (fp32, per key) and dV (fp16 into the dZ|dV buffer)
@@ -791,7 +803,7 @@ static hipError_t launch_attn_bwd_t(const Dims& d, const ProjBuffers& p, const f
                                     hipStream_t s) {
   using C = BwdCfg<M, DV>;
   const dim3 grid(xcd_grid((d.N + C::KW - 1) / C::KW, d.B * d.H));
-  hipLaunchKernelGGL((attn_bwd_kernel<M, DV>), grid, dim3(256), 0, s, p.qa, p.ka, p.vt, g.qstat, grad_out, g.dq, g.dk,
+  hipLaunchKernelGGL((attn_bwd_kernel<M, DV>), grid, dim3(256), 0, s, p.qa, p.ka, p.vt, g.aug, grad_out, g.dq, g.dk,
                      g.dcb, g.dzv, d.N, d.NP, d.H, d.D, d.HM, d.B * d.H, d.causal);
   return hipGetLastError();
 }
