@@ -57,6 +57,15 @@ __device__ __forceinline__ bool xcd_map(int nblk, int BH, int& bh, int& blk) {
   blk = slot % nblk;
   return bh < BH;
 }
+// Same XCD per head, but block-major within an XCD: for causal problems block
+// 0 is the longest, so all heads' long blocks start first (longest processing
+// time first), and the short ones fill in at the end.
+__device__ __forceinline__ bool xcd_map_lpt(int nblk, int BH, int& bh, int& blk) {
+  const int i = blockIdx.x, xcd = i & 7, slot = i >> 3, hx = (BH + 7) / 8;
+  bh = 8 * (slot % hx) + xcd;
+  blk = slot / hx;
+  return bh < BH;
+}
 __host__ inline unsigned xcd_grid(int nblk, int BH) { return 8u * (unsigned)((BH + 7) / 8) * (unsigned)nblk; }
 
 // ============================================================ forward
@@ -89,8 +98,11 @@ struct FwdCfg {
   static constexpr int CW = 3 * M + 8;    // code row width
   static constexpr int NCH = 3 * M / 16;  // 16-wide code chunks
   static constexpr int KT = 64;           // keys per tile
-  static constexpr int WAVES = 8;
-  static constexpr int QW = 32 * WAVES;   // queries per workgroup
+  // Each wave owns QB blocks of 32 queries: every K / V fragment read from LDS
+  // then feeds QB MFMAs. Two blocks where the registers allow it.
+  static constexpr int QB = (M <= 32 && DV <= 64) ? 2 : 1;
+  static constexpr int WAVES = 8 / QB;
+  static constexpr int QW = 32 * QB * WAVES;  // 256 queries per workgroup
   // A stage holds one key tile [KT][CW] (rows in swap23 order within each 32,
   // unpadded: CW = 8 (mod 16) halves keeps b128 reads conflict-free) and one
   // V^T tile [2 DV][KT] (V_hi^T rows, then V_lo^T rows, chunk-swizzled), both
@@ -101,15 +113,12 @@ struct FwdCfg {
   static constexpr int NPW_K = (KCH + WAVES - 1) / WAVES;      // key-only tiles (exact-max pass)
   static constexpr int VOFF = KCH * 512;  // V^T offset in a stage (halves)
   static constexpr int STAGE = WAVES * NPW * 512;              // halves, incl. padding chunks
-  // Two workgroups per CU (4 waves per SIMD, <= 128 VGPRs) when the code is
-  // narrow and two stages fit in half the 160 KiB LDS (less 1 KiB for the
-  // rest); otherwise one workgroup with the registers and LDS to itself.
-  // PIPE: software-pipelined main loop (steps S(j+1) | E(j) | PV(j-1)), which
-  // needs the registers of two waves per SIMD; otherwise tile-at-a-time code
-  // with four waves per SIMD. The latter measures faster on MI355X.
-  static constexpr bool PIPE = false;
-  static constexpr bool TWO = !PIPE && M == 16 && 2 * STAGE * 2 <= 79 * 1024;
+  // Two workgroups per CU when two stages of each fit in half the 160 KiB LDS
+  // (less 1 KiB for the rest) and, with one query block per wave, the code is
+  // narrow enough for 128 VGPRs; otherwise one workgroup per CU.
+  static constexpr bool TWO = 2 * STAGE * 2 <= 79 * 1024 && (QB == 2 || M == 16);
   static constexpr int WG_PER_CU = TWO ? 2 : 1;
+  static constexpr int WAVES_PER_EU = WG_PER_CU * WAVES / 4;
   static constexpr int LDS_BUDGET = (TWO ? 79 : 158) * 1024;
   static constexpr int NSTAGE = 3 * STAGE * 2 <= LDS_BUDGET ? 3 : 2;
 };
@@ -123,14 +132,16 @@ struct FwdCfg {
 template <int M, int DV, bool MAXPASS>
 __device__ __forceinline__ void fwd_pass(const f16* __restrict__ ka, const f16* __restrict__ vt, int64_t rowbase,
                                          int64_t vbase, int N, int NP, int causal, int kend, int q0, int qw0,
-                                         int q, f16* smem, const f16x8 (&qf)[FwdCfg<M, DV>::NCH], const f16x4& qaug,
-                                         f32x16 (&o)[DV / 32], float& lsum, float& rmax) {
+                                         f16* smem, const f16x8 (&qf)[FwdCfg<M, DV>::QB][FwdCfg<M, DV>::NCH],
+                                         const f16x4 (&qaug)[FwdCfg<M, DV>::QB],
+                                         f32x16 (&o)[FwdCfg<M, DV>::QB][DV / 32], float (&lsum)[FwdCfg<M, DV>::QB],
+                                         float (&rmax)[FwdCfg<M, DV>::QB]) {
   using C = FwdCfg<M, DV>;
+  constexpr int QB = C::QB;
   constexpr int NPWX = MAXPASS ? C::NPW_K : C::NPW;
   const int tid = threadIdx.x, lane = tid & 63, h32 = lane >> 5, l32 = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nkt = (kend + C::KT - 1) / C::KT;
-  const int wave_kend = causal ? min(N, qw0 + 32) : N;
 
   // LDS byte address of the stage area (the DMA takes raw LDS addresses)
   const unsigned sbase = (unsigned)(uintptr_t)(__attribute__((address_space(3))) f16*)smem;
@@ -171,59 +182,79 @@ __device__ __forceinline__ void fwd_pass(const f16* __restrict__ ka, const f16* 
       for (int p = 0; p < 2; ++p)
         vofs[x][p] = C::VOFF + l32 * C::KT + 8 * (4 * (x ^ (z >> 2)) + 2 * (p ^ ((z >> 1) & 1)) + (h32 ^ (z & 1)));
   }
-  // O^T += V^T P for the 32 keys of block kb: A rows are value columns (hi,
-  // then lo), k = key. The DV / 32 accumulators are independent and are
-  // interleaved, so consecutive MFMAs never wait on each other.
-  auto pv = [&](const f16* tile, int kb, const f16x8& p0, const f16x8& p1) {
+  // V^T fragments of block kb: [part][dvb], part = (hi, k 0-15), (hi, k 16-31),
+  // (lo, k 0-15), (lo, k 16-31); A rows are value columns, k = key.
+  auto vfrags = [&](const f16* tile, int kb, f16x8 (&vf)[4][DV / 32]) {
 #pragma unroll
-    for (int part = 0; part < 4; ++part) {  // (hi, k 0-15), (hi, k 16-31), (lo, ...), (lo, ...)
+    for (int part = 0; part < 4; ++part)
 #pragma unroll
       for (int dvb = 0; dvb < DV / 32; ++dvb) {
         const int j = (part >= 2 ? DV / 32 : 0) + dvb;  // 32-row block of the V^T tile
-        const f16* src = tile + vofs[kb ^ (j & 1)][part & 1] + 32 * C::KT * j;
-        o[dvb] = mfma16(*reinterpret_cast<const f16x8*>(src), (part & 1) ? p1 : p0, o[dvb]);
+        vf[part][dvb] = *reinterpret_cast<const f16x8*>(tile + vofs[kb ^ (j & 1)][part & 1] + 32 * C::KT * j);
       }
-    }
   };
-  auto expo = [&](const f32x16& s, f16x8& p0, f16x8& p1) {
+  // O^T += V^T P; the DV / 32 accumulators are independent and interleaved
+  auto pv = [&](const f16x8 (&vf)[4][DV / 32], int qb, const f16x8& p0, const f16x8& p1) {
+#pragma unroll
+    for (int part = 0; part < 4; ++part)
+#pragma unroll
+      for (int dvb = 0; dvb < DV / 32; ++dvb)
+        o[qb][dvb] = mfma16(vf[part][dvb], (part & 1) ? p1 : p0, o[qb][dvb]);
+  };
+  auto kfrags = [&](const f16* tile, int kb, f16x8 (&kf)[C::NCH], f16x4& kx) {
+    const f16* krow = tile + (32 * kb + l32) * C::CW;
+#pragma unroll
+    for (int c = 0; c < C::NCH; ++c) kf[c] = *reinterpret_cast<const f16x8*>(krow + chunk_off<M>(c) + 8 * h32);
+    kx = *reinterpret_cast<const f16x4*>(krow + M + 4 * h32);
+  };
+  auto score = [&](const f16x8 (&kf)[C::NCH], const f16x4& kx, int qb) {
+    f32x16 sc = {};
+#pragma unroll
+    for (int c = 0; c < C::NCH; ++c) sc = mfma16(kf[c], qf[qb][c], sc);
+    return mfma8(kx, qaug[qb], sc);
+  };
+  auto expo = [&](const f32x16& sc, int qb, f16x8& p0, f16x8& p1) {
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
-      p0[r] = (f16)fast_exp2(s[r]);
-      p1[r] = (f16)fast_exp2(s[r + 8]);
+      p0[r] = (f16)fast_exp2(sc[r]);
+      p1[r] = (f16)fast_exp2(sc[r + 8]);
     }
-    lsum += sum8(p0) + sum8(p1);
+    lsum[qb] += sum8(p0) + sum8(p1);
   };
-
   auto stage = [&](int t) { return smem + (t % C::NSTAGE) * C::STAGE; };
 
-  // Any tile: per 32-key block, with masks where needed.
+  // Any tile: per 32-key block and query block, with masks where needed.
   auto compute = [&](const f16* tile, int k0) {
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       const int kbase = k0 + 32 * kb;
-      if (kbase >= wave_kend) continue;  // wave-uniform
-      const f16* krow = tile + (32 * kb + l32) * C::CW;
-      f32x16 s = {};
+      if (kbase >= N || (causal && kbase > qw0 + 32 * QB - 1)) continue;  // wave-uniform
+      f16x8 kf[C::NCH];
+      f16x4 kx;
+      kfrags(tile, kb, kf, kx);
+      f16x8 vf[4][DV / 32];
+      if (!MAXPASS) vfrags(tile, kb, vf);
 #pragma unroll
-      for (int c = 0; c < C::NCH; ++c)
-        s = mfma16(*reinterpret_cast<const f16x8*>(krow + chunk_off<M>(c) + 8 * h32), qf[c], s);
-      s = mfma8(*reinterpret_cast<const f16x4*>(krow + M + 4 * h32), qaug, s);
-      const bool need_mask = (kbase + 31 >= N) || (causal && kbase + 31 > qw0);
-      if (need_mask) {
+      for (int qb = 0; qb < QB; ++qb) {
+        const int qb0 = qw0 + 32 * qb;
+        if (causal && kbase > qb0 + 31) continue;  // wave-uniform
+        f32x16 sc = score(kf, kx, qb);
+        if ((kbase + 31 >= N) || (causal && kbase + 31 > qb0)) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = kbase + swap23(acc_row(r, lane));
-          if (key >= N || (causal && key > q)) s[r] = kNegInf;
+          for (int r = 0; r < 16; ++r) {
+            const int key = kbase + swap23(acc_row(r, lane));
+            if (key >= N || (causal && key > qb0 + l32)) sc[r] = kNegInf;
+          }
         }
-      }
-      if (MAXPASS) {
+        if (MAXPASS) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) rmax = fmaxf(rmax, s[r]);
-        continue;
+          for (int r = 0; r < 16; ++r) rmax[qb] = fmaxf(rmax[qb], sc[r]);
+          continue;
+        }
+        f16x8 p0, p1;
+        expo(sc, qb, p0, p1);
+        pv(vf, qb, p0, p1);
       }
-      f16x8 p0, p1;
-      expo(s, p0, p1);
-      pv(tile, kb, p0, p1);
     }
   };
 
@@ -242,110 +273,30 @@ __device__ __forceinline__ void fwd_pass(const f16* __restrict__ ka, const f16* 
 
   int t = 0;
   issue_upto(1);
-  if (!MAXPASS && !C::PIPE) {
-    // ---- tiles whose 64 keys are unmasked for every wave, one at a time. In
-    // program order [S0 chain] [S1 chain, exp S0] [P0.V, exp S1] [P1.V]: the
-    // exponentials of one block sit next to the MFMAs of another.
+  if (!MAXPASS) {
+    // ---- tiles whose 64 keys are unmasked for every query of the workgroup
     const int nfull = min(nkt, (causal ? q0 : N) / C::KT);
     for (; t < nfull; ++t) {
       publish(t);
       issue_upto(t + C::NSTAGE - 1);
       const f16* tile = stage(t);
-      const f16* k0row = tile + l32 * C::CW;
-      const f16* k1row = k0row + 32 * C::CW;
-      f32x16 s0 = {}, s1 = {};
 #pragma unroll
-      for (int c = 0; c < C::NCH; ++c)
-        s0 = mfma16(*reinterpret_cast<const f16x8*>(k0row + chunk_off<M>(c) + 8 * h32), qf[c], s0);
-      s0 = mfma8(*reinterpret_cast<const f16x4*>(k0row + M + 4 * h32), qaug, s0);
-#pragma unroll
-      for (int c = 0; c < C::NCH; ++c)
-        s1 = mfma16(*reinterpret_cast<const f16x8*>(k1row + chunk_off<M>(c) + 8 * h32), qf[c], s1);
-      s1 = mfma8(*reinterpret_cast<const f16x4*>(k1row + M + 4 * h32), qaug, s1);
-      f16x8 a0, a1, b0, b1;
-      expo(s0, a0, a1);
-      pv(tile, 0, a0, a1);
-      expo(s1, b0, b1);
-      pv(tile, 1, b0, b1);
-    }
-  }
-  if (!MAXPASS && C::PIPE) {
-    // ---- software-pipelined main loop over the tiles [0, nfull), whose keys
-    // are unmasked for every wave. Block j (32 keys; tile j / 2) passes through
-    // S(j) score MFMAs, E(j) exponentials and PV(j) value MFMAs in three
-    // successive steps; step j issues S(j + 1), E(j) and PV(j - 1), which are
-    // independent, so the matrix pipe and the VALU overlap inside a wave.
-    // Barrier B_k sits between steps 2k and 2k + 1: it publishes tile k + 1
-    // (needed by S(2k + 2)) and then refills the stage of tile k - 1, whose
-    // last reader, PV(2k - 1), ran in step 2k.
-    const int nfull = min(nkt, (causal ? q0 : N) / C::KT);
-    if (nfull > 0) {
-      f32x16 s_cur;
-      f16x8 pp0 = {}, pp1 = {};
-      auto kfrags = [&](const f16* tile, int kb, f16x8 (&kf)[C::NCH], f16x4& kx) {
-        const f16* krow = tile + (32 * kb + l32) * C::CW;
-#pragma unroll
-        for (int c = 0; c < C::NCH; ++c) kf[c] = *reinterpret_cast<const f16x8*>(krow + chunk_off<M>(c) + 8 * h32);
-        kx = *reinterpret_cast<const f16x4*>(krow + M + 4 * h32);
-      };
-      auto vfrags = [&](const f16* tile, int kb, f16x8 (&vf)[4][DV / 32]) {
-#pragma unroll
-        for (int part = 0; part < 4; ++part)
-#pragma unroll
-          for (int dvb = 0; dvb < DV / 32; ++dvb) {
-            const int j = (part >= 2 ? DV / 32 : 0) + dvb;
-            vf[part][dvb] = *reinterpret_cast<const f16x8*>(tile + vofs[kb ^ (j & 1)][part & 1] + 32 * C::KT * j);
-          }
-      };
-      auto score = [&](const f16x8 (&kf)[C::NCH], const f16x4& kx) {
-        f32x16 sc = {};
-#pragma unroll
-        for (int c = 0; c < C::NCH; ++c) sc = mfma16(kf[c], qf[c], sc);
-        return mfma8(kx, qaug, sc);
-      };
-      // one step: S of (tS, kbS) if do_s; E of s_cur; PV of (tV, kbV) with the
-      // previous P if do_pv
-      auto step = [&](bool do_s, const f16* tS, int kbS, bool do_pv, const f16* tV, int kbV) {
+      for (int kb = 0; kb < 2; ++kb) {
         f16x8 kf[C::NCH];
         f16x4 kx;
+        kfrags(tile, kb, kf, kx);
+        f32x16 sc[QB];
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) sc[qb] = score(kf, kx, qb);
         f16x8 vf[4][DV / 32];
-        if (do_s) kfrags(tS, kbS, kf, kx);
-        if (do_pv) vfrags(tV, kbV, vf);
-        __builtin_amdgcn_sched_barrier(0);  // all fragment reads in flight before the math
-        f32x16 s_nxt;
-        if (do_s) s_nxt = score(kf, kx);
-        f16x8 c0, c1;
-        expo(s_cur, c0, c1);
-        if (do_pv) {
+        vfrags(tile, kb, vf);
 #pragma unroll
-          for (int part = 0; part < 4; ++part)
-#pragma unroll
-            for (int dvb = 0; dvb < DV / 32; ++dvb)
-              o[dvb] = mfma16(vf[part][dvb], (part & 1) ? pp1 : pp0, o[dvb]);
+        for (int qb = 0; qb < QB; ++qb) {
+          f16x8 p0, p1;
+          expo(sc[qb], qb, p0, p1);
+          pv(vf, qb, p0, p1);
         }
-        if (do_s) s_cur = s_nxt;
-        pp0 = c0;
-        pp1 = c1;
-      };
-
-      publish(0);  // B_-1: tile 0
-      {
-        f16x8 kf[C::NCH];
-        f16x4 kx;
-        kfrags(stage(0), 0, kf, kx);
-        s_cur = score(kf, kx);
       }
-      step(true, stage(0), 1, false, nullptr, 0);  // step 0
-      for (int k = 0; k + 1 < nfull; ++k) {
-        publish(k + 1);  // B_k
-        issue_upto(k + 2);
-        step(true, stage(k + 1), 0, true, stage(k), 0);  // step 2k + 1
-        step(true, stage(k + 1), 1, true, stage(k), 1);  // step 2k + 2
-      }
-      const int L = nfull - 1;
-      step(false, nullptr, 0, true, stage(L), 0);  // step 2L + 1
-      pv(stage(L), 1, pp0, pp1);                   // PV(2L + 1)
-      t = nfull;
     }
   }
   // ---- remaining tiles (masked ones; all of them in the exact-max pass)
@@ -357,72 +308,93 @@ __device__ __forceinline__ void fwd_pass(const f16* __restrict__ ka, const f16* 
 }
 
 template <int M, int DV>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2 * FwdCfg<M, DV>::WG_PER_CU)))
+__global__ __launch_bounds__((64 * FwdCfg<M, DV>::WAVES))
+__attribute__((amdgpu_waves_per_eu(FwdCfg<M, DV>::WAVES_PER_EU)))
 void attn_fwd_kernel(const f16* __restrict__ qa, const f16* __restrict__ ka, const f16* __restrict__ vt,
                      const float4* __restrict__ tstat, f16* __restrict__ out, float* __restrict__ lse, int N, int NP,
                      int H, int D, int BH, int causal) {
   using C = FwdCfg<M, DV>;
+  constexpr int QB = C::QB;
   __shared__ __align__(16) f16 smem[C::NSTAGE * C::STAGE];
   const int tid = threadIdx.x, lane = tid & 63, h32 = lane >> 5, l32 = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, scalar
   const int nqb = (N + C::QW - 1) / C::QW;
   int bh, blk;
-  if (!xcd_map(nqb, BH, bh, blk)) return;
+  if (!(causal ? xcd_map_lpt(nqb, BH, bh, blk) : xcd_map(nqb, BH, bh, blk))) return;
   const int qblk = causal ? nqb - 1 - blk : blk;  // longest rows first
-  const int q0 = qblk * C::QW, qw0 = q0 + 32 * w, q = qw0 + l32;
-  const bool qvalid = q < N;
+  const int q0 = qblk * C::QW, qw0 = q0 + 32 * QB * w;
   const int b = bh / H, h = bh - b * H;
   const int64_t rowbase = (int64_t)bh * N;
   const int64_t vbase = (int64_t)bh * 2 * DV * NP;
 
-  f16x8 qf[C::NCH];
-  f16x4 qaug = {};
+  f16x8 qf[QB][C::NCH];
+  f16x4 qaug[QB];
+  float R[QB], lsum[QB], rmax[QB];
+  float4 ts[QB];
+  f32x16 o[QB][DV / 32];
+  bool any_gap = false;
 #pragma unroll
-  for (int c = 0; c < C::NCH; ++c) qf[c] = f16x8{};
-  float4 ts = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (qvalid) {
-    const f16* qrow = qa + (rowbase + q) * C::CW;
+  for (int qb = 0; qb < QB; ++qb) {
+    const int q = qw0 + 32 * qb + l32;
+    qaug[qb] = f16x4{};
 #pragma unroll
-    for (int c = 0; c < C::NCH; ++c) qf[c] = *reinterpret_cast<const f16x8*>(qrow + chunk_off<M>(c) + 8 * h32);
-    qaug = *reinterpret_cast<const f16x4*>(qrow + M + 4 * h32);
-    ts = tstat[rowbase + q];
+    for (int c = 0; c < C::NCH; ++c) qf[qb][c] = f16x8{};
+    ts[qb] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (q < N) {
+      const f16* qrow = qa + (rowbase + q) * C::CW;
+#pragma unroll
+      for (int c = 0; c < C::NCH; ++c) qf[qb][c] = *reinterpret_cast<const f16x8*>(qrow + chunk_off<M>(c) + 8 * h32);
+      qaug[qb] = *reinterpret_cast<const f16x4*>(qrow + M + 4 * h32);
+      ts[qb] = tstat[rowbase + q];
+      any_gap = any_gap || ts[qb].z > kGapExact;
+    }
+    R[qb] = ts[qb].y;
+    lsum[qb] = 0.f;
+    rmax[qb] = kNegInf;
+#pragma unroll
+    for (int i = 0; i < DV / 32; ++i) o[qb][i] = f32x16{};
   }
-  float R = ts.y;
   const int kend = causal ? min(N, q0 + C::QW) : N;
-  f32x16 o[DV / 32];
-#pragma unroll
-  for (int i = 0; i < DV / 32; ++i) o[i] = f32x16{};
-  float lsum = 0.f, rmax = kNegInf;
 
-  const bool exact = __syncthreads_or(qvalid && ts.z > kGapExact);
-  if (exact) {
+  if (__syncthreads_or(any_gap)) {
     // pass 1: exact row max of the base-2 exponent without the reference
-    f16x4 qa0 = qaug;
-    if (h32 == 0) { qa0[2] = (f16)0.f; qa0[3] = (f16)0.f; }
-    fwd_pass<M, DV, true>(ka, vt, rowbase, vbase, N, NP, causal, kend, q0, qw0, q, smem, qf, qa0, o, lsum, rmax);
-    rmax = fmaxf(rmax, __shfl_xor(rmax, 32));
-    R = qvalid ? rmax : 0.f;
-    f16 rh, rl;
-    split_hi_lo(-R, rh, rl);
-    if (h32 == 0) { qaug[2] = rh; qaug[3] = rl; }
+    f16x4 qa0[QB];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      qa0[qb] = qaug[qb];
+      if (h32 == 0) { qa0[qb][2] = (f16)0.f; qa0[qb][3] = (f16)0.f; }
+    }
+    fwd_pass<M, DV, true>(ka, vt, rowbase, vbase, N, NP, causal, kend, q0, qw0, smem, qf, qa0, o, lsum, rmax);
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      const float m = fmaxf(rmax[qb], __shfl_xor(rmax[qb], 32));
+      R[qb] = qw0 + 32 * qb + l32 < N ? m : 0.f;
+      f16 rh, rl;
+      split_hi_lo(-R[qb], rh, rl);
+      if (h32 == 0) { qaug[qb][2] = rh; qaug[qb][3] = rl; }
+    }
     __syncthreads();  // every wave is done with the stages before they are refilled
   }
-  fwd_pass<M, DV, false>(ka, vt, rowbase, vbase, N, NP, causal, kend, q0, qw0, q, smem, qf, qaug, o, lsum, rmax);
+  fwd_pass<M, DV, false>(ka, vt, rowbase, vbase, N, NP, causal, kend, q0, qw0, smem, qf, qaug, o, lsum, rmax);
 
-  const float ltot = lsum + __shfl_xor(lsum, 32);
-  if (qvalid) {
-    const float inv = ltot > 0.f ? 1.0f / ltot : 0.f;
-    f16* orow = out + ((int64_t)b * N + q) * D + h * DV;
 #pragma unroll
-    for (int dvb = 0; dvb < DV / 32; ++dvb)
+  for (int qb = 0; qb < QB; ++qb) {
+    const int q = qw0 + 32 * qb + l32;
+    const float ltot = lsum[qb] + __shfl_xor(lsum[qb], 32);
+    if (q < N) {
+      const float inv = ltot > 0.f ? 1.0f / ltot : 0.f;
+      f16* orow = out + ((int64_t)b * N + q) * D + h * DV;
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        f16x4 v;
+      for (int dvb = 0; dvb < DV / 32; ++dvb)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = (f16)(o[dvb][4 * g + e] * inv);
-        *reinterpret_cast<f16x4*>(orow + 32 * dvb + 8 * g + 4 * h32) = v;
-      }
-    if (h32 == 0) lse[rowbase + q] = ltot > 0.f ? R + fast_log2(ltot) + ts.x : -kFltMax;
+        for (int g = 0; g < 4; ++g) {
+          f16x4 v;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = (f16)(o[qb][dvb][4 * g + e] * inv);
+          *reinterpret_cast<f16x4*>(orow + 32 * dvb + 8 * g + 4 * h32) = v;
+        }
+      if (h32 == 0) lse[rowbase + q] = ltot > 0.f ? R[qb] + fast_log2(ltot) + ts[qb].x : -kFltMax;
+    }
   }
 }
 
@@ -578,7 +550,8 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ q
   const int tid = threadIdx.x, lane = tid & 63, h32 = lane >> 5, l32 = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, scalar
   int bh, kblk;
-  if (!xcd_map((N + C::KW - 1) / C::KW, BH, bh, kblk)) return;
+  const int nkb = (N + C::KW - 1) / C::KW;
+  if (!(causal ? xcd_map_lpt(nkb, BH, bh, kblk) : xcd_map(nkb, BH, bh, kblk))) return;
   const int k0 = kblk * C::KW;  // causal: low key blocks see the most queries; they start first
   const int kw0 = k0 + 32 * w;
   const int key = kw0 + l32;
