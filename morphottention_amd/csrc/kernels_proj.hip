@@ -324,23 +324,26 @@ hipError_t launch_dx_gemm(const Dims& d, const f16* W_phi, const f16* W_V, const
 }
 
 // ---------------------------------------------------------------- [dW_phi | dW_V] = X^T [dZ | dV]
+// Split-K over tokens: one K slice per XCD (workgroup id % 8), so the tiles
+// that share a slice's A and B panels run on one L2 and stream them together.
 int dw_splits(const Dims& d) {
-  const int tiles = ((d.HM + d.D + kGemmBN - 1) / kGemmBN) * ((d.D + kGemmBM - 1) / kGemmBM);
-  int s = (512 + tiles - 1) / tiles;
   const int kmax = (int)((d.T + 255) / 256);  // keep >= 256 tokens per split
-  if (s > kmax) s = kmax;
-  if (s < 1) s = 1;
-  return s;
+  return kmax < 8 ? kmax : 8;
 }
 
 __global__ __launch_bounds__(256) void dw_gemm_kernel(const f16* __restrict__ X, const f16* __restrict__ dzv,
-                                                      float* __restrict__ wpart, Dims d, int kchunk) {
+                                                      float* __restrict__ wpart, Dims d, int kchunk, int nsplit) {
   using ML = GemmMainloop<false, false>;
   __shared__ __align__(16) f16 smem[ML::kLdsHalves];
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = w >> 1, wn = w & 1;
-  const int n0 = blockIdx.x * kGemmBN, m0 = blockIdx.y * kGemmBM, z = blockIdx.z;
   const int NC = d.HM + d.D;
+  // id = 8 * slot + xcd; split = xcd (+ 8 per extra round), tile = slot within the split
+  const int ntn = (NC + kGemmBN - 1) / kGemmBN, ntm = (d.D + kGemmBM - 1) / kGemmBM;
+  const int id = blockIdx.x, xcd = id & 7, slot = id >> 3;
+  const int tile = slot % (ntn * ntm), z = xcd + 8 * (slot / (ntn * ntm));
+  if (z >= nsplit) return;
+  const int n0 = (tile % ntn) * kGemmBN, m0 = (tile / ntn) * kGemmBM;
   const int T = (int)d.T;
   const int kbeg = z * kchunk;
   const int kend = kbeg + kchunk < T ? kbeg + kchunk : T;
@@ -367,8 +370,10 @@ hipError_t launch_dw_gemm(const Dims& d, const f16* X, const BwdBuffers& g, hipS
   const int T = (int)d.T;
   int kchunk = (T + S - 1) / S;
   kchunk = (kchunk + kGemmBK - 1) / kGemmBK * kGemmBK;
-  dim3 grid((d.HM + d.D + kGemmBN - 1) / kGemmBN, (d.D + kGemmBM - 1) / kGemmBM, S);
-  hipLaunchKernelGGL(dw_gemm_kernel, grid, dim3(256), 0, s, X, g.dzv, g.wpart, d, kchunk);
+  const int tiles = ((d.HM + d.D + kGemmBN - 1) / kGemmBN) * ((d.D + kGemmBM - 1) / kGemmBM);
+  const int rounds = (S + 7) / 8;
+  dim3 grid(8u * (unsigned)tiles * (unsigned)rounds);
+  hipLaunchKernelGGL(dw_gemm_kernel, grid, dim3(256), 0, s, X, g.dzv, g.wpart, d, kchunk, S);
   return hipGetLastError();
 }
 
