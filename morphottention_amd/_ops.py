@@ -26,7 +26,7 @@ def _load_c_extension() -> str:
             return matches[0]
     raise ImportError(
         f"Could not find the compiled morphottention '_C' extension in {pkg_dir}. "
-        "Build it with `python -m morphottention_amd.build` (hipcc, gfx950)."
+        "Build it with `python morphottention_amd/build.py` (hipcc, gfx950)."
     )
 
 

@@ -5,7 +5,8 @@
 * ``_C.so`` -- the ``torch.ops.morphottention`` registrations, a thin C++ layer
   that calls the C ABI (host code only, compiled with g++).
 
-Usage: ``python -m morphottention_amd.build`` (or ``__graft_entry__.build()``).
+Usage: ``python morphottention_amd/build.py`` (or ``__graft_entry__.build()``). It is
+run as a script, not as ``-m``: importing the package needs the built library.
 """
 
 from __future__ import annotations

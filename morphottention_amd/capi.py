@@ -21,7 +21,7 @@ def lib() -> ctypes.CDLL:
     global _lib
     if _lib is None:
         if not os.path.exists(LIB_PATH):
-            raise ImportError(f"{LIB_PATH} is missing; build it with `python -m morphottention_amd.build`")
+            raise ImportError(f"{LIB_PATH} is missing; build it with `python morphottention_amd/build.py`")
         L = ctypes.CDLL(LIB_PATH)
         i64, vp, sz = ctypes.c_int64, ctypes.c_void_p, ctypes.c_size_t
         L.morpho_version.restype = ctypes.c_int
