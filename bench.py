@@ -85,7 +85,8 @@ def load_traffic(kernel, config):
     try:
         with open(path) as f:
             data = json.load(f)
-        return data["kernels"][kernel]["hbm_bytes_per_launch"]
+        # the profiler names the device function, e.g. attn_bwd -> attn_bwd_kernel
+        return data["kernels"][f"{kernel}_kernel"]["hbm_bytes_per_launch"]
     except (OSError, KeyError, ValueError):
         return None
 
