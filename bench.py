@@ -50,8 +50,7 @@ def kernel_flops(name, B, N, D, H, m, causal):
         "proj_fwd": 2.0 * T * D * (HM + D),
         "attn_fwd": 2.0 * P * (m + dv),
         "attn_bwd": 2.0 * P * (3 * m + 2 * dv),
-        "dx_gemm": 2.0 * T * (HM + D) * D,
-        "dw_gemm": 2.0 * T * D * (HM + D),
+        "bwd_gemm": 4.0 * T * (HM + D) * D,  # dX and [dW_phi | dW_V] in one launch
     }.get(name)
 
 

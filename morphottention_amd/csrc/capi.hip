@@ -81,6 +81,19 @@ int make_dims(int64_t B, int64_t N, int64_t D, int64_t H, int64_t M, float scale
   d.CW = 3 * (int)M + 8;
   d.scale = scale;
   d.causal = causal ? 1 : 0;
+  // projection tiles: 320 columns when that divides H*M + D, else 256; the
+  // interleaved column order needs whole heads and 8-column pieces per tile
+  const int NC = d.HM + d.D;
+  d.PBN = NC % 320 == 0 ? 320 : 256;
+  d.PCPT = d.PVPT = 0;
+  if (NC % d.PBN == 0) {
+    const int ntn = NC / d.PBN;
+    if (d.HM % ntn == 0 && d.D % ntn == 0 && (d.HM / ntn) % d.M == 0 && (d.HM / ntn) % 8 == 0 &&
+        (d.D / ntn) % 8 == 0) {
+      d.PCPT = d.HM / ntn;
+      d.PVPT = d.D / ntn;
+    }
+  }
   return MORPHO_OK;
 }
 
@@ -92,6 +105,7 @@ size_t proj_bytes(const Dims& d) {
   s += align_up((size_t)d.B * d.H * d.NP * d.DV * 4);  // vt (hi | lo rows)
   s += align_up(bhn * 16);               // tstat
   s += align_up((size_t)(d.HM + d.D) * d.D * 2);  // wt
+  s += align_up((size_t)(d.HM + d.D) * d.D * 2);  // wcat
   return s;
 }
 
@@ -103,7 +117,8 @@ ProjBuffers carve_proj(void* base, const Dims& d) {
   b.ka = reinterpret_cast<_Float16*>(p); p += align_up(bhn * d.CW * 2);
   b.vt = reinterpret_cast<_Float16*>(p); p += align_up((size_t)d.B * d.H * d.NP * d.DV * 4);
   b.tstat = reinterpret_cast<float4*>(p); p += align_up(bhn * 16);
-  b.wt = reinterpret_cast<_Float16*>(p);
+  b.wt = reinterpret_cast<_Float16*>(p); p += align_up((size_t)(d.HM + d.D) * d.D * 2);
+  b.wcat = reinterpret_cast<_Float16*>(p);
   return b;
 }
 
@@ -150,7 +165,7 @@ bool misaligned(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) !=
 int run_projection(const Dims& d, const void* X, const void* W_phi, const void* gate_q, const void* gate_k,
                    const void* W_V, const ProjBuffers& p, hipStream_t s) {
   MORPHO_LAUNCH("transpose_weights", launch_transpose_weights(d, static_cast<const _Float16*>(W_phi),
-                                                              static_cast<const _Float16*>(W_V), p.wt, s));
+                                                              static_cast<const _Float16*>(W_V), p.wt, p.wcat, s));
   MORPHO_LAUNCH("proj_fwd", launch_proj_fwd(d, static_cast<const _Float16*>(X), static_cast<const _Float16*>(gate_q),
                                             static_cast<const _Float16*>(gate_k), p, s));
   return MORPHO_OK;
@@ -276,13 +291,11 @@ MORPHO_EXPORT int morpho_backward(const void* grad_out, const void* X, const voi
   MORPHO_LAUNCH("attn_bwd", launch_attn_bwd(d, p, go, g, s));
   MORPHO_LAUNCH("proj_bwd_elem", launch_proj_bwd_elem(d, static_cast<const _Float16*>(gate_q),
                                                       static_cast<const _Float16*>(gate_k), p, g, s));
-  MORPHO_LAUNCH("gate_reduce", launch_gate_reduce(d, g, static_cast<const _Float16*>(gate_q),
-                                                  static_cast<const _Float16*>(gate_k), static_cast<_Float16*>(d_gate_q),
-                                                  static_cast<_Float16*>(d_gate_k), s));
-  MORPHO_LAUNCH("dx_gemm", launch_dx_gemm(d, static_cast<const _Float16*>(W_phi), static_cast<const _Float16*>(W_V), g,
-                                          static_cast<_Float16*>(dX), s));
-  MORPHO_LAUNCH("dw_gemm", launch_dw_gemm(d, static_cast<const _Float16*>(X), g, s));
-  MORPHO_LAUNCH("dw_reduce", launch_dw_reduce(d, g, static_cast<_Float16*>(dW_phi), static_cast<_Float16*>(dW_V), s));
+  MORPHO_LAUNCH("bwd_gemm", launch_bwd_gemm(d, p, g, static_cast<const _Float16*>(X), static_cast<_Float16*>(dX), s));
+  MORPHO_LAUNCH("dw_reduce", launch_dw_reduce(d, g, static_cast<const _Float16*>(gate_q),
+                                              static_cast<const _Float16*>(gate_k), static_cast<_Float16*>(dW_phi),
+                                              static_cast<_Float16*>(dW_V), static_cast<_Float16*>(d_gate_q),
+                                              static_cast<_Float16*>(d_gate_k), s));
   return MORPHO_OK;
 }
 

@@ -105,6 +105,33 @@ __device__ __forceinline__ f16x8 pack8(const f32x16& v, int base) {
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
 
+// s_waitcnt on the vector-memory counter only (gfx9 encoding: vmcnt[3:0],
+// expcnt[6:4] = 7 and lgkmcnt[11:8] = 15 mean "no wait", vmcnt[5:4] at [15:14]).
+template <int CNT>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(CNT >= 0 && CNT < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((CNT & 15) | (7 << 4) | (15 << 8) | ((CNT >> 4) << 14));
+}
+
+// 16 bytes per lane from global memory straight into LDS: lane l of the wave
+// writes LDS byte address lds_addr + 16 l (lds_addr wave-uniform). Issued as
+// inline asm so that the compiler does not order every later LDS read after
+// it: the callers wait for these loads explicitly (wait_vmcnt) before the
+// barrier that publishes a stage.
+__device__ __forceinline__ void lds_dma16(const f16* g, unsigned lds_addr) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds_addr))
+               : "memory", "m0");
+}
+
+// s_waitcnt: vector-memory count CNT and LDS count 0 (gfx9 encoding).
+template <int CNT>
+__device__ __forceinline__ void wait_vmcnt_lgkm0() {
+  static_assert(CNT >= 0 && CNT < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((CNT & 15) | (7 << 4) | (0 << 8) | ((CNT >> 4) << 14));
+}
+
 __device__ __forceinline__ float sigmoidf_(float z) { return 1.0f / (1.0f + __expf(-z)); }
 
 }  // namespace morpho

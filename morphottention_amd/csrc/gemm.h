@@ -1,159 +1,244 @@
 // Block-tiled fp16 MFMA GEMM main loop (fp32 accumulation) for gfx950.
 //
-// C[m][n] = sum_k A(m, k) * B(k, n) over one 128 x 128 output tile per
-// 256-thread workgroup (4 waves, each 64 x 64 = 2 x 2 blocks of 32x32x16
-// MFMAs), k stepped by 64 through double-buffered LDS with the global loads of
-// the next two k-steps in flight during the current one.
+// C[m][n] = sum_k A(m, k) B(k, n) over one BM x BN output tile per workgroup
+// of 8 waves (512 threads, two per SIMD) in a WM x WN arrangement, each wave
+// owning a (BM / WM) x (BN / WN) block of 32x32x16 MFMA accumulators. k
+// advances by 64 through two LDS stages that the waves fill by DMA
+// (global_load_lds_dwordx4, 1 KiB per wave instruction): the stage of k-step
+// t + 1 is issued right after the barrier that opens k-step t and lands while
+// t is computed, so no VGPRs hold prefetched data.
 //
-// Operands are described by OperandDesc. "k-contiguous" operands are staged in
-// LDS row = m (or n), and read with one 16-byte load per fragment; "k-major"
-// operands (k is the row index in memory, e.g. X read as X^T) are staged as
-// they lie in memory and read with ds_read_b64_tr_b16, so no transposing
-// stores are needed.
+// Why these shapes: a 256 x 256 (or 256 x 320) tile moves 64 (72) KiB from L2
+// per 8.4 (10.5) MFLOP. With 256 x 128 tiles the L2 -> CU traffic at the
+// MFMA rate (~25 TB/s for the whole chip) was the bound; here it is ~15 TB/s.
+//
+// Operand kinds:
+//  * k-contiguous ("KC", element (row, k) at p[row * ld + k]): LDS rows of
+//    64 halves (128 bytes), the 16-byte chunk c of row r stored at chunk
+//    position c ^ ((r >> 1) & 7). A fragment is one ds_read_b128 per lane and
+//    the 16 lanes of a read phase hit 16 distinct 4-bank groups.
+//  * k-major ("KM", element (k, row) at p[k * ld + row], e.g. X read as X^T):
+//    LDS rows k of ROWS halves (ROWS a power of two >= 128), chunk c of row k
+//    stored at c ^ ((k & 3) << 2). Fragments come from ds_read_b64_tr_b16 (the
+//    transposing read); the 32 lanes of a phase cover 4 rows x 64 bytes on 64
+//    distinct banks.
+// Rows past the operand's extent load clamped (finite) data that only feeds
+// discarded outputs; k past kend is zeroed in LDS on the last k-step.
 #pragma once
 
 #include "common.h"
 
 namespace morpho {
 
-struct OperandDesc {
-  const f16* p;   // segment 0
-  int64_t ld;     // leading dimension of segment 0 (elements)
-  const f16* p2;  // segment 1 (k >= kseg), k-contiguous operands only
-  int64_t ld2;
-  int kseg;       // first k of segment 1 (multiple of 8); INT_MAX if none
+constexpr int kGemmWaves = 8;
+constexpr int kGemmThreads = 64 * kGemmWaves;
+
+// DMA of one 16-byte piece per lane from sbase + voff (32-bit unsigned lane
+// offset, 64-bit wave-uniform base) to LDS byte address lds_addr + 16 lane.
+__device__ __forceinline__ void lds_dma16_so(const void* sbase, unsigned voff, unsigned lds_addr) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(voff), "s"(sbase), "s"(__builtin_amdgcn_readfirstlane(lds_addr))
+               : "memory", "m0");
+}
+
+template <bool KC, int ROWS, int BK>
+struct OpTile {
+  static_assert(BK == 32 || BK == 64, "k-step of 32 or 64");
+  static constexpr int kBytes = ROWS * BK * 2;
+  static constexpr int kDma = kBytes / 1024;            // 1 KiB DMA pieces per tile
+  static constexpr int kRowChunks = KC ? BK / 8 : ROWS / 8;  // 16-byte chunks per LDS row
+  // KC chunk swizzle: with 8 chunks per row (BK = 64) rows r and r + 1 share a
+  // swizzle and 16 rows span 8 values; with 4 (BK = 32) rows r .. r + 3 share.
+  __device__ __forceinline__ static int kc_swz(int r) { return BK == 64 ? (r >> 1) & 7 : (r >> 2) & 3; }
+  static_assert(KC || (ROWS >= 128 && (ROWS & (ROWS - 1)) == 0), "KM swizzle needs 2^n >= 16 chunks per row");
+
+  // Tile row and k of LDS chunk q = 64 piece + lane.
+  __device__ __forceinline__ static void chunk(int q, int& r, int& k8) {
+    if (KC) {
+      r = q / kRowChunks;
+      k8 = 8 * ((q % kRowChunks) ^ kc_swz(r));  // first k of the chunk
+    } else {
+      k8 = q / kRowChunks;                           // the chunk's k
+      r = 8 * ((q % kRowChunks) ^ ((k8 & 3) << 2));  // first row of the chunk
+    }
+  }
+
+  // Byte offset of the chunk from the tile's base (operand at row0, k0), with
+  // rows clamped into [0, rmax): rows past the extent re-read a valid row and
+  // only feed discarded outputs. Fits 32 bits for ld <= 65536.
+  __device__ __forceinline__ static unsigned lane_off(int64_t ld, int rmax, int piece, int lane) {
+    int r, k8;
+    chunk(64 * piece + lane, r, k8);
+    if (KC) return (unsigned)(((int64_t)min(r, rmax - 1) * ld + k8) * 2);
+    return (unsigned)(((int64_t)k8 * ld + min(r, rmax - 8)) * 2);
+  }
+  __device__ __forceinline__ static const char* tile_base(const f16* p, int64_t ld, int row0, int k0) {
+    return reinterpret_cast<const char*>(KC ? p + (int64_t)row0 * ld + k0 : p + (int64_t)k0 * ld + row0);
+  }
+  // Full address with k clamped into [k0, kend) as well (the ragged last
+  // k-step). KC needs kend % 8 == 0; KM needs nrows % 8 == 0.
+  __device__ __forceinline__ static const f16* tail_src(const f16* p, int64_t ld, int row0, int nrows, int k0,
+                                                        int kend, int piece, int lane) {
+    int r, k8;
+    chunk(64 * piece + lane, r, k8);
+    if (KC) return p + (int64_t)min(row0 + r, nrows - 1) * ld + min(k0 + k8, kend - 8);
+    return p + (int64_t)min(k0 + k8, kend - 1) * ld + min(row0 + r, nrows - 8);
+  }
+
+  // Zero the k >= kvalid part of a stage tile (kvalid < BK; last k-step only).
+  __device__ __forceinline__ static void zero_tail(char* s, int kvalid, int tid) {
+    for (int q = tid; q < kBytes / 16; q += kGemmThreads) {
+      int r, k8;
+      chunk(q, r, k8);
+      if (k8 >= kvalid) *reinterpret_cast<f16x8*>(s + 16 * q) = f16x8{};
+    }
+  }
+
+  // MFMA 32x32x16 operand for the 32-row block at tile row (or column) mn0,
+  // k chunk kc (k = 16 kc .. 16 kc + 15): lane l supplies row mn0 + l % 32,
+  // k = 16 kc + 8 (l / 32) + j.
+  __device__ __forceinline__ static f16x8 frag(const char* s, int mn0, int kc, int lane) {
+    if (KC) {
+      const int row = mn0 + (lane & 31);  // mn0 % 32 == 0, so kc_swz(row) == kc_swz(lane & 31)
+      const int c = (2 * kc + (lane >> 5)) ^ kc_swz(lane & 31);
+      return *reinterpret_cast<const f16x8*>(s + row * (BK * 2) + 16 * c);
+    } else {
+      const int g = lane >> 4;
+      const int k = 16 * kc + 8 * (g >> 1) + ((lane & 15) >> 2);
+      const int col = mn0 + 16 * (g & 1) + 4 * (lane & 3);
+      const int c = (col >> 3) ^ (((lane >> 2) & 3) << 2);  // (k & 3) == (lane >> 2) & 3
+      const char* p = s + k * (ROWS * 2) + 16 * c + 2 * (col & 7);
+      typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
+      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p + 4 * ROWS * 2));
+      return __builtin_bit_cast(f16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+    }
+  }
 };
 
-constexpr int kGemmBM = 128, kGemmBN = 128, kGemmBK = 64, kGemmThreads = 256;
+template <int BM, int BN, int WM, bool AKC, bool BKC, int BK = 32, int STAGES = 4>
+struct Gemm {
+  static constexpr int kBK = BK;
+  static constexpr int WN = kGemmWaves / WM;
+  using TA = OpTile<AKC, BM, BK>;
+  using TB = OpTile<BKC, BN, BK>;
+  static constexpr int kStages = STAGES;
+  static constexpr int kStageBytes = TA::kBytes + TB::kBytes;
+  static constexpr int kLdsBytes = kStages * kStageBytes;
+  static constexpr int WTM = BM / WM, WTN = BN / WN;  // wave tile
+  static constexpr int FI = WTM / 32, FJ = WTN / 32;
+  // DMA pieces of a stage, A's first; wave w issues pieces w, w + 8, ...
+  // A's piece count is a multiple of 8, so whether a wave's i-th piece is A or
+  // B is known at compile time; the first kP % 8 waves issue one piece more.
+  static constexpr int kP = TA::kDma + TB::kDma;
+  static constexpr int kPA = TA::kDma / kGemmWaves;      // A pieces per wave
+  static constexpr int kPBmax = (TB::kDma + kGemmWaves - 1) / kGemmWaves;
+  static constexpr int kNhi = (kP + kGemmWaves - 1) / kGemmWaves, kNlo = kP / kGemmWaves;
+  static_assert(TA::kDma % kGemmWaves == 0, "A pieces must split evenly over the waves");
+  static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be whole 32x32 blocks");
+  static_assert((STAGES - 2) * kNhi < 64, "vmcnt range");
 
-template <bool KCONTIG, int ROWS>
-struct GemmOperandTile {
-  // LDS row stride (halves): 36 dwords for b128 fragment reads (8 rows -> 8
-  // distinct bank groups), 16 (mod 64) halves for transposed reads.
-  static constexpr int kStride = KCONTIG ? (kGemmBK + 8) : (ROWS + 16);
-  static constexpr int kElems = KCONTIG ? ROWS * kStride : kGemmBK * kStride;  // one buffer
-  static constexpr int kVecs = ROWS * kGemmBK / 8;                           // 16-byte vectors per tile
-  static constexpr int kRegs = kVecs / kGemmThreads;
-  static constexpr int kRowVecs = KCONTIG ? kGemmBK / 8 : ROWS / 8;           // vectors per LDS row
-
-  f16x8 reg[kRegs];
-
-  // Global -> registers for the tile at (row0, k0); rows >= nrows or k >= kend
-  // read as zero. nrows and kend are multiples of 8 for the contiguous axis.
-  __device__ __forceinline__ void load(const OperandDesc& d, int row0, int nrows, int k0, int kend, int tid) {
-#pragma unroll
-    for (int i = 0; i < kRegs; ++i) {
-      const int v = tid + kGemmThreads * i;
-      const int lr = v / kRowVecs, lc = (v % kRowVecs) * 8;  // LDS row, column
-      f16x8 x = {};
-      if (KCONTIG) {
-        const int gr = row0 + lr, gk = k0 + lc;
-        if (gr < nrows && gk < kend) {
-          const f16* src = gk < d.kseg ? d.p + (int64_t)gr * d.ld + gk : d.p2 + (int64_t)gr * d.ld2 + (gk - d.kseg);
-          x = *reinterpret_cast<const f16x8*>(src);
-        }
-      } else {
-        const int gk = k0 + lr, gr = row0 + lc;
-        if (gk < kend && gr < nrows) x = *reinterpret_cast<const f16x8*>(d.p + (int64_t)gk * d.ld + gr);
-      }
-      reg[i] = x;
-    }
+  // wait until this wave's pieces of the stage issued `ahead` stages before
+  // the latest one have landed (the later `ahead` stages may be in flight)
+  template <int AHEAD>
+  __device__ __forceinline__ static void wait_stage(int w) {
+    if (w < kP % kGemmWaves)
+      wait_vmcnt_lgkm0<AHEAD * kNhi>();
+    else
+      wait_vmcnt_lgkm0<AHEAD * kNlo>();
   }
 
-  __device__ __forceinline__ void store(f16* s, int tid) const {
-#pragma unroll
-    for (int i = 0; i < kRegs; ++i) {
-      const int v = tid + kGemmThreads * i;
-      const int lr = v / kRowVecs, lc = (v % kRowVecs) * 8;
-      *reinterpret_cast<f16x8*>(s + lr * kStride + lc) = reg[i];
-    }
-  }
-
-  // Fragment for the 32-row block starting at `row0` (tile-local), k chunk c.
-  __device__ __forceinline__ static f16x8 frag(const f16* s, int row0, int c, int lane) {
-    if (KCONTIG) return frag_kcontig(s, kStride, row0 + (lane & 31), 16 * c, lane);
-    return frag_kmajor(s, kStride, 16 * c, row0, lane);
-  }
-};
-
-template <bool AKC, bool BKC>
-struct GemmMainloop {
-  using TA = GemmOperandTile<AKC, kGemmBM>;
-  using TB = GemmOperandTile<BKC, kGemmBN>;
-  static constexpr int kLdsHalves = 2 * (TA::kElems + TB::kElems);
-
-  // acc[i][j] holds C rows m0 + 64*wm + 32*i + acc_row(r), cols n0 + 64*wn + 32*j + lane%32
-  __device__ __forceinline__ static void compute(const f16* sa, const f16* sb, int wm, int wn, int lane,
-                                                 f32x16 acc[2][2]) {
-#pragma unroll
-    for (int c = 0; c < kGemmBK / 16; ++c) {
-      f16x8 a0 = TA::frag(sa, 64 * wm, c, lane);
-      f16x8 a1 = TA::frag(sa, 64 * wm + 32, c, lane);
-      f16x8 b0 = TB::frag(sb, 64 * wn, c, lane);
-      f16x8 b1 = TB::frag(sb, 64 * wn + 32, c, lane);
-      acc[0][0] = mfma16(a0, b0, acc[0][0]);
-      acc[0][1] = mfma16(a0, b1, acc[0][1]);
-      acc[1][0] = mfma16(a1, b0, acc[1][0]);
-      acc[1][1] = mfma16(a1, b1, acc[1][1]);
-    }
-  }
-
-  // Two register stages: while k-step kt is computed from LDS, the loads of
-  // k-steps kt+1 and kt+2 are in flight. The loop is unrolled by two so the
-  // stages never change registers while their loads are outstanding.
-  __device__ __forceinline__ static void run(const OperandDesc& A, const OperandDesc& B, int M, int N, int m0, int n0,
-                                             int kbeg, int kend, f16* lds, f32x16 acc[2][2]) {
+  // Wave w owns rows WTM * (w / WN) .. and columns WTN * (w % WN) .. of the
+  // tile; acc[i][j] holds C rows m0 + WTM * (w / WN) + 32 i + acc_row(r, lane),
+  // columns n0 + WTN * (w % WN) + 32 j + lane % 32.
+  // Operands: A (M rows) and B (N rows = columns of C), each one matrix
+  // (p, ld); k runs over [kbeg, kend). lds: kLdsBytes, 16-byte aligned.
+  __device__ __forceinline__ static void run(const f16* Ap, int64_t lda, const f16* Bp, int64_t ldb, int M, int N,
+                                             int m0, int n0, int kbeg, int kend, char* lds, f32x16 (&acc)[FI][FJ]) {
     const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = w >> 1, wn = w & 1;
-    f16* sA[2] = {lds, lds + TA::kElems};
-    f16* sB[2] = {lds + 2 * TA::kElems, lds + 2 * TA::kElems + TB::kElems};
+    const int wm = w / WN, wn = w % WN;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < FI; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
-    const int nk = (kend - kbeg + kGemmBK - 1) / kGemmBK;
+      for (int j = 0; j < FJ; ++j) acc[i][j] = f32x16{};
+    const int nk = (kend - kbeg + kBK - 1) / kBK;
     if (nk <= 0) return;
-    TA ta0, ta1;
-    TB tb0, tb1;
-    auto kof = [&](int kt) { return kbeg + kt * kGemmBK; };
-    ta0.load(A, m0, M, kof(0), kend, tid);
-    tb0.load(B, n0, N, kof(0), kend, tid);
-    ta0.store(sA[0], tid);
-    tb0.store(sB[0], tid);
-    if (nk > 1) {
-      ta1.load(A, m0, M, kof(1), kend, tid);
-      tb1.load(B, n0, N, kof(1), kend, tid);
+    const unsigned sbase = (unsigned)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
+
+    // this wave's pieces: A pieces w + 8 i, B pieces w + 8 i (< TB::kDma)
+    unsigned offA[kPA], offB[kPBmax];
+#pragma unroll
+    for (int i = 0; i < kPA; ++i) offA[i] = TA::lane_off(lda, M - m0, w + kGemmWaves * i, lane);
+#pragma unroll
+    for (int i = 0; i < kPBmax; ++i)
+      offB[i] = TB::lane_off(ldb, N - n0, min(w + kGemmWaves * i, TB::kDma - 1), lane);
+    const int64_t stepA = AKC ? 2 * kBK : 2 * kBK * lda, stepB = BKC ? 2 * kBK : 2 * kBK * ldb;  // bytes per k-step
+    const char* baseA = TA::tile_base(Ap, lda, m0, kbeg);
+    const char* baseB = TB::tile_base(Bp, ldb, n0, kbeg);
+
+    auto issue = [&](int t) {
+      const unsigned st = sbase + (unsigned)((t % kStages) * kStageBytes);
+      const int k0 = kbeg + t * kBK;
+      if (k0 + kBK <= kend) {  // uniform
+#pragma unroll
+        for (int i = 0; i < kPA; ++i)
+          lds_dma16_so(baseA + t * stepA, offA[i], st + 1024u * (unsigned)(w + kGemmWaves * i));
+#pragma unroll
+        for (int i = 0; i < kPBmax; ++i)
+          if (w + kGemmWaves * i < TB::kDma)  // uniform
+            lds_dma16_so(baseB + t * stepB, offB[i],
+                         st + (unsigned)TA::kBytes + 1024u * (unsigned)(w + kGemmWaves * i));
+      } else {
+#pragma unroll
+        for (int i = 0; i < kPA; ++i)
+          lds_dma16(TA::tail_src(Ap, lda, m0, M, k0, kend, w + kGemmWaves * i, lane),
+                    st + 1024u * (unsigned)(w + kGemmWaves * i));
+#pragma unroll
+        for (int i = 0; i < kPBmax; ++i)
+          if (w + kGemmWaves * i < TB::kDma)
+            lds_dma16(TB::tail_src(Bp, ldb, n0, N, k0, kend, w + kGemmWaves * i, lane),
+                      st + (unsigned)TA::kBytes + 1024u * (unsigned)(w + kGemmWaves * i));
+      }
+    };
+
+    // stages t .. t + STAGES - 2 are in flight when k-step t opens
+#pragma unroll
+    for (int t = 0; t < STAGES - 1; ++t)
+      if (t < nk) issue(t);
+    for (int t = 0; t < nk; ++t) {
+      // this wave's pieces of stage t have landed (later stages may not have)
+      if (t + STAGES - 2 < nk)
+        wait_stage<STAGES - 2>(w);
+      else
+        wait_vmcnt_lgkm0<0>();
+      asm volatile("s_barrier" ::: "memory");  // ... and every wave's; stage t - 1 is free
+      char* sa = lds + (t % kStages) * kStageBytes;
+      char* sb = sa + TA::kBytes;
+      const int kvalid = kend - (kbeg + t * kBK);
+      if (kvalid < kBK) {  // uniform: last k-step of a ragged K
+        TA::zero_tail(sa, kvalid, tid);
+        TB::zero_tail(sb, kvalid, tid);
+        wait_vmcnt_lgkm0<0>();
+        asm volatile("s_barrier" ::: "memory");
+      }
+      if (t + STAGES - 1 < nk) issue(t + STAGES - 1);
+#pragma unroll
+      for (int kc = 0; kc < kBK / 16; ++kc) {
+        f16x8 a[FI], b[FJ];
+#pragma unroll
+        for (int i = 0; i < FI; ++i) a[i] = TA::frag(sa, WTM * wm + 32 * i, kc, lane);
+#pragma unroll
+        for (int j = 0; j < FJ; ++j) b[j] = TB::frag(sb, WTN * wn + 32 * j, kc, lane);
+#pragma unroll
+        for (int i = 0; i < FI; ++i)
+#pragma unroll
+          for (int j = 0; j < FJ; ++j) acc[i][j] = mfma16(a[i], b[j], acc[i][j]);
+      }
     }
-    if (nk > 2) {
-      ta0.load(A, m0, M, kof(2), kend, tid);
-      tb0.load(B, n0, N, kof(2), kend, tid);
-    }
-    __syncthreads();
-    for (int kt = 0; kt < nk; kt += 2) {
-      // even step: LDS buffer 0 holds kt; stage 1 holds kt+1; stage 0 holds kt+2
-      compute(sA[0], sB[0], wm, wn, lane, acc);
-      if (kt + 1 < nk) {
-        ta1.store(sA[1], tid);
-        tb1.store(sB[1], tid);
-      }
-      __syncthreads();
-      if (kt + 3 < nk) {
-        ta1.load(A, m0, M, kof(kt + 3), kend, tid);
-        tb1.load(B, n0, N, kof(kt + 3), kend, tid);
-      }
-      if (kt + 1 >= nk) break;
-      // odd step: LDS buffer 1 holds kt+1; stage 0 holds kt+2; stage 1 holds kt+3
-      compute(sA[1], sB[1], wm, wn, lane, acc);
-      if (kt + 2 < nk) {
-        ta0.store(sA[0], tid);
-        tb0.store(sB[0], tid);
-      }
-      __syncthreads();
-      if (kt + 4 < nk) {
-        ta0.load(A, m0, M, kof(kt + 4), kend, tid);
-        tb0.load(B, n0, N, kof(kt + 4), kend, tid);
-      }
-    }
+    // every wave is done with the stages before the caller reuses the LDS
+    wait_vmcnt_lgkm0<0>();
+    asm volatile("s_barrier" ::: "memory");
   }
 };
 
@@ -161,8 +246,8 @@ struct GemmMainloop {
 // XCDs (id % 8). Give all `ncols` column tiles of one row panel ids that are
 // congruent mod 8, so the panel is fetched into one XCD's L2. Returns false for
 // padding ids; the grid must have 8 * ceil(nrows / 8) * ncols workgroups.
-__device__ __forceinline__ bool gemm_tile_map(int nrows, int ncols, int& tr, int& tc) {
-  const int i = blockIdx.x, xcd = i & 7, slot = i >> 3;
+__device__ __forceinline__ bool gemm_tile_map(int id, int nrows, int ncols, int& tr, int& tc) {
+  const int xcd = id & 7, slot = id >> 3;
   tr = 8 * (slot / ncols) + xcd;
   tc = slot % ncols;
   return tr < nrows;

@@ -15,7 +15,25 @@ struct Dims {
   int CW;                 // 3 * M + 8: code row width (hi/lo split codes + affine augmentation)
   float scale;
   int causal;
+  // Column order of the forward projection's B operand (wt rows): tiles of
+  // PBN columns; when PCPT > 0 tile j holds code columns [j PCPT, (j+1) PCPT)
+  // then value columns [j PVPT, (j+1) PVPT), so every tile does the same
+  // epilogue work; PCPT == 0 keeps the natural order [W_phi | W_V].
+  int PBN, PCPT, PVPT;
 };
+
+// Original [W_phi | W_V] column of local column lc of projection tile tn.
+__host__ __device__ inline int proj_col(const Dims& d, int tn, int lc) {
+  if (d.PCPT == 0) return tn * d.PBN + lc;
+  return lc < d.PCPT ? tn * d.PCPT + lc : d.HM + tn * d.PVPT + (lc - d.PCPT);
+}
+// wt row (position in the projection's column order) of original column c.
+__host__ __device__ inline int proj_row(const Dims& d, int c) {
+  if (d.PCPT == 0) return c;
+  if (c < d.HM) return (c / d.PCPT) * d.PBN + c % d.PCPT;
+  const int v = c - d.HM;
+  return (v / d.PVPT) * d.PBN + d.PCPT + v % d.PVPT;
+}
 
 // Products of the forward projection; the forward workspace holds exactly these.
 //
@@ -36,6 +54,7 @@ struct ProjBuffers {
                    // zero for tokens N..NP-1
   float4* tstat;   // [B*H, N] {b, R, gap, 0}: token bias, softmax reference, bound gap (base 2)
   _Float16* wt;    // [H*M + D, D] transposed [W_phi | W_V]
+  _Float16* wcat;  // [D, H*M + D] [W_phi | W_V] as one row-major matrix
 };
 
 struct BwdBuffers {
@@ -53,18 +72,17 @@ constexpr int kGateTokensPerBlock = 64;
 
 // kernels_proj.hip
 hipError_t launch_transpose_weights(const Dims& d, const _Float16* W_phi, const _Float16* W_V, _Float16* wt,
-                                    hipStream_t s);
+                                    _Float16* wcat, hipStream_t s);
 hipError_t launch_proj_fwd(const Dims& d, const _Float16* X, const _Float16* gate_q, const _Float16* gate_k,
                            const ProjBuffers& p, hipStream_t s);
 hipError_t launch_proj_bwd_elem(const Dims& d, const _Float16* gate_q, const _Float16* gate_k, const ProjBuffers& p,
                                 const BwdBuffers& g, hipStream_t s);
-hipError_t launch_gate_reduce(const Dims& d, const BwdBuffers& g, const _Float16* gate_q, const _Float16* gate_k,
-                              _Float16* d_gate_q, _Float16* d_gate_k, hipStream_t s);
-hipError_t launch_dx_gemm(const Dims& d, const _Float16* W_phi, const _Float16* W_V, const BwdBuffers& g,
-                          _Float16* dX, hipStream_t s);
-hipError_t launch_dw_gemm(const Dims& d, const _Float16* X, const BwdBuffers& g, hipStream_t s);
-hipError_t launch_dw_reduce(const Dims& d, const BwdBuffers& g, _Float16* dW_phi, _Float16* dW_V, hipStream_t s);
+hipError_t launch_bwd_gemm(const Dims& d, const ProjBuffers& p, const BwdBuffers& g, const _Float16* X, _Float16* dX,
+                           hipStream_t s);
+hipError_t launch_dw_reduce(const Dims& d, const BwdBuffers& g, const _Float16* gate_q, const _Float16* gate_k,
+                            _Float16* dW_phi, _Float16* dW_V, _Float16* d_gate_q, _Float16* d_gate_k, hipStream_t s);
 int dw_splits(const Dims& d);
+__host__ __device__ int dw_tiles(const Dims& d);
 
 // kernels_attn.hip
 hipError_t launch_attn_fwd(const Dims& d, const ProjBuffers& p, _Float16* out, float* lse, hipStream_t s);

@@ -69,26 +69,6 @@ __device__ __forceinline__ bool xcd_map_lpt(int nblk, int BH, int& bh, int& blk)
 __host__ inline unsigned xcd_grid(int nblk, int BH) { return 8u * (unsigned)((BH + 7) / 8) * (unsigned)nblk; }
 
 // ============================================================ forward
-// s_waitcnt on the vector-memory counter only (gfx9 encoding: vmcnt[3:0],
-// expcnt[6:4] = 7 and lgkmcnt[11:8] = 15 mean "no wait", vmcnt[5:4] at [15:14]).
-template <int CNT>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(CNT >= 0 && CNT < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((CNT & 15) | (7 << 4) | (15 << 8) | ((CNT >> 4) << 14));
-}
-
-// 16 bytes per lane from global memory straight into LDS: lane l of the wave
-// writes LDS byte address lds_addr + 16 l (lds_addr wave-uniform). Issued as
-// inline asm so that the compiler does not order every later LDS read after
-// it: the callers wait for these loads explicitly (wait_vmcnt) before the
-// barrier that publishes a stage.
-__device__ __forceinline__ void lds_dma16(const f16* g, unsigned lds_addr) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
-               :
-               : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds_addr))
-               : "memory", "m0");
-}
-
 // XOR swizzle of the 16-byte chunk index within a 128-byte V^T tile row: the
 // 16 rows one b128 read phase touches land on distinct bank groups.
 __device__ __forceinline__ int vswz(int r) { return (r ^ (r >> 3)) & 7; }
@@ -426,30 +406,34 @@ hipError_t launch_attn_fwd(const Dims& d, const ProjBuffers& p, f16* out, float*
 }
 
 // ============================================================ backward prep
-// Backward affine blocks from lse and delta_i = dO_i . O_i (fp32), one thread per
-// (token, head), heads fastest so a wave reads whole contiguous rows; the same
-// grid zeroes the dq accumulator with contiguous stores.
+// Backward affine blocks from lse and delta_i = dO_i . O_i (fp32). DV / 8
+// consecutive lanes share one (head, token), each reading 16 bytes of dO and
+// of O; consecutive lane groups take consecutive tokens of one head, so the
+// per-row lse / tstat reads and aug writes are contiguous too, and a wave
+// reads whole 128-byte row pieces of dO and O. The partial dot products meet
+// in xor shuffles. The same grid zeroes the dq accumulator.
 template <int M, int DV>
 __global__ __launch_bounds__(256) void bwd_prep_kernel(const f16* __restrict__ grad_out, const f16* __restrict__ out,
                                                        const float* __restrict__ lse,
                                                        const float4* __restrict__ tstat, f16* __restrict__ aug,
                                                        float* __restrict__ dq, int64_t T, int N, int H, int D) {
+  constexpr int G = DV / 8;  // lanes per (head, token): 4, 8 or 16, aligned within the wave
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (idx < T * H) {
-    const int h = (int)(idx % H);
-    const int64_t t = idx / H;
-    const int b = (int)(t / N), n = (int)(t - (int64_t)b * N);
-    const int64_t bhn = (int64_t)(b * H + h) * N + n;
-    const f16* go = grad_out + t * D + h * DV;
-    const f16* oo = out + t * D + h * DV;
-    float delta = 0.f;
+  const int64_t nvec = T * (D / 8);
+  const int64_t bhn = idx / G;  // (b * H + h) * N + n
+  float delta = 0.f;
+  if (idx < nvec) {
+    const int64_t bh = bhn / N;
+    const int n = (int)(bhn - bh * N), b = (int)(bh / H), h = (int)(bh - (int64_t)b * H);
+    const int64_t off = ((int64_t)b * N + n) * D + h * DV + 8 * (int)(idx & (G - 1));
+    const f16x8 a = *reinterpret_cast<const f16x8*>(grad_out + off);
+    const f16x8 o = *reinterpret_cast<const f16x8*>(out + off);
 #pragma unroll
-    for (int c = 0; c < DV; c += 8) {
-      const f16x8 a = *reinterpret_cast<const f16x8*>(go + c);
-      const f16x8 o = *reinterpret_cast<const f16x8*>(oo + c);
+    for (int e = 0; e < 8; ++e) delta += (float)a[e] * (float)o[e];
+  }
 #pragma unroll
-      for (int e = 0; e < 8; ++e) delta += (float)a[e] * (float)o[e];
-    }
+  for (int sh = 1; sh < G; sh <<= 1) delta += __shfl_xor(delta, sh);
+  if (idx < nvec && (threadIdx.x & (G - 1)) == 0) {
     // affine blocks of the backward code rows: query side {1, 1, -(lse - b)},
     // dO side {-delta}, as fp16 hi/lo pairs
     f16 lh, ll, dh, dl;
@@ -468,7 +452,7 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(const f16* __restrict__ g
 template <int M, int DV>
 static hipError_t launch_bwd_prep_t(const Dims& d, const ProjBuffers& p, const f16* grad_out, const f16* out,
                                     const float* lse, const BwdBuffers& g, hipStream_t s) {
-  const int64_t n = d.T * d.H;
+  const int64_t n = d.T * (d.D / 8);
   hipLaunchKernelGGL((bwd_prep_kernel<M, DV>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, grad_out, out, lse,
                      p.tstat, g.aug, g.dq, d.T, d.N, d.H, d.D);
   return hipGetLastError();
@@ -516,13 +500,6 @@ __device__ __forceinline__ f16x8 frag_kmajor_swz(const f16* tile, int stride, in
   f16x4 lo = lds_read_tr4(tile + rlo * stride + col);
   f16x4 hi = lds_read_tr4(tile + rhi * stride + col);
   return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-}
-
-// s_waitcnt: vector-memory count CNT and LDS count 0 (gfx9 encoding).
-template <int CNT>
-__device__ __forceinline__ void wait_vmcnt_lgkm0() {
-  static_assert(CNT >= 0 && CNT < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((CNT & 15) | (7 << 4) | (0 << 8) | ((CNT >> 4) << 14));
 }
 
 // Key-side (KV-outer) backward. A workgroup owns 128 keys (32 per wave, kept in

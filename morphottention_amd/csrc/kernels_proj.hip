@@ -19,82 +19,113 @@
 namespace morpho {
 
 // ---------------------------------------------------------------- weights^T
+// wt = [W_phi | W_V]^T (rows in the projection's column order) for the
+// forward projection and wcat = [W_phi | W_V]
+// (one row-major matrix) for dX. 64 x 64 tiles with 16-byte loads and
+// stores: each thread reads two 8-column pieces of W rows (and writes them to
+// wcat), and writes two 8-row pieces of wt rows gathered from the LDS tile.
+// HM and D are multiples of 8, so no piece straddles W_phi / W_V or a matrix
+// edge.
 __global__ __launch_bounds__(256) void transpose_weights_kernel(const f16* __restrict__ W_phi,
                                                                 const f16* __restrict__ W_V, f16* __restrict__ wt,
-                                                                int D, int HM) {
-  __shared__ f16 tile[64][66];
+                                                                f16* __restrict__ wcat, Dims dm) {
+  __shared__ __align__(16) f16 tile[64][72];  // [d][n]
+  const int D = dm.D, HM = dm.HM;
   const int n0 = blockIdx.x * 64, d0 = blockIdx.y * 64, NC = HM + D;
-  for (int idx = threadIdx.x; idx < 64 * 64; idx += 256) {
-    const int dd = idx >> 6, nn = idx & 63;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int v = threadIdx.x + 256 * i;
+    const int dd = v >> 3, nn = (v & 7) * 8;
     const int dg = d0 + dd, ng = n0 + nn;
-    f16 x = (f16)0.f;
-    if (dg < D && ng < NC) x = ng < HM ? W_phi[(int64_t)dg * HM + ng] : W_V[(int64_t)dg * D + (ng - HM)];
-    tile[dd][nn] = x;
+    f16x8 x = {};
+    if (dg < D && ng < NC) {
+      x = ng < HM ? *reinterpret_cast<const f16x8*>(W_phi + (int64_t)dg * HM + ng)
+                  : *reinterpret_cast<const f16x8*>(W_V + (int64_t)dg * D + (ng - HM));
+      *reinterpret_cast<f16x8*>(wcat + (int64_t)dg * NC + ng) = x;
+    }
+    *reinterpret_cast<f16x8*>(&tile[dd][nn]) = x;
   }
   __syncthreads();
-  for (int idx = threadIdx.x; idx < 64 * 64; idx += 256) {
-    const int nn = idx >> 6, dd = idx & 63;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int v = threadIdx.x + 256 * i;
+    const int nn = v >> 3, dd = (v & 7) * 8;
     const int dg = d0 + dd, ng = n0 + nn;
-    if (dg < D && ng < NC) wt[(int64_t)ng * D + dg] = tile[dd][nn];
+    if (dg < D && ng < NC) {
+      f16x8 y;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) y[e] = tile[dd + e][nn];
+      *reinterpret_cast<f16x8*>(wt + (int64_t)proj_row(dm, ng) * D + dg) = y;
+    }
   }
 }
 
-hipError_t launch_transpose_weights(const Dims& d, const f16* W_phi, const f16* W_V, f16* wt, hipStream_t s) {
+hipError_t launch_transpose_weights(const Dims& d, const f16* W_phi, const f16* W_V, f16* wt, f16* wcat,
+                                    hipStream_t s) {
   dim3 grid((d.HM + d.D + 63) / 64, (d.D + 63) / 64);
-  hipLaunchKernelGGL(transpose_weights_kernel, grid, dim3(256), 0, s, W_phi, W_V, wt, d.D, d.HM);
+  hipLaunchKernelGGL(transpose_weights_kernel, grid, dim3(256), 0, s, W_phi, W_V, wt, wcat, d);
   return hipGetLastError();
 }
 
 // ---------------------------------------------------------------- projection forward
-constexpr int kStageStride = 132;  // fp32 epilogue stage row stride
+// [Z | V] = X [W_phi | W_V] on 256 x BN tiles (BN = 320 when it divides the
+// H*M + D columns, e.g. 1280 at B4 N4096 D1024 H16 m16, which makes the grid
+// exactly one round of 256 tiles; 256 otherwise). The epilogue takes the
+// tile through LDS in four 64-row slabs (the slab of wave row wm is that
+// wave row's accumulators), fp32 with row stride BN + 1 = 1 (mod 64) banks so
+// that both passes below read conflict-free.
+template <int BN>
+using ProjGemm = Gemm<256, BN, 4, true, true, 64, 2>;
+constexpr int kProjBM = 256;
 
-template <int M, int DV>
-__global__ __launch_bounds__(256) void proj_fwd_kernel(const f16* __restrict__ X, const f16* __restrict__ gate_q,
-                                                       const f16* __restrict__ gate_k, Dims d, ProjBuffers p) {
-  using ML = GemmMainloop<true, true>;
-  constexpr int kMainBytes = ML::kLdsHalves * 2;
-  constexpr int kStageBytes = 64 * kStageStride * 4;
-  __shared__ __align__(16) unsigned char smem[kMainBytes > kStageBytes ? kMainBytes : kStageBytes];
+template <int M, int DV, int BN>
+__global__ __launch_bounds__(kGemmThreads) void proj_fwd_kernel(const f16* __restrict__ X,
+                                                               const f16* __restrict__ gate_q,
+                                                               const f16* __restrict__ gate_k, Dims d, ProjBuffers p) {
+  using G = ProjGemm<BN>;
+  constexpr int SS = BN + 1;  // stage row stride (floats)
+  static_assert(64 * SS * 4 <= G::kLdsBytes, "epilogue slab must fit the main loop's LDS");
+  __shared__ __align__(16) char smem[G::kLdsBytes];
   constexpr int CW = 3 * M + 8;
 
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = w >> 1, wn = w & 1;
+  const int wm = w / G::WN, wn = w % G::WN;
   const int NC = d.HM + d.D;
   const int T = (int)d.T;
   int tm, tn;
-  if (!gemm_tile_map((T + kGemmBM - 1) / kGemmBM, (NC + kGemmBN - 1) / kGemmBN, tm, tn)) return;
-  const int n0 = tn * kGemmBN, m0 = tm * kGemmBM;
-  OperandDesc A{X, d.D, nullptr, 0, INT_MAX};
-  OperandDesc B{p.wt, d.D, nullptr, 0, INT_MAX};
-  f32x16 acc[2][2];
-  ML::run(A, B, T, NC, m0, n0, 0, d.D, reinterpret_cast<f16*>(smem), acc);
+  if (!gemm_tile_map(blockIdx.x, (T + kProjBM - 1) / kProjBM, (NC + BN - 1) / BN, tm, tn)) return;
+  const int n0 = tn * BN, m0 = tm * kProjBM;
+  f32x16 acc[G::FI][G::FJ];
+  G::run(X, d.D, p.wt, d.D, T, NC, m0, n0, 0, d.D, smem, acc);
 
   float* stage = reinterpret_cast<float*>(smem);
   const float c1 = 2.0f * d.scale * kLog2e;
-  for (int pass = 0; pass < 2; ++pass) {
-    __syncthreads();
-    if (wm == pass) {
+  static_assert(G::WTM == 64, "one wave row per 64-row slab");
+  for (int slab = 0; slab < kProjBM / 64; ++slab) {
+    if (slab > 0) __syncthreads();  // the previous slab has been consumed
+    if (wm == slab) {
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < G::FI; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < G::FJ; ++j)
 #pragma unroll
           for (int r = 0; r < 16; ++r)
-            stage[(32 * i + acc_row(r, lane)) * kStageStride + 64 * wn + 32 * j + (lane & 31)] = acc[i][j][r];
+            stage[(32 * i + acc_row(r, lane)) * SS + G::WTN * wn + 32 * j + (lane & 31)] = acc[i][j][r];
     }
     __syncthreads();
-    const int row0 = m0 + 64 * pass;
-    // soft-hypercube codes: one (token, head) per item
-    constexpr int kHeadsPerTile = kGemmBN / M;
-    for (int idx = tid; idx < 64 * kHeadsPerTile; idx += 256) {
+    const int row0 = m0 + 64 * slab;
+    // soft-hypercube codes: one (token, head) per item (a head's M columns
+    // are contiguous in both column orders)
+    constexpr int kHeadsPerTile = BN / M;
+    for (int idx = tid; idx < 64 * kHeadsPerTile; idx += kGemmThreads) {
       const int hh = idx / 64, r = idx % 64;
-      const int col0 = n0 + hh * M;
+      const int col0 = proj_col(d, tn, hh * M);
       const int t = row0 + r;
       if (col0 >= d.HM || t >= T) continue;
       const int h = col0 / M;
       const int b = t / d.N, n = t - b * d.N;
       const int64_t bhn = (int64_t)(b * d.H + h) * d.N + n;
-      const float* z = stage + r * kStageStride + hh * M;
+      const float* z = stage + r * SS + hh * M;
       f16* qrow = p.qa + bhn * CW;
       f16* krow = p.ka + bhn * CW;
       float sumb = 0.f, tii = 0.f, U = 0.f;
@@ -141,22 +172,23 @@ __global__ __launch_bounds__(256) void proj_fwd_kernel(const f16* __restrict__ X
     }
     // values, transposed: vt[bh][dd][n] = V_hi, vt[bh][DV + dd][n] = V_lo.
     // One item = one column x 8 consecutive tokens; 8 neighbouring threads
-    // cover 64 consecutive tokens of a column (128 contiguous bytes).
-    if (n0 + kGemmBN > d.HM) {  // the tile has value columns (uniform)
+    // cover the slab's 64 consecutive tokens of a column (128 contiguous
+    // bytes), a wave 8 columns.
+    if (proj_col(d, tn, BN - 1) >= d.HM) {  // the tile has value columns (uniform)
       const bool vec = d.N % 8 == 0;
-      for (int idx = tid; idx < 8 * kGemmBN; idx += 256) {
+      for (int idx = tid; idx < 8 * BN; idx += kGemmThreads) {
         const int rg = idx & 7, cc = idx >> 3;
-        const int col = n0 + cc, tb = row0 + 8 * rg;
-        if (col < d.HM || col >= NC || tb >= T) continue;
+        const int col = proj_col(d, tn, cc), tb = row0 + 8 * rg;
+        if (col < d.HM || n0 + cc >= NC || tb >= T) continue;
         const int vcol = col - d.HM, h = vcol / DV, dd = vcol % DV;
-        const float* src = stage + 8 * rg * kStageStride + cc;
+        const float* src = stage + 8 * rg * SS + cc;
         if (vec) {
           // N % 8 == 0 and tb % 8 == 0: the 8 tokens share one batch row
           const int b = tb / d.N, n = tb - b * d.N;
           f16x8 vh, vl;
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
-            const float x = src[e * kStageStride];
+            const float x = src[e * SS];
             vh[e] = (f16)x;
             vl[e] = (f16)(x - (float)vh[e]);
           }
@@ -172,7 +204,7 @@ __global__ __launch_bounds__(256) void proj_fwd_kernel(const f16* __restrict__ X
         } else {
           for (int e = 0; e < 8 && tb + e < T; ++e) {
             const int t = tb + e, b = t / d.N, n = t - b * d.N;
-            const float x = src[e * kStageStride];
+            const float x = src[e * SS];
             const f16 vh = (f16)x, vl = (f16)(x - (float)vh);
             f16* dst = p.vt + ((int64_t)(b * d.H + h) * 2 * DV + dd) * d.NP + n;
             const int64_t lo = (int64_t)DV * d.NP;
@@ -193,8 +225,14 @@ __global__ __launch_bounds__(256) void proj_fwd_kernel(const f16* __restrict__ X
 template <int M, int DV>
 static hipError_t launch_proj_fwd_t(const Dims& d, const f16* X, const f16* gq, const f16* gk, const ProjBuffers& p,
                                     hipStream_t s) {
-  const dim3 grid(gemm_tile_grid((int)((d.T + kGemmBM - 1) / kGemmBM), (d.HM + d.D + kGemmBN - 1) / kGemmBN));
-  hipLaunchKernelGGL((proj_fwd_kernel<M, DV>), grid, dim3(256), 0, s, X, gq, gk, d, p);
+  const int NC = d.HM + d.D, nrows = (int)((d.T + kProjBM - 1) / kProjBM);
+  if (d.PBN == 320) {
+    hipLaunchKernelGGL((proj_fwd_kernel<M, DV, 320>), dim3(gemm_tile_grid(nrows, NC / 320)), dim3(kGemmThreads), 0,
+                       s, X, gq, gk, d, p);
+  } else {
+    hipLaunchKernelGGL((proj_fwd_kernel<M, DV, 256>), dim3(gemm_tile_grid(nrows, (NC + 255) / 256)),
+                       dim3(kGemmThreads), 0, s, X, gq, gk, d, p);
+  }
   return hipGetLastError();
 }
 
@@ -218,31 +256,63 @@ hipError_t launch_proj_fwd(const Dims& d, const f16* X, const f16* gq, const f16
 // (both use sum_j dS_ij = 0). dL/dG is taken from the key-side sums only, whose
 // terms share the same rounded dS, so its cancellation stays exact; then
 // d gate_q = dL/dG gate_k and d gate_k = dL/dG gate_q.
-// One thread per projection column, kGateTokensPerBlock tokens per block.
+// A block covers kGateTokensPerBlock tokens and 256 projection columns. Each
+// thread owns 8 consecutive columns (one head) and every 8th token of the
+// block, so all loads and stores are 16-byte vectors: a wave covers 32
+// column groups of 2 tokens, i.e. whole 512-byte dZ rows and, per head, 2
+// consecutive rows of dq / dk. The per-thread gate sums meet in LDS in a
+// fixed order.
 __global__ __launch_bounds__(256) void proj_bwd_elem_kernel(const f16* __restrict__ gate_q,
                                                             const f16* __restrict__ gate_k, Dims d, ProjBuffers p,
                                                             BwdBuffers g) {
-  const int col = blockIdx.y * 256 + threadIdx.x;
-  if (col >= d.HM) return;
+  __shared__ float red[8][257];
+  const int c8 = threadIdx.x & 31, sub = threadIdx.x >> 5;
+  const int col = blockIdx.y * 256 + 8 * c8;  // first of this thread's 8 columns
+  const bool active = col < d.HM;
   const int h = col / d.M, c = col - h * d.M;
-  const float sG = d.scale * (float)gate_q[col] * (float)gate_k[col];
   const int NC = d.HM + d.D;
-  const int64_t t0 = (int64_t)blockIdx.x * kGateTokensPerBlock;
-  const int64_t t1 = t0 + kGateTokensPerBlock < d.T ? t0 + kGateTokensPerBlock : d.T;
-  float sg = 0.f;
-  for (int64_t t = t0; t < t1; ++t) {
-    const int b = (int)(t / d.N), n = (int)(t - (int64_t)b * d.N);
-    const int64_t bhn = (int64_t)(b * d.H + h) * d.N + n;
-    const f16* qrow = p.qa + bhn * d.CW;
-    const float phi = (float)qrow[c] + (float)qrow[d.M + 8 + c];
-    const float dq = g.dq[bhn * d.M + c];
-    const float dk = g.dk[bhn * d.M + c];
-    const float dcb = g.dcb[bhn];
-    const float dphi = sG * (2.f * (dq + dk) - dcb);
-    g.dzv[t * NC + col] = (f16)(dphi * phi * (1.f - phi));
-    sg += phi * (2.f * dk - dcb);
+  float sg[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (active) {
+    float sG[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sG[e] = d.scale * (float)gate_q[col + e] * (float)gate_k[col + e];
+    const int64_t t0 = (int64_t)blockIdx.x * kGateTokensPerBlock;
+#pragma unroll 2
+    for (int k = 0; k < kGateTokensPerBlock / 8; ++k) {
+      const int64_t t = t0 + sub + 8 * k;
+      if (t >= d.T) break;
+      const int b = (int)(t / d.N), n = (int)(t - (int64_t)b * d.N);
+      const int64_t bhn = (int64_t)(b * d.H + h) * d.N + n;
+      const f16* qrow = p.qa + bhn * d.CW;
+      const f16x8 ph = *reinterpret_cast<const f16x8*>(qrow + c);
+      const f16x8 pl = *reinterpret_cast<const f16x8*>(qrow + d.M + 8 + c);
+      const float4* dqp = reinterpret_cast<const float4*>(g.dq + bhn * d.M + c);
+      const float4* dkp = reinterpret_cast<const float4*>(g.dk + bhn * d.M + c);
+      const float4 q0 = dqp[0], q1 = dqp[1], k0 = dkp[0], k1 = dkp[1];
+      const float dq[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+      const float dk[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+      const float dcb = g.dcb[bhn];
+      f16x8 dz;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float phi = (float)ph[e] + (float)pl[e];
+        const float dphi = sG[e] * (2.f * (dq[e] + dk[e]) - dcb);
+        dz[e] = (f16)(dphi * phi * (1.f - phi));
+        sg[e] += phi * (2.f * dk[e] - dcb);
+      }
+      *reinterpret_cast<f16x8*>(g.dzv + t * NC + col) = dz;
+    }
   }
-  g.gpart[(int64_t)blockIdx.x * d.HM + col] = sg;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) red[sub][8 * c8 + e] = sg[e];
+  __syncthreads();
+  const int cc = blockIdx.y * 256 + threadIdx.x;
+  if (cc < d.HM) {
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s += red[i][threadIdx.x];
+    g.gpart[(int64_t)blockIdx.x * d.HM + cc] = s;
+  }
 }
 
 hipError_t launch_proj_bwd_elem(const Dims& d, const f16* gq, const f16* gk, const ProjBuffers& p,
@@ -252,133 +322,153 @@ hipError_t launch_proj_bwd_elem(const Dims& d, const f16* gq, const f16* gk, con
   return hipGetLastError();
 }
 
-__global__ __launch_bounds__(256) void gate_reduce_kernel(const float* __restrict__ gpart, int nblk, int HM,
-                                                          float scale, const f16* __restrict__ gate_q,
-                                                          const f16* __restrict__ gate_k, f16* __restrict__ d_gate_q,
-                                                          f16* __restrict__ d_gate_k) {
-  // 64 columns x 4 row groups per block; fixed summation order (deterministic)
-  __shared__ float part[4][64];
-  const int cl = threadIdx.x & 63, grp = threadIdx.x >> 6;
-  const int col = blockIdx.x * 64 + cl;
-  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
-  if (col < HM) {
-    int i = grp;
-    for (; i + 12 < nblk; i += 16) {
-      s0 += gpart[(int64_t)i * HM + col];
-      s1 += gpart[(int64_t)(i + 4) * HM + col];
-      s2 += gpart[(int64_t)(i + 8) * HM + col];
-      s3 += gpart[(int64_t)(i + 12) * HM + col];
-    }
-    for (; i < nblk; i += 4) s0 += gpart[(int64_t)i * HM + col];
-  }
-  part[grp][cl] = (s0 + s1) + (s2 + s3);
-  __syncthreads();
-  if (grp == 0 && col < HM) {
-    const float dG = scale * ((part[0][cl] + part[1][cl]) + (part[2][cl] + part[3][cl]));
-    d_gate_q[col] = (f16)(dG * (float)gate_k[col]);
-    d_gate_k[col] = (f16)(dG * (float)gate_q[col]);
-  }
-}
+// ---------------------------------------------------------------- backward GEMMs
+// One launch computes
+//   dX = [dZ | dV] [W_phi | W_V]^T                    (dX tiles)
+//   [dW_phi | dW_V] = X^T [dZ | dV]                   (dW tiles, split-K over tokens)
+// Workgroup ids: [0, n_dw) dW, then [n_dw, n_dw + n_dx) dX; the dW tiles,
+// which run longer, are dispatched first. Split z of dW tile tl covers tokens
+// [z kchunk, (z + 1) kchunk), runs on XCD z % 8 (ids are dispatched
+// round-robin over the 8 XCDs, so the tiles of one split share their X and
+// dZ|dV panels in one L2) and stores an fp32 partial; dw_reduce sums the
+// partials in split order.
+using DxGemm = Gemm<256, 256, 4, true, true, 64, 2>;    // A = dZ|dV [T][NC], B = wcat = [W_phi | W_V] [D][NC]
+using DwGemm = Gemm<256, 256, 4, false, false, 64, 2>;  // A = X (k-major) [T][D], B = dZ|dV (k-major) [T][NC]
+constexpr int kDxBM = 256, kDxBN = 256, kDwBM = 256, kDwBN = 256;
+constexpr int kBwdLds = DxGemm::kLdsBytes > DwGemm::kLdsBytes ? DxGemm::kLdsBytes : DwGemm::kLdsBytes;
+constexpr int kDxStageStride = kDxBN + 8;  // halves: one 64-row slab of fp16 dX for 16-byte stores
+static_assert(64 * kDxStageStride * 2 <= kBwdLds, "dX slab must fit the main loop's LDS");
 
-hipError_t launch_gate_reduce(const Dims& d, const BwdBuffers& g, const f16* gq, const f16* gk, f16* dgq, f16* dgk,
-                              hipStream_t s) {
-  const int nblk = (int)((d.T + kGateTokensPerBlock - 1) / kGateTokensPerBlock);
-  hipLaunchKernelGGL(gate_reduce_kernel, dim3((d.HM + 63) / 64), dim3(256), 0, s, g.gpart, nblk, d.HM, d.scale, gq,
-                     gk, dgq, dgk);
-  return hipGetLastError();
-}
-
-// ---------------------------------------------------------------- dX = [dZ | dV] [W_phi | W_V]^T
-__global__ __launch_bounds__(256) void dx_gemm_kernel(const f16* __restrict__ W_phi, const f16* __restrict__ W_V,
-                                                      const f16* __restrict__ dzv, f16* __restrict__ dX, Dims d) {
-  using ML = GemmMainloop<true, true>;
-  __shared__ __align__(16) f16 smem[ML::kLdsHalves];
-  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = w >> 1, wn = w & 1;
-  const int T = (int)d.T, NC = d.HM + d.D;
-  int tm, tn;
-  if (!gemm_tile_map((T + kGemmBM - 1) / kGemmBM, (d.D + kGemmBN - 1) / kGemmBN, tm, tn)) return;
-  const int n0 = tn * kGemmBN, m0 = tm * kGemmBM;
-  OperandDesc A{dzv, NC, nullptr, 0, INT_MAX};
-  OperandDesc B{W_phi, d.HM, W_V, d.D, d.HM};
-  f32x16 acc[2][2];
-  ML::run(A, B, T, d.D, m0, n0, 0, NC, smem, acc);
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int col = n0 + 64 * wn + 32 * j + (lane & 31);
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = m0 + 64 * wm + 32 * i + acc_row(r, lane);
-        if (row < T && col < d.D) dX[(int64_t)row * d.D + col] = (f16)acc[i][j][r];
-      }
-    }
-}
-
-hipError_t launch_dx_gemm(const Dims& d, const f16* W_phi, const f16* W_V, const BwdBuffers& g, f16* dX,
-                          hipStream_t s) {
-  const dim3 grid(gemm_tile_grid((int)((d.T + kGemmBM - 1) / kGemmBM), (d.D + kGemmBN - 1) / kGemmBN));
-  hipLaunchKernelGGL(dx_gemm_kernel, grid, dim3(256), 0, s, W_phi, W_V, g.dzv, dX, d);
-  return hipGetLastError();
-}
-
-// ---------------------------------------------------------------- [dW_phi | dW_V] = X^T [dZ | dV]
-// Split-K over tokens: one K slice per XCD (workgroup id % 8), so the tiles
-// that share a slice's A and B panels run on one L2 and stream them together.
+__host__ __device__ int dw_tiles(const Dims& d) { return ((d.D + kDwBM - 1) / kDwBM) * ((d.HM + d.D + kDwBN - 1) / kDwBN); }
+// Splits of the token (k) range: about one round of the 256 CUs for the dW
+// tiles, at least 256 tokens per split.
 int dw_splits(const Dims& d) {
-  const int kmax = (int)((d.T + 255) / 256);  // keep >= 256 tokens per split
-  return kmax < 8 ? kmax : 8;
+  const int by_cus = 256 / dw_tiles(d), by_k = (int)((d.T + 255) / 256);
+  const int s = by_cus < by_k ? by_cus : by_k;
+  return s < 1 ? 1 : s;
 }
 
-__global__ __launch_bounds__(256) void dw_gemm_kernel(const f16* __restrict__ X, const f16* __restrict__ dzv,
-                                                      float* __restrict__ wpart, Dims d, int kchunk, int nsplit) {
-  using ML = GemmMainloop<false, false>;
-  __shared__ __align__(16) f16 smem[ML::kLdsHalves];
+struct BwdGemmArgs {
+  const f16* X;
+  const f16* wcat;
+  f16* dX;
+  int n_dw, n_dx, kchunk;
+};
+
+__global__ __launch_bounds__(kGemmThreads) void bwd_gemm_kernel(Dims d, BwdBuffers g, BwdGemmArgs a) {
+  __shared__ __align__(16) char smem[kBwdLds];
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = w >> 1, wn = w & 1;
+  const int wm = w / DxGemm::WN, wn = w % DxGemm::WN;  // same wave grid for dX and dW
+  static_assert(DxGemm::WN == DwGemm::WN && DxGemm::WTM == 64, "shared wave grid, 64-row wave tiles");
   const int NC = d.HM + d.D;
-  // id = 8 * slot + xcd; split = xcd (+ 8 per extra round), tile = slot within the split
-  const int ntn = (NC + kGemmBN - 1) / kGemmBN, ntm = (d.D + kGemmBM - 1) / kGemmBM;
-  const int id = blockIdx.x, xcd = id & 7, slot = id >> 3;
-  const int tile = slot % (ntn * ntm), z = xcd + 8 * (slot / (ntn * ntm));
-  if (z >= nsplit) return;
-  const int n0 = (tile % ntn) * kGemmBN, m0 = (tile / ntn) * kGemmBM;
   const int T = (int)d.T;
-  const int kbeg = z * kchunk;
-  const int kend = kbeg + kchunk < T ? kbeg + kchunk : T;
-  OperandDesc A{X, d.D, nullptr, 0, INT_MAX};
-  OperandDesc B{dzv, NC, nullptr, 0, INT_MAX};
-  f32x16 acc[2][2];
-  ML::run(A, B, d.D, NC, m0, n0, kbeg, kend, smem, acc);
-  float* out = wpart + (int64_t)z * d.D * NC;
+  const int id = blockIdx.x;
+
+  if (id >= a.n_dw) {
+    // ---- dX tile
+    int tm, tn;
+    if (!gemm_tile_map(id - a.n_dw, (T + kDxBM - 1) / kDxBM, (d.D + kDxBN - 1) / kDxBN, tm, tn)) return;
+    const int m0 = tm * kDxBM, n0 = tn * kDxBN;
+    f32x16 acc[DxGemm::FI][DxGemm::FJ];
+    DxGemm::run(g.dzv, NC, a.wcat, NC, T, d.D, m0, n0, 0, NC, smem, acc);
+    // fp16 through LDS in 64-row slabs (slab = wave row), then 16-byte row stores
+    f16* st = reinterpret_cast<f16*>(smem);
+    for (int slab = 0; slab < kDxBM / 64; ++slab) {
+      if (slab > 0) __syncthreads();
+      if (wm == slab) {
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < DxGemm::FI; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int col = n0 + 64 * wn + 32 * j + (lane & 31);
+          for (int j = 0; j < DxGemm::FJ; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+              st[(32 * i + acc_row(r, lane)) * kDxStageStride + DxGemm::WTN * wn + 32 * j + (lane & 31)] =
+                  (f16)acc[i][j][r];
+      }
+      __syncthreads();
+      for (int q = tid; q < 64 * (kDxBN / 8); q += kGemmThreads) {
+        const int r = q / (kDxBN / 8), c = 8 * (q % (kDxBN / 8));
+        const int row = m0 + 64 * slab + r, col = n0 + c;
+        if (row < T && col < d.D)
+          *reinterpret_cast<f16x8*>(a.dX + (int64_t)row * d.D + col) =
+              *reinterpret_cast<const f16x8*>(st + r * kDxStageStride + c);
+      }
+    }
+    return;
+  }
+
+  // ---- dW split-K tile
+  const int ntn = (NC + kDwBN - 1) / kDwBN, tiles = dw_tiles(d);
+  const int xcd = id & 7, slot = id >> 3;
+  const int tl = slot % tiles, z = xcd + 8 * (slot / tiles);
+  if (z >= g.splits) return;
+  const int m0 = (tl / ntn) * kDwBM, n0 = (tl % ntn) * kDwBN;
+  const int kbeg = min(z * a.kchunk, T), kend = min(kbeg + a.kchunk, T);
+  f32x16 acc[DwGemm::FI][DwGemm::FJ];
+  DwGemm::run(a.X, d.D, g.dzv, NC, d.D, NC, m0, n0, kbeg, kend, smem, acc);
+  const int64_t tot = (int64_t)d.D * NC;
+  float* part = g.wpart + (int64_t)z * tot;
+#pragma unroll
+  for (int i = 0; i < DwGemm::FI; ++i)
+#pragma unroll
+    for (int j = 0; j < DwGemm::FJ; ++j) {
+      const int col = n0 + DwGemm::WTN * wn + 32 * j + (lane & 31);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int row = m0 + 64 * wm + 32 * i + acc_row(r, lane);
-        if (row < d.D && col < NC) out[(int64_t)row * NC + col] = acc[i][j][r];
+        const int row = m0 + DwGemm::WTM * wm + 32 * i + acc_row(r, lane);
+        if (row < d.D && col < NC) part[(int64_t)row * NC + col] = acc[i][j][r];
       }
     }
 }
 
-hipError_t launch_dw_gemm(const Dims& d, const f16* X, const BwdBuffers& g, hipStream_t s) {
-  const int S = g.splits;
-  const int T = (int)d.T;
-  int kchunk = (T + S - 1) / S;
-  kchunk = (kchunk + kGemmBK - 1) / kGemmBK * kGemmBK;
-  const int tiles = ((d.HM + d.D + kGemmBN - 1) / kGemmBN) * ((d.D + kGemmBM - 1) / kGemmBM);
-  const int rounds = (S + 7) / 8;
-  dim3 grid(8u * (unsigned)tiles * (unsigned)rounds);
-  hipLaunchKernelGGL(dw_gemm_kernel, grid, dim3(256), 0, s, X, g.dzv, g.wpart, d, kchunk, S);
+hipError_t launch_bwd_gemm(const Dims& d, const ProjBuffers& p, const BwdBuffers& g, const f16* X, f16* dX,
+                           hipStream_t s) {
+  BwdGemmArgs a;
+  a.X = X; a.wcat = p.wcat; a.dX = dX;
+  const int S = g.splits, T = (int)d.T;
+  a.kchunk = ((T + S - 1) / S + DwGemm::kBK - 1) / DwGemm::kBK * DwGemm::kBK;
+  a.n_dw = 8 * dw_tiles(d) * ((S + 7) / 8);
+  a.n_dx = (int)gemm_tile_grid((T + kDxBM - 1) / kDxBM, (d.D + kDxBN - 1) / kDxBN);
+  hipLaunchKernelGGL(bwd_gemm_kernel, dim3((unsigned)(a.n_dw + a.n_dx)), dim3(kGemmThreads), 0, s, d, g, a);
   return hipGetLastError();
 }
 
+// Finalisation of the weight and gate gradients, one launch. Blocks
+// [0, nw) sum the split-K partials of [dW_phi | dW_V] (4 consecutive outputs
+// per thread, splits in order); blocks [nw, nw + ceil(HM / 16)) sum the
+// per-block gate partials: 16 columns x 16 row groups per block, group g
+// summing rows g, g + 16, ... with two accumulators, the groups then combined
+// in a fixed order. Both orders are fixed, so results are deterministic.
 __global__ __launch_bounds__(256) void dw_reduce_kernel(const float* __restrict__ wpart, int splits, int D, int HM,
-                                                        f16* __restrict__ dW_phi, f16* __restrict__ dW_V) {
+                                                        f16* __restrict__ dW_phi, f16* __restrict__ dW_V, int nw,
+                                                        const float* __restrict__ gpart, int nblk, float scale,
+                                                        const f16* __restrict__ gate_q, const f16* __restrict__ gate_k,
+                                                        f16* __restrict__ d_gate_q, f16* __restrict__ d_gate_k) {
+  __shared__ float part[16][17];
+  if ((int)blockIdx.x >= nw) {
+    const int cl = threadIdx.x & 15, grp = threadIdx.x >> 4;
+    const int col = ((int)blockIdx.x - nw) * 16 + cl;
+    float s0 = 0.f, s1 = 0.f;
+    if (col < HM) {
+      int i = grp;
+      for (; i + 16 < nblk; i += 32) {
+        s0 += gpart[(int64_t)i * HM + col];
+        s1 += gpart[(int64_t)(i + 16) * HM + col];
+      }
+      if (i < nblk) s0 += gpart[(int64_t)i * HM + col];
+    }
+    part[grp][cl] = s0 + s1;
+    __syncthreads();
+    if (grp == 0 && col < HM) {
+      float t = 0.f;
+#pragma unroll
+      for (int g2 = 0; g2 < 16; ++g2) t += part[g2][cl];
+      const float dG = scale * t;
+      d_gate_q[col] = (f16)(dG * (float)gate_k[col]);
+      d_gate_k[col] = (f16)(dG * (float)gate_q[col]);
+    }
+    return;
+  }
   const int NC = HM + D;
   const int64_t total = (int64_t)D * NC;
   const int64_t idx = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
@@ -391,13 +481,17 @@ __global__ __launch_bounds__(256) void dw_reduce_kernel(const float* __restrict_
   const int row = (int)(idx / NC), col = (int)(idx - (int64_t)row * NC);
   // 4 consecutive columns never straddle HM (HM and NC are multiples of 16)
   f16* dst = col < HM ? dW_phi + (int64_t)row * HM + col : dW_V + (int64_t)row * D + (col - HM);
-  dst[0] = (f16)s.x; dst[1] = (f16)s.y; dst[2] = (f16)s.z; dst[3] = (f16)s.w;
+  *reinterpret_cast<f16x4*>(dst) = f16x4{(f16)s.x, (f16)s.y, (f16)s.z, (f16)s.w};
 }
 
-hipError_t launch_dw_reduce(const Dims& d, const BwdBuffers& g, f16* dW_phi, f16* dW_V, hipStream_t s) {
+hipError_t launch_dw_reduce(const Dims& d, const BwdBuffers& g, const f16* gq, const f16* gk, f16* dW_phi, f16* dW_V,
+                            f16* dgq, f16* dgk, hipStream_t s) {
   const int64_t total = (int64_t)d.D * (d.HM + d.D);
-  const unsigned blocks = (unsigned)((total / 4 + 255) / 256);
-  hipLaunchKernelGGL(dw_reduce_kernel, dim3(blocks), dim3(256), 0, s, g.wpart, g.splits, d.D, d.HM, dW_phi, dW_V);
+  const int nw = (int)((total / 4 + 255) / 256);
+  const int ngate = (d.HM + 15) / 16;
+  const int nblk = (int)((d.T + kGateTokensPerBlock - 1) / kGateTokensPerBlock);
+  hipLaunchKernelGGL(dw_reduce_kernel, dim3((unsigned)(nw + ngate)), dim3(256), 0, s, g.wpart, g.splits, d.D, d.HM,
+                     dW_phi, dW_V, nw, g.gpart, nblk, d.scale, gq, gk, dgq, dgk);
   return hipGetLastError();
 }
 
