@@ -126,7 +126,7 @@ size_t bwd_bytes(const Dims& d) {
   const size_t bhn = (size_t)d.B * d.H * d.N;
   const size_t nblk = (size_t)((d.T + kGateTokensPerBlock - 1) / kGateTokensPerBlock);
   size_t s = 0;
-  s += align_up(bhn * 32);                             // aug
+  s += align_up(bhn * 16);                             // aug
   s += align_up(bhn * d.M * 4);                        // dq
   s += align_up(bhn * d.M * 4);                        // dk
   s += align_up(bhn * 4);                              // dcb
@@ -141,7 +141,7 @@ BwdBuffers carve_bwd(void* base, const Dims& d) {
   const size_t nblk = (size_t)((d.T + kGateTokensPerBlock - 1) / kGateTokensPerBlock);
   char* p = static_cast<char*>(base);
   BwdBuffers g;
-  g.aug = reinterpret_cast<_Float16*>(p); p += align_up(bhn * 32);
+  g.aug = reinterpret_cast<_Float16*>(p); p += align_up(bhn * 16);
   g.dq = reinterpret_cast<float*>(p); p += align_up(bhn * d.M * 4);
   g.dk = reinterpret_cast<float*>(p); p += align_up(bhn * d.M * 4);
   g.dcb = reinterpret_cast<float*>(p); p += align_up(bhn * 4);
@@ -287,7 +287,9 @@ MORPHO_EXPORT int morpho_backward(const void* grad_out, const void* X, const voi
   }
   const BwdBuffers g = carve_bwd(ws, d);
   const auto* go = static_cast<const _Float16*>(grad_out);
-  MORPHO_LAUNCH("bwd_prep", launch_bwd_prep(d, p, go, static_cast<const _Float16*>(out), lse, g, s));
+  // the forward leaves the backward's query affine block in its code rows; a
+  // projection computed here still holds its own
+  MORPHO_LAUNCH("bwd_prep", launch_bwd_prep(d, p, go, static_cast<const _Float16*>(out), lse, g, have_fwd ? 0 : 1, s));
   MORPHO_LAUNCH("attn_bwd", launch_attn_bwd(d, p, go, g, s));
   MORPHO_LAUNCH("proj_bwd_elem", launch_proj_bwd_elem(d, static_cast<const _Float16*>(gate_q),
                                                       static_cast<const _Float16*>(gate_k), p, g, s));

@@ -125,6 +125,15 @@ __device__ __forceinline__ void lds_dma16(const f16* g, unsigned lds_addr) {
                : "memory", "m0");
 }
 
+// DMA of one 16-byte piece per lane from sbase + voff (32-bit unsigned lane
+// offset, 64-bit wave-uniform base) to LDS byte address lds_addr + 16 lane.
+__device__ __forceinline__ void lds_dma16_so(const void* sbase, unsigned voff, unsigned lds_addr) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(voff), "s"(sbase), "s"(__builtin_amdgcn_readfirstlane(lds_addr))
+               : "memory", "m0");
+}
+
 // s_waitcnt: vector-memory count CNT and LDS count 0 (gfx9 encoding).
 template <int CNT>
 __device__ __forceinline__ void wait_vmcnt_lgkm0() {

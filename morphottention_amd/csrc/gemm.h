@@ -33,15 +33,6 @@ namespace morpho {
 constexpr int kGemmWaves = 8;
 constexpr int kGemmThreads = 64 * kGemmWaves;
 
-// DMA of one 16-byte piece per lane from sbase + voff (32-bit unsigned lane
-// offset, 64-bit wave-uniform base) to LDS byte address lds_addr + 16 lane.
-__device__ __forceinline__ void lds_dma16_so(const void* sbase, unsigned voff, unsigned lds_addr) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
-               :
-               : "v"(voff), "s"(sbase), "s"(__builtin_amdgcn_readfirstlane(lds_addr))
-               : "memory", "m0");
-}
-
 template <bool KC, int ROWS, int BK>
 struct OpTile {
   static_assert(BK == 32 || BK == 64, "k-step of 32 or 64");

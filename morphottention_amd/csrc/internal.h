@@ -40,6 +40,8 @@ __host__ __device__ inline int proj_row(const Dims& d, int c) {
 // Code rows carry each code as an fp16 hi/lo pair laid out so that one MFMA
 // contraction over CW columns yields (to ~2^-22) the exact base-2 exponent:
 //   query row  [phi_hi | 1, 1, -R_hi, -R_lo, 0 x4 | phi_lo | phi_hi]
+//              (after the forward: [.. | 1, 1, -(lse - b) hi, lo, 0 x4 | ..],
+//               the backward's row reference)
 //   key row    [kc_hi  | b_hi, b_lo, 1, 1, 0 x4   | kc_hi  | kc_lo ]
 // (the 8-wide affine block sits right after the first M codes so that a
 // 32-row transposed read of the query row starting at column 32*floor(M/32)
@@ -58,7 +60,7 @@ struct ProjBuffers {
 };
 
 struct BwdBuffers {
-  _Float16* aug;   // [B*H, N, 16] per query: {1, 1, -(lse - b) hi, lo, 0 x4} then {-delta hi, lo, 0 x6}
+  _Float16* aug;   // [B*H, N, 8] per query: the dO rows' affine block {-delta hi, lo, 0 x6}
   float* dq;       // [B*H, N, M] sum_j dS_ij phi_j (query side), fp32 atomics
   float* dk;       // [B*H, N, M] sum_i dS_ij phi_i (key side)
   float* dcb;      // [B*H, N]    sum_i dS_ij
@@ -87,7 +89,7 @@ __host__ __device__ int dw_tiles(const Dims& d);
 // kernels_attn.hip
 hipError_t launch_attn_fwd(const Dims& d, const ProjBuffers& p, _Float16* out, float* lse, hipStream_t s);
 hipError_t launch_bwd_prep(const Dims& d, const ProjBuffers& p, const _Float16* grad_out, const _Float16* out,
-                           const float* lse, const BwdBuffers& g, hipStream_t s);
+                           const float* lse, const BwdBuffers& g, int write_q, hipStream_t s);
 hipError_t launch_attn_bwd(const Dims& d, const ProjBuffers& p, const _Float16* grad_out, const BwdBuffers& g,
                            hipStream_t s);
 

@@ -86,13 +86,18 @@ struct FwdCfg {
   // A stage holds one key tile [KT][CW] (rows in swap23 order within each 32,
   // unpadded: CW = 8 (mod 16) halves keeps b128 reads conflict-free) and one
   // V^T tile [2 DV][KT] (V_hi^T rows, then V_lo^T rows, chunk-swizzled), both
-  // filled by 1 KiB DMA chunks spread evenly over the waves.
+  // filled by 1 KiB DMA chunks: each wave issues NKW key chunks (the key slots
+  // are padded to a multiple of the wave count; padding slots repeat the last
+  // chunk) and NVW V^T chunks, so every wave's i-th chunk kind is fixed.
   static constexpr int KCH = CW / 8;      // key tile chunks
   static constexpr int VCH = DV / 4;      // V^T tile chunks
-  static constexpr int NPW = (KCH + VCH + WAVES - 1) / WAVES;  // chunks per wave per tile
-  static constexpr int NPW_K = (KCH + WAVES - 1) / WAVES;      // key-only tiles (exact-max pass)
-  static constexpr int VOFF = KCH * 512;  // V^T offset in a stage (halves)
-  static constexpr int STAGE = WAVES * NPW * 512;              // halves, incl. padding chunks
+  static constexpr int NKW = (KCH + WAVES - 1) / WAVES;  // key chunks per wave
+  static constexpr int NVW = VCH / WAVES;                // V^T chunks per wave
+  static_assert(VCH % WAVES == 0, "V^T chunks must split evenly over the waves");
+  static constexpr int NPW = NKW + NVW;   // chunks per wave per tile
+  static constexpr int NPW_K = NKW;       // key-only tiles (exact-max pass)
+  static constexpr int VOFF = NKW * WAVES * 512;  // V^T offset in a stage (halves)
+  static constexpr int STAGE = WAVES * NPW * 512; // halves, incl. padding slots
   // Two workgroups per CU when two stages of each fit in half the 160 KiB LDS
   // (less 1 KiB for the rest) and, with one query block per wave, the code is
   // narrow enough for 128 VGPRs; otherwise one workgroup per CU.
@@ -101,6 +106,9 @@ struct FwdCfg {
   static constexpr int WAVES_PER_EU = WG_PER_CU * WAVES / 4;
   static constexpr int LDS_BUDGET = (TWO ? 79 : 158) * 1024;
   static constexpr int NSTAGE = 3 * STAGE * 2 <= LDS_BUDGET ? 3 : 2;
+  // both 32-key blocks of a tile in flight at once (fits the registers except
+  // with the widest codes and values)
+  static constexpr bool PIPE = !(M >= 64 && DV >= 128);
 };
 
 // One pass over the key tiles [0, kend) of a workgroup. Tiles stream through
@@ -125,27 +133,45 @@ __device__ __forceinline__ void fwd_pass(const f16* __restrict__ ka, const f16* 
 
   // LDS byte address of the stage area (the DMA takes raw LDS addresses)
   const unsigned sbase = (unsigned)(uintptr_t)(__attribute__((address_space(3))) f16*)smem;
+  // Per-lane byte offsets of this wave's chunks from the tile's key base
+  // ka + (rowbase + k0) CW and V^T base vt + vbase + k0 (both wave-uniform),
+  // computed once: key chunk w + WAVES i (slots past KCH repeat the last
+  // chunk), V^T chunk w + WAVES j.
+  unsigned koff[C::NKW], voff[C::NVW > 0 ? C::NVW : 1];
+#pragma unroll
+  for (int i = 0; i < C::NKW; ++i) {
+    const int p = 64 * min(w + C::WAVES * i, C::KCH - 1) + lane;
+    const int row = p / (C::CW / 8), col = 8 * (p % (C::CW / 8));
+    koff[i] = (unsigned)((((row & ~31) | swap23(row & 31)) * C::CW + col) * 2);
+  }
+#pragma unroll
+  for (int j = 0; j < C::NVW; ++j) {
+    const int pv = 64 * (w + C::WAVES * j) + lane;
+    const int r = pv >> 3, lc = (pv & 7) ^ vswz(r);
+    voff[j] = (unsigned)(((int64_t)r * NP + 8 * lc) * 2);
+  }
   auto issue = [&](int t) {
     const unsigned st = sbase + 2u * (unsigned)((t % C::NSTAGE) * C::STAGE);
     const int k0 = t * C::KT;
+    if (k0 + C::KT <= N) {  // uniform: no key row past N
+      const f16* kbase = ka + (rowbase + k0) * C::CW;
 #pragma unroll
-    for (int i = 0; i < NPWX; ++i) {
-      const int c = w + C::WAVES * i;  // wave-uniform chunk id
-      const f16* src;
-      if (c < C::KCH) {
-        const int p = 64 * c + lane;
+      for (int i = 0; i < C::NKW; ++i) lds_dma16_so(kbase, koff[i], st + 1024u * (unsigned)(w + C::WAVES * i));
+    } else {
+#pragma unroll
+      for (int i = 0; i < C::NKW; ++i) {
+        const int p = 64 * min(w + C::WAVES * i, C::KCH - 1) + lane;
         const int row = p / (C::CW / 8), col = 8 * (p % (C::CW / 8));
         // rows past N read the (finite) last row; every score they feed is masked
         const int key = min(k0 + ((row & ~31) | swap23(row & 31)), N - 1);
-        src = ka + (rowbase + key) * C::CW + col;
-      } else if (!MAXPASS && c < C::KCH + C::VCH) {
-        const int pv = 64 * (c - C::KCH) + lane;
-        const int r = pv >> 3, lc = (pv & 7) ^ vswz(r);
-        src = vt + vbase + (int64_t)r * NP + k0 + 8 * lc;  // V^T rows are zero past N
-      } else {
-        src = ka + (rowbase + min(k0 + lane, N - 1)) * C::CW;  // padding chunk: any in-bounds bytes
+        lds_dma16(ka + (rowbase + key) * C::CW + col, st + 1024u * (unsigned)(w + C::WAVES * i));
       }
-      lds_dma16(src, st + 1024u * (unsigned)c);
+    }
+    if (!MAXPASS) {
+      const f16* vb = vt + vbase + k0;  // V^T rows are zero from N to NP >= k0 + KT
+#pragma unroll
+      for (int j = 0; j < C::NVW; ++j)
+        lds_dma16_so(vb, voff[j], st + 2u * C::VOFF + 1024u * (unsigned)(w + C::WAVES * j));
     }
   };
 
@@ -260,23 +286,71 @@ __device__ __forceinline__ void fwd_pass(const f16* __restrict__ ka, const f16* 
       publish(t);
       issue_upto(t + C::NSTAGE - 1);
       const f16* tile = stage(t);
+      if (!C::PIPE) {  // registers too tight for two blocks in flight: one block at a time
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        f16x8 kf[C::NCH];
-        f16x4 kx;
-        kfrags(tile, kb, kf, kx);
-        f32x16 sc[QB];
+        for (int kb = 0; kb < 2; ++kb) {
+          f16x8 kf[C::NCH];
+          f16x4 kx;
+          kfrags(tile, kb, kf, kx);
+          f32x16 sc[QB];
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb) sc[qb] = score(kf, kx, qb);
-        f16x8 vf[4][DV / 32];
-        vfrags(tile, kb, vf);
+          for (int qb = 0; qb < QB; ++qb) sc[qb] = score(kf, kx, qb);
+          f16x8 vf[4][DV / 32];
+          vfrags(tile, kb, vf);
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb) {
-          f16x8 p0, p1;
-          expo(sc[qb], qb, p0, p1);
-          pv(vf, qb, p0, p1);
+          for (int qb = 0; qb < QB; ++qb) {
+            f16x8 p0, p1;
+            expo(sc[qb], qb, p0, p1);
+            pv(vf, qb, p0, p1);
+          }
         }
+        continue;
       }
+      // Software pipeline over the tile's two 32-key blocks: block 1's score
+      // MFMAs run while block 0's exponentials are on the VALU, and block 0's
+      // P.V MFMAs while block 1's exponentials are:
+      //   A: K reads, block 0 scores;  B: block 1 scores | exp(block 0), V reads
+      //   C: P.V block 0 | exp(block 1), V reads;  D: P.V block 1
+      f16x8 kf0[C::NCH], kf1[C::NCH];
+      f16x4 kx0, kx1;
+      kfrags(tile, 0, kf0, kx0);
+      kfrags(tile, 1, kf1, kx1);
+      f32x16 sc0[QB], sc1[QB];
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) sc0[qb] = score(kf0, kx0, qb);
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) sc1[qb] = score(kf1, kx1, qb);
+      f16x8 pa[QB][2], pb[QB][2];
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) expo(sc0[qb], qb, pa[qb][0], pa[qb][1]);
+      f16x8 vf0[4][DV / 32], vf1[4][DV / 32];
+      vfrags(tile, 0, vf0);
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) pv(vf0, qb, pa[qb][0], pa[qb][1]);
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) expo(sc1[qb], qb, pb[qb][0], pb[qb][1]);
+      vfrags(tile, 1, vf1);
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) pv(vf1, qb, pb[qb][0], pb[qb][1]);
+      // instruction groups (mask: 0x008 MFMA, 0x002 VALU, 0x100 LDS read)
+      constexpr int KRD = C::NCH + 1, VRD = 4 * (DV / 32);  // LDS reads per block
+      constexpr int SMF = QB * (C::NCH + 1), PMF = QB * 4 * (DV / 32);  // MFMAs per block
+      constexpr int EXV = QB * 36;  // VALU per block's exponentials (exp, cvt, dot2, adds)
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * KRD, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, SMF, 0);
+#pragma unroll
+      for (int i = 0; i < SMF; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, EXV / SMF, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, (VRD + SMF - 1) / SMF, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < PMF; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, (EXV + PMF - 1) / PMF, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, (VRD + PMF - 1) / PMF, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, PMF, 0);
     }
   }
   // ---- remaining tiles (masked ones; all of them in the exact-max pass)
@@ -290,7 +364,7 @@ __device__ __forceinline__ void fwd_pass(const f16* __restrict__ ka, const f16* 
 template <int M, int DV>
 __global__ __launch_bounds__((64 * FwdCfg<M, DV>::WAVES))
 __attribute__((amdgpu_waves_per_eu(FwdCfg<M, DV>::WAVES_PER_EU)))
-void attn_fwd_kernel(const f16* __restrict__ qa, const f16* __restrict__ ka, const f16* __restrict__ vt,
+void attn_fwd_kernel(f16* __restrict__ qa, const f16* __restrict__ ka, const f16* __restrict__ vt,
                      const float4* __restrict__ tstat, f16* __restrict__ out, float* __restrict__ lse, int N, int NP,
                      int H, int D, int BH, int causal) {
   using C = FwdCfg<M, DV>;
@@ -373,7 +447,15 @@ void attn_fwd_kernel(const f16* __restrict__ qa, const f16* __restrict__ ka, con
           for (int e = 0; e < 4; ++e) v[e] = (f16)(o[qb][dvb][4 * g + e] * inv);
           *reinterpret_cast<f16x4*>(orow + 32 * dvb + 8 * g + 4 * h32) = v;
         }
-      if (h32 == 0) lse[rowbase + q] = ltot > 0.f ? R[qb] + fast_log2(ltot) + ts[qb].x : -kFltMax;
+      if (h32 == 0) {
+        const float l2 = ltot > 0.f ? R[qb] + fast_log2(ltot) : -kFltMax;  // lse - b
+        lse[rowbase + q] = ltot > 0.f ? l2 + ts[qb].x : -kFltMax;
+        // the query row's affine block becomes the backward's {1, 1, -(lse - b)}:
+        // this wave was its only reader
+        f16 bh_, bl_;
+        split_hi_lo(-l2, bh_, bl_);
+        *reinterpret_cast<f16x2*>(qa + (rowbase + q) * C::CW + M + 2) = f16x2{bh_, bl_};
+      }
     }
   }
 }
@@ -406,18 +488,22 @@ hipError_t launch_attn_fwd(const Dims& d, const ProjBuffers& p, f16* out, float*
 }
 
 // ============================================================ backward prep
-// Backward affine blocks from lse and delta_i = dO_i . O_i (fp32). DV / 8
-// consecutive lanes share one (head, token), each reading 16 bytes of dO and
-// of O; consecutive lane groups take consecutive tokens of one head, so the
-// per-row lse / tstat reads and aug writes are contiguous too, and a wave
+// The dO rows' affine block {-delta} with delta_i = dO_i . O_i (fp32), and,
+// when the backward computed the projection itself (the forward's query rows
+// still hold its own reference), the query rows' block {1, 1, -(lse - b)}.
+// DV / 8 consecutive lanes share one (head, token), each reading 16 bytes of
+// dO and of O; consecutive lane groups take consecutive tokens of one head, so
+// the per-row lse / tstat reads and aug writes are contiguous too, and a wave
 // reads whole 128-byte row pieces of dO and O. The partial dot products meet
 // in xor shuffles. The same grid zeroes the dq accumulator.
 template <int M, int DV>
 __global__ __launch_bounds__(256) void bwd_prep_kernel(const f16* __restrict__ grad_out, const f16* __restrict__ out,
                                                        const float* __restrict__ lse,
                                                        const float4* __restrict__ tstat, f16* __restrict__ aug,
-                                                       float* __restrict__ dq, int64_t T, int N, int H, int D) {
+                                                       f16* __restrict__ qa, int write_q, float* __restrict__ dq,
+                                                       int64_t T, int N, int H, int D) {
   constexpr int G = DV / 8;  // lanes per (head, token): 4, 8 or 16, aligned within the wave
+  constexpr int CW = 3 * M + 8;
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int64_t nvec = T * (D / 8);
   const int64_t bhn = idx / G;  // (b * H + h) * N + n
@@ -434,14 +520,15 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(const f16* __restrict__ g
 #pragma unroll
   for (int sh = 1; sh < G; sh <<= 1) delta += __shfl_xor(delta, sh);
   if (idx < nvec && (threadIdx.x & (G - 1)) == 0) {
-    // affine blocks of the backward code rows: query side {1, 1, -(lse - b)},
-    // dO side {-delta}, as fp16 hi/lo pairs
-    f16 lh, ll, dh, dl;
-    split_hi_lo(-(lse[bhn] - tstat[bhn].x), lh, ll);
+    f16 dh, dl;
     split_hi_lo(-delta, dh, dl);
-    const f16 one = (f16)1.f, zero = (f16)0.f;
-    *reinterpret_cast<f16x8*>(aug + bhn * 16) = f16x8{one, one, lh, ll, zero, zero, zero, zero};
-    *reinterpret_cast<f16x8*>(aug + bhn * 16 + 8) = f16x8{dh, dl, zero, zero, zero, zero, zero, zero};
+    const f16 zero = (f16)0.f;
+    *reinterpret_cast<f16x8*>(aug + bhn * 8) = f16x8{dh, dl, zero, zero, zero, zero, zero, zero};
+    if (write_q) {
+      f16 lh, ll;
+      split_hi_lo(-(lse[bhn] - tstat[bhn].x), lh, ll);
+      *reinterpret_cast<f16x2*>(qa + bhn * CW + M + 2) = f16x2{lh, ll};
+    }
   }
   // zero dq: T * H * M floats, M / 4 float4 per (token, head)
   float4* z = reinterpret_cast<float4*>(dq);
@@ -451,19 +538,70 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(const f16* __restrict__ g
 
 template <int M, int DV>
 static hipError_t launch_bwd_prep_t(const Dims& d, const ProjBuffers& p, const f16* grad_out, const f16* out,
-                                    const float* lse, const BwdBuffers& g, hipStream_t s) {
+                                    const float* lse, const BwdBuffers& g, int write_q, hipStream_t s) {
   const int64_t n = d.T * (d.D / 8);
   hipLaunchKernelGGL((bwd_prep_kernel<M, DV>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, grad_out, out, lse,
-                     p.tstat, g.aug, g.dq, d.T, d.N, d.H, d.D);
+                     p.tstat, g.aug, p.qa, write_q, g.dq, d.T, d.N, d.H, d.D);
   return hipGetLastError();
 }
 
 hipError_t launch_bwd_prep(const Dims& d, const ProjBuffers& p, const f16* grad_out, const f16* out, const float* lse,
-                           const BwdBuffers& g, hipStream_t s) {
-  MORPHO_MDV_DISPATCH(launch_bwd_prep_t, d, p, grad_out, out, lse, g, s);
+                           const BwdBuffers& g, int write_q, hipStream_t s) {
+  MORPHO_MDV_DISPATCH(launch_bwd_prep_t, d, p, grad_out, out, lse, g, write_q, s);
 }
 
 // ============================================================ backward
+// Chunk swizzle of the 16-byte chunks of an LDS row of RB bytes (RB = 64, 128
+// or a multiple of 256): physical chunk = logical chunk ^ rswz<RB>(row). With
+// 64 banks of 4 bytes it makes both access patterns of the backward
+// conflict-free:
+//  (a) 16 lanes reading (b128) one logical chunk of 16 consecutive rows;
+//  (b) transposing b64 reads of 32 lanes covering 4 consecutive rows x 4
+//      aligned chunks (32x32x16 operands), or rows {r..r+3, r+8..r+11} x 2
+//      aligned chunks (16x16x32 operands).
+template <int RB>
+__device__ __forceinline__ int rswz(int r) {
+  static_assert(RB == 64 || RB == 128 || RB % 256 == 0, "row bytes");
+  if constexpr (RB == 64) return (r >> 2) & 3;
+  else if constexpr (RB == 128) return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
+  else return ((r & 3) << 2) | ((r >> 2) & 3);
+}
+__host__ __device__ constexpr int pow2_bytes(int x) { return x <= 64 ? 64 : 2 * pow2_bytes((x + 1) / 2); }
+// stored row of logical row r in a tile whose rows are in swap23 order within each 32
+__device__ __forceinline__ int srow23(int r) { return (r & ~31) | swap23(r & 31); }
+
+// MFMA 32x32x16 operand from a row-major LDS tile (rows in swap23 order,
+// chunk-swizzled rows of RB bytes) whose rows are the contraction index:
+// value(mn, k) = logical row k0 + k, column mn0 + mn. Each lane's two reads
+// (rows +0 and +4) stay inside one 16-byte chunk.
+template <int RB>
+__device__ __forceinline__ f16x8 tfrag32(const char* tile, int k0, int mn0, int lane) {
+  const int g = lane >> 4;
+  const int row = k0 + 8 * (g >> 1) + ((lane & 15) >> 2);
+  const int col = mn0 + 16 * (g & 1) + 4 * (lane & 3);
+  auto at = [&](int lr) {
+    const int sr = srow23(lr);
+    return tile + sr * RB + 16 * ((col >> 3) ^ rswz<RB>(sr)) + 2 * (col & 7);
+  };
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(at(row)));
+  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(at(row + 4)));
+  return __builtin_bit_cast(f16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+// MFMA 16x16x32 operand from a row-major LDS tile (rows in natural order,
+// chunk-swizzled rows of RB bytes): value(mn, k) = row k0 + k, column mn0 +
+// mn, mn = lane % 16, k = 8 (lane / 16) + j.
+template <int RB>
+__device__ __forceinline__ f16x8 tfrag16(const char* tile, int k0, int mn0, int lane) {
+  const int row = k0 + 8 * (lane >> 4) + ((lane & 15) >> 2);
+  const int col = mn0 + 4 * (lane & 3);
+  auto at = [&](int r) { return tile + r * RB + 16 * ((col >> 3) ^ rswz<RB>(r)) + 2 * (col & 7); };
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(at(row)));
+  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(at(row + 4)));
+  return __builtin_bit_cast(f16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
 template <int M, int DV>
 struct BwdCfg {
   static constexpr int CW = 3 * M + 8;
@@ -471,36 +609,23 @@ struct BwdCfg {
   static constexpr int MB = M / 32 + 1;         // 32-row blocks of dk^T (codes + the ones row at row M)
   static constexpr int QT = M <= 32 ? 64 : 32;  // queries per step
   static constexpr int NSB = QT / 32;           // 32-query sub-blocks per step
-  // Query tile [QT][CW] and dO tile [QT][DV + 8] (values, then the affine
-  // block), rows in swap23 order within each 32; row strides CW and DV + 8 are
-  // 8 (mod 16) halves, conflict-free for the b128 operand reads.
-  static constexpr int QS = CW;
-  static constexpr int OS = DV + 8;
-  static constexpr int SS = QT + 16;            // dS^T tile stride (transposed reads only)
-  static constexpr int PKS = M + 16;            // key phi tile stride (transposed reads only)
+  // LDS rows (bytes): query rows padded to a power of two, dO rows, the
+  // per-query dO affine block (16 bytes), dS^T rows (one per key, QT
+  // queries), key phi rows (at least 32 halves). Query and dO rows are stored
+  // in swap23 order within each 32.
+  static constexpr int QRB = pow2_bytes(2 * CW);
+  static constexpr int ORB = 2 * DV;
+  static constexpr int SRB = 2 * QT;
+  static constexpr int PRB = 2 * (M < 32 ? 32 : M);
   static constexpr int KW = 128;                // keys per workgroup (4 waves x 32)
   static constexpr int DQT = (QT / 16) * (M / 16) / 4;  // 16x16 dq tiles per wave per step
-  // a stage = both tiles, filled by 1 KiB DMA chunks spread over the 4 waves
-  static constexpr int QCH = (QT * CW + 511) / 512;
-  static constexpr int OCH = (QT * OS + 511) / 512;
-  static constexpr int NPW = (QCH + OCH + 3) / 4;
-  static constexpr int OOFF = QCH * 512;        // dO tile offset in a stage (halves)
-  static constexpr int STAGE = 4 * NPW * 512;   // halves, incl. padding chunks
+  // a stage = query tile, dO tile, affine tile; 1 KiB DMA pieces
+  static constexpr int QP = QT * QRB / 1024, OP = QT * ORB / 1024;
+  static constexpr int QPW = QP / 4, OPW = (OP + 3) / 4;  // pieces per wave (dO: the first OP % 4 waves)
+  static_assert(QP % 4 == 0, "query pieces must split evenly over the waves");
+  static constexpr int OOFF = QT * QRB, AOFF = OOFF + QT * ORB;  // bytes
+  static constexpr int STAGE = AOFF + 1024;
 };
-
-// MFMA 32x32x16 operand from a row-major LDS tile whose rows (the contraction
-// index) are stored in swap23 order within each 32-row block: value(mn, k) =
-// logical row k0 + k, column mn0 + mn. Each of the two transposed reads still
-// covers 4 consecutive stored rows.
-__device__ __forceinline__ f16x8 frag_kmajor_swz(const f16* tile, int stride, int k0, int mn0, int lane) {
-  const int g = lane >> 4;
-  const int row = k0 + 8 * (g >> 1) + ((lane & 15) >> 2);
-  const int col = mn0 + 16 * (g & 1) + 4 * (lane & 3);
-  const int rlo = (row & ~31) | swap23(row & 31), rhi = ((row + 4) & ~31) | swap23((row + 4) & 31);
-  f16x4 lo = lds_read_tr4(tile + rlo * stride + col);
-  f16x4 hi = lds_read_tr4(tile + rhi * stride + col);
-  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-}
 
 // Key-side (KV-outer) backward. A workgroup owns 128 keys (32 per wave, kept in
 // registers: codes, V_hi, dk / dV accumulators) and streams the query steps
@@ -512,6 +637,10 @@ __device__ __forceinline__ f16x8 frag_kmajor_swz(const f16* tile, int stride, in
 // Every wave issues exactly 4 DQT atomics per step (masked lanes add 0.0 to a
 // valid address), so the tile wait can leave the latest step's atomics in
 // flight: vector-memory operations complete in issue order.
+// The query rows come from the projection's code rows, whose affine block
+// holds {1, 1, -(lse - b)} by now (written by the forward, or by bwd_prep when
+// the backward computed the projection itself); the dO rows come from
+// grad_out and their affine block {-delta} from bwd_prep's aug rows.
 template <int M, int DV>
 __global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ qa, const f16* __restrict__ ka,
                                                        const f16* __restrict__ vt, const f16* __restrict__ aug,
@@ -520,9 +649,9 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ q
                                                        f16* __restrict__ dzv, int N, int NP, int H, int D, int HM, int BH,
                                                        int causal) {
   using C = BwdCfg<M, DV>;
-  __shared__ __align__(16) f16 stg[2 * C::STAGE];
-  __shared__ __align__(16) f16 sdS[2][C::KW * C::SS];  // dS^T of the whole workgroup: row = key
-  __shared__ __align__(16) f16 sPk[C::KW * C::PKS];     // phi_hi of the workgroup's keys: row = key
+  __shared__ __align__(16) char stg[2 * C::STAGE];
+  __shared__ __align__(16) char sdS[2][C::KW * C::SRB];  // dS^T of the whole workgroup: row = key
+  __shared__ __align__(16) char sPk[C::KW * C::PRB];     // phi_hi of the workgroup's keys: row = key
 
   const int tid = threadIdx.x, lane = tid & 63, h32 = lane >> 5, l32 = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, scalar
@@ -562,10 +691,10 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ q
   const f16x4 vaug = h32 == 0 ? f16x4{one, one, zero, zero} : f16x4{zero, zero, zero, zero};
   // phi_hi of the workgroup's keys for the dq product (zero past N)
   for (int v = tid; v < C::KW * (M / 8); v += 256) {
-    const int r = v / (M / 8), cv = (v % (M / 8)) * 8;
+    const int r = v / (M / 8), c = v % (M / 8);
     f16x8 x = {};
-    if (k0 + r < N) x = *reinterpret_cast<const f16x8*>(qa + (rowbase + k0 + r) * C::CW + cv);
-    *reinterpret_cast<f16x8*>(sPk + r * C::PKS + cv) = x;
+    if (k0 + r < N) x = *reinterpret_cast<const f16x8*>(qa + (rowbase + k0 + r) * C::CW + 8 * c);
+    *reinterpret_cast<f16x8*>(sPk + r * C::PRB + 16 * (c ^ rswz<C::PRB>(r))) = x;
   }
 
   f32x16 dva[DV / 32], dka[C::MB];
@@ -577,40 +706,55 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ q
   const int qstart = causal ? k0 : 0;
   const int nsteps = qstart < N ? (N - qstart + C::QT - 1) / C::QT : 0;
 
-  // ---- DMA of the query and dO tiles of a step (rows clamped to N - 1: every
-  // score of a query past N is masked)
-  const unsigned sbase = (unsigned)(uintptr_t)(__attribute__((address_space(3))) f16*)stg;
-  auto issue = [&](int st) {
-    const unsigned dst = sbase + 2u * (unsigned)((st & 1) * C::STAGE);
-    const int qs = qstart + st * C::QT;
+  // ---- DMA of a step's tiles. Per-lane byte offsets from the step's bases
+  // (query rows qa + (rowbase + qs) CW, dO rows grad_out + (tokbase + qs) D +
+  // h DV, affine rows aug + (rowbase + qs) 8), computed once; padding chunks
+  // of the query rows load column 0 of the same row.
+  unsigned qoff[C::QPW], ooff[C::OPW], aoff;
 #pragma unroll
-    for (int i = 0; i < C::NPW; ++i) {
-      const int c = w + 4 * i;  // wave-uniform chunk id
-      const f16* src;
-      if (c < C::QCH) {
-        const int p = 64 * c + lane;
-        const int r = p / (C::CW / 8), col = p % (C::CW / 8);
-        const int qrow = min(qs + ((r & ~31) | swap23(r & 31)), N - 1);
-        if (p >= C::QT * C::CW / 8)
-          src = qa + (rowbase + qs % N) * C::CW;  // padding piece: any in-bounds bytes
-        else if (col == M / 8)
-          src = aug + (rowbase + qrow) * 16;  // affine block of the backward
-        else
-          src = qa + (rowbase + qrow) * C::CW + 8 * col;
-      } else if (c < C::QCH + C::OCH) {
-        const int p = 64 * (c - C::QCH) + lane;
-        const int r = p / (C::OS / 8), col = p % (C::OS / 8);
-        const int qrow = min(qs + ((r & ~31) | swap23(r & 31)), N - 1);
-        if (p >= C::QT * C::OS / 8)
-          src = qa + (rowbase + qs % N) * C::CW;
-        else if (col == DV / 8)
-          src = aug + (rowbase + qrow) * 16 + 8;
-        else
-          src = grad_out + (tokbase + qrow) * D + h * DV + 8 * col;
-      } else {
-        src = qa + (rowbase + qs % N) * C::CW;
+  for (int i = 0; i < C::QPW; ++i) {
+    const int q = 64 * (w + 4 * i) + lane, r = q / (C::QRB / 16);
+    const int c = (q % (C::QRB / 16)) ^ rswz<C::QRB>(r);
+    qoff[i] = (unsigned)((srow23(r) * C::CW + (8 * c < C::CW ? 8 * c : 0)) * 2);
+  }
+#pragma unroll
+  for (int j = 0; j < C::OPW; ++j) {
+    const int q = 64 * min(w + 4 * j, C::OP - 1) + lane, r = q / (C::ORB / 16);
+    const int c = (q % (C::ORB / 16)) ^ rswz<C::ORB>(r);
+    ooff[j] = (unsigned)(((int64_t)srow23(r) * D + 8 * c) * 2);
+  }
+  aoff = (unsigned)(srow23(lane % C::QT) * 16);
+  const unsigned sbase = (unsigned)(uintptr_t)(__attribute__((address_space(3))) char*)stg;
+  auto issue = [&](int st) {
+    const unsigned dst = sbase + (unsigned)((st & 1) * C::STAGE);
+    const int qs = qstart + st * C::QT;
+    if (qs + C::QT <= N) {  // uniform
+      const f16* qbase = qa + (rowbase + qs) * C::CW;
+#pragma unroll
+      for (int i = 0; i < C::QPW; ++i) lds_dma16_so(qbase, qoff[i], dst + 1024u * (unsigned)(w + 4 * i));
+      const f16* obase = grad_out + (tokbase + qs) * D + h * DV;
+#pragma unroll
+      for (int j = 0; j < C::OPW; ++j)
+        if (w + 4 * j < C::OP) lds_dma16_so(obase, ooff[j], dst + C::OOFF + 1024u * (unsigned)(w + 4 * j));
+      if (w == 0) lds_dma16_so(aug + (rowbase + qs) * 8, aoff, dst + C::AOFF);
+    } else {  // ragged last step: rows past N read row N - 1 (every score they feed is masked)
+#pragma unroll
+      for (int i = 0; i < C::QPW; ++i) {
+        const int q = 64 * (w + 4 * i) + lane, r = q / (C::QRB / 16);
+        const int c = (q % (C::QRB / 16)) ^ rswz<C::QRB>(r);
+        const int qrow = min(qs + srow23(r), N - 1);
+        lds_dma16(qa + (rowbase + qrow) * C::CW + (8 * c < C::CW ? 8 * c : 0), dst + 1024u * (unsigned)(w + 4 * i));
       }
-      lds_dma16(src, dst + 1024u * (unsigned)c);
+#pragma unroll
+      for (int j = 0; j < C::OPW; ++j)
+        if (w + 4 * j < C::OP) {
+          const int q = 64 * (w + 4 * j) + lane, r = q / (C::ORB / 16);
+          const int c = (q % (C::ORB / 16)) ^ rswz<C::ORB>(r);
+          const int qrow = min(qs + srow23(r), N - 1);
+          lds_dma16(grad_out + (tokbase + qrow) * D + h * DV + 8 * c, dst + C::OOFF + 1024u * (unsigned)(w + 4 * j));
+        }
+      if (w == 0)
+        lds_dma16(aug + (rowbase + min(qs + srow23(lane % C::QT), N - 1)) * 8, dst + C::AOFF);
     }
   };
 
@@ -625,8 +769,8 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ q
       const int qt = tile % (C::QT / 16), ct = tile / (C::QT / 16);
 #pragma unroll
       for (int kc = 0; kc < C::KW / 32; ++kc) {
-        dqa[t][kc] = frag16_kmajor(sdS[st & 1], C::SS, 32 * kc, 16 * qt, lane);
-        dqb[t][kc] = frag16_kmajor(sPk, C::PKS, 32 * kc, 16 * ct, lane);
+        dqa[t][kc] = tfrag16<C::SRB>(sdS[st & 1], 32 * kc, 16 * qt, lane);
+        dqb[t][kc] = tfrag16<C::PRB>(sPk, 32 * kc, 16 * ct, lane);
       }
     }
   };
@@ -650,6 +794,8 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ q
     }
   };
 
+  const int qz = rswz<C::QRB>(l32), oz = rswz<C::ORB>(l32);  // this lane's row swizzles (rows 32 sb + l32)
+  const int kr = 32 * w + l32;                                // this lane's dS^T row (its key)
   if (nsteps > 0) issue(0);
   for (int step = 0; step < nsteps; ++step) {
     // this step's tiles have landed (the atomics of step - 2, issued after
@@ -663,28 +809,29 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ q
     if (step >= 1) dq_load(step - 1);
 
     const int qs = qstart + step * C::QT;
-    const f16* tQ = stg + (step & 1) * C::STAGE;
-    const f16* tO = tQ + C::OOFF;
-    f16* tS = sdS[step & 1] + (32 * w + l32) * C::SS;  // this lane's key row
+    const char* tQ = stg + (step & 1) * C::STAGE;
+    const char* tO = tQ + C::OOFF;
+    const char* tA = tQ + C::AOFF;
+    char* tS = sdS[step & 1] + kr * C::SRB;  // this lane's key row
 #pragma unroll
     for (int sb = 0; sb < C::NSB; ++sb) {
       const int q0 = qs + 32 * sb;
       f16x8 ds16[2] = {f16x8{}, f16x8{}};
       if (!((causal && kw0 > q0 + 31) || kw0 >= N || q0 >= N)) {  // wave-uniform: something unmasked
         // S = Q~ K~^T (rows: queries in swap23 order; lane: key)
-        const f16* qrow = tQ + (32 * sb + l32) * C::QS;
+        const char* qrow = tQ + (32 * sb + l32) * C::QRB;
         f32x16 s = {};
 #pragma unroll
         for (int c = 0; c < C::NCH; ++c)
-          s = mfma16(*reinterpret_cast<const f16x8*>(qrow + chunk_off<M>(c) + 8 * h32), kf[c], s);
-        s = mfma8(*reinterpret_cast<const f16x4*>(qrow + M + 4 * h32), kaug, s);
+          s = mfma16(*reinterpret_cast<const f16x8*>(qrow + 16 * ((chunk_off<M>(c) / 8 + h32) ^ qz)), kf[c], s);
+        s = mfma8(*reinterpret_cast<const f16x4*>(qrow + 16 * ((M / 8) ^ qz) + 8 * h32), kaug, s);
         // dP - delta = dO~ V~^T
-        const f16* orow = tO + (32 * sb + l32) * C::OS;
+        const char* orow = tO + (32 * sb + l32) * C::ORB;
         f32x16 dp = {};
 #pragma unroll
         for (int c = 0; c < DV / 16; ++c)
-          dp = mfma16(*reinterpret_cast<const f16x8*>(orow + 16 * c + 8 * h32), vf[c], dp);
-        dp = mfma8(*reinterpret_cast<const f16x4*>(orow + DV + 4 * h32), vaug, dp);
+          dp = mfma16(*reinterpret_cast<const f16x8*>(orow + 16 * ((2 * c + h32) ^ oz)), vf[c], dp);
+        dp = mfma8(*reinterpret_cast<const f16x4*>(tA + (32 * sb + l32) * 16 + 8 * h32), vaug, dp);
         const bool need_mask = (q0 + 32 > N) || (kw0 + 31 >= N) || (causal && kw0 + 31 > q0);
         if (need_mask) {  // wave-uniform; masked scores become -inf (P = 0)
 #pragma unroll
@@ -705,15 +852,16 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ q
         for (int c = 0; c < 2; ++c) {
 #pragma unroll
           for (int dvb = 0; dvb < DV / 32; ++dvb)
-            dva[dvb] = mfma16(frag_kmajor_swz(tO, C::OS, 32 * sb + 16 * c, 32 * dvb, lane), p16[c], dva[dvb]);
+            dva[dvb] = mfma16(tfrag32<C::ORB>(tO, 32 * sb + 16 * c, 32 * dvb, lane), p16[c], dva[dvb]);
 #pragma unroll
           for (int mb = 0; mb < C::MB; ++mb)
-            dka[mb] = mfma16(frag_kmajor_swz(tQ, C::QS, 32 * sb + 16 * c, 32 * mb, lane), ds16[c], dka[mb]);
+            dka[mb] = mfma16(tfrag32<C::QRB>(tQ, 32 * sb + 16 * c, 32 * mb, lane), ds16[c], dka[mb]);
         }
       }
       // dS^T row of this key (zeros where nothing was computed)
 #pragma unroll
-      for (int c = 0; c < 2; ++c) *reinterpret_cast<f16x8*>(tS + 32 * sb + 16 * c + 8 * h32) = ds16[c];
+      for (int c = 0; c < 2; ++c)
+        *reinterpret_cast<f16x8*>(tS + 16 * ((4 * sb + 2 * c + h32) ^ rswz<C::SRB>(kr))) = ds16[c];
     }
     if (step >= 1) dq_finish(step - 1);
   }
