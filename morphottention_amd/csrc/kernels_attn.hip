@@ -25,6 +25,8 @@
 //    tiles with ds_read_b64_tr_b16.
 //  * Both loops are software-pipelined: the next tile's global loads are in
 //    flight while the current LDS tile is consumed, one barrier per tile.
+#include <type_traits>
+
 #include "common.h"
 #include "internal.h"
 
@@ -758,46 +760,119 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ q
     }
   };
 
+  // ---- per-lane LDS offsets, computed once. Every read below is one of
+  // these plus a compile-time constant (the stage, the 32-row sub-block, the
+  // 16-row k half), which the compiler folds into the instruction's offset.
+  // Transposing reads (32x32x16 operands, tfrag32): half hh (rows +4 hh) of
+  // the column block mn0 at k0 = 0; a k0 of 16 c adds 16 c RB.
+  auto toff = [&](auto RBc, int mn0, int hh) {
+    constexpr int RB = decltype(RBc)::value;
+    const int g = lane >> 4;
+    const int sr = srow23(8 * (g >> 1) + ((lane & 15) >> 2) + 4 * hh);
+    const int col = mn0 + 16 * (g & 1) + 4 * (lane & 3);
+    return sr * RB + 16 * ((col >> 3) ^ rswz<RB>(sr)) + 2 * (col & 7);
+  };
+  using QRBc = std::integral_constant<int, C::QRB>;
+  using ORBc = std::integral_constant<int, C::ORB>;
+  int t_o[DV / 32][2], t_q[C::MB][2];
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+#pragma unroll
+    for (int dvb = 0; dvb < DV / 32; ++dvb) t_o[dvb][hh] = toff(ORBc{}, 32 * dvb, hh);
+#pragma unroll
+    for (int mb = 0; mb < C::MB; ++mb) t_q[mb][hh] = toff(QRBc{}, 32 * mb, hh);
+  }
+  auto tread = [&](const char* tile, int off, int k0rb) {
+    typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+    return __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(tile + k0rb + off)));
+  };
+  auto tfrag = [&](const char* tile, const int (&offs)[2], int k0rb) {
+    const f16x4 lo = tread(tile, offs[0], k0rb), hi = tread(tile, offs[1], k0rb);
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  };
+  // Row reads of this lane's query / dO row (row 32 sb + l32): code chunks,
+  // the query affine block, dO chunks.
+  const int qz = rswz<C::QRB>(l32), oz = rswz<C::ORB>(l32);
+  int r_q[C::NCH], r_o[DV / 16];
+#pragma unroll
+  for (int c = 0; c < C::NCH; ++c) r_q[c] = l32 * C::QRB + 16 * ((chunk_off<M>(c) / 8 + h32) ^ qz);
+  const int r_qa = l32 * C::QRB + 16 * ((M / 8) ^ qz) + 8 * h32;
+#pragma unroll
+  for (int c = 0; c < DV / 16; ++c) r_o[c] = l32 * C::ORB + 16 * ((2 * c + h32) ^ oz);
+  const int r_oa = l32 * 16 + 8 * h32;
+  const int kr = 32 * w + l32;  // this lane's dS^T row (its key)
+  const int sz = rswz<C::SRB>(kr);
+
   // ---- dq[q][code] += sum_key dS[q][key] phi[key][code]: 16 x 16 output
   // tiles split over the waves, contraction over all 128 keys of the workgroup
-  // (rows past N are zero in both operands)
+  // (rows past N are zero in both operands). The phi operand never changes:
+  // it is read once.
   f16x8 dqa[C::DQT][C::KW / 32], dqb[C::DQT][C::KW / 32];
-  auto dq_load = [&](int st) {
+  int d_s[C::DQT][2];
 #pragma unroll
-    for (int t = 0; t < C::DQT; ++t) {
-      const int tile = w + 4 * t;
-      const int qt = tile % (C::QT / 16), ct = tile / (C::QT / 16);
+  for (int t = 0; t < C::DQT; ++t) {
+    const int tile = w + 4 * t;
+    const int qt = tile % (C::QT / 16), ct = tile / (C::QT / 16);
 #pragma unroll
-      for (int kc = 0; kc < C::KW / 32; ++kc) {
-        dqa[t][kc] = tfrag16<C::SRB>(sdS[st & 1], 32 * kc, 16 * qt, lane);
-        dqb[t][kc] = tfrag16<C::PRB>(sPk, 32 * kc, 16 * ct, lane);
-      }
+    for (int hh = 0; hh < 2; ++hh) {
+      const int row = 8 * (lane >> 4) + ((lane & 15) >> 2) + 4 * hh;
+      const int col = 16 * qt + 4 * (lane & 3);
+      d_s[t][hh] = row * C::SRB + 16 * ((col >> 3) ^ rswz<C::SRB>(row)) + 2 * (col & 7);
     }
+  }
+  __syncthreads();  // sPk is complete
+#pragma unroll
+  for (int t = 0; t < C::DQT; ++t) {
+    const int ct = (w + 4 * t) / (C::QT / 16);
+#pragma unroll
+    for (int kc = 0; kc < C::KW / 32; ++kc) dqb[t][kc] = tfrag16<C::PRB>(sPk, 32 * kc, 16 * ct, lane);
+  }
+  auto dq_load = [&](const char* sd) {
+#pragma unroll
+    for (int t = 0; t < C::DQT; ++t)
+#pragma unroll
+      for (int kc = 0; kc < C::KW / 32; ++kc) dqa[t][kc] = tfrag(sd, d_s[t], 32 * kc * C::SRB);
   };
+  // dq atomics: rows qs + 16 qt + 4 (lane / 16) + r, column 16 ct + lane % 16,
+  // one uniform base per step plus a lane offset
+  int a_off[C::DQT];
+#pragma unroll
+  for (int t = 0; t < C::DQT; ++t) {
+    const int tile = w + 4 * t;
+    const int qt = tile % (C::QT / 16), ct = tile / (C::QT / 16);
+    a_off[t] = (16 * qt + 4 * (lane >> 4)) * M + 16 * ct + (lane & 15);
+  }
   auto dq_finish = [&](int st) {
     const int qs = qstart + st * C::QT;
+    float* base = dq + (rowbase + qs) * M;
+    const bool full = qs + C::QT <= N;  // uniform
 #pragma unroll
     for (int t = 0; t < C::DQT; ++t) {
       const int tile = w + 4 * t;
-      const int qt = tile % (C::QT / 16), ct = tile / (C::QT / 16);
+      const int qt = tile % (C::QT / 16);
       f32x4 acc = {};
 #pragma unroll
       for (int kc = 0; kc < C::KW / 32; ++kc) acc = mfma16x16(dqa[t][kc], dqb[t][kc], acc);
-      const int code = 16 * ct + (lane & 15);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int qq = qs + 16 * qt + 4 * (lane >> 4) + r;
-        const bool ok = qq < N;
-        // always issued (a fixed count per step); rows past N add 0 to row N - 1
-        unsafeAtomicAdd(dq + (rowbase + (ok ? qq : N - 1)) * M + code, ok ? acc[r] : 0.f);
+        if (full) {
+          unsafeAtomicAdd(base + (unsigned)a_off[t] + r * M, acc[r]);
+        } else {
+          const int qq = qs + 16 * qt + 4 * (lane >> 4) + r;
+          const bool ok = qq < N;
+          // always issued (a fixed count per step); rows past N add 0 to row N - 1
+          unsafeAtomicAdd(dq + (rowbase + (ok ? qq : N - 1)) * M + 16 * ((w + 4 * t) / (C::QT / 16)) + (lane & 15),
+                          ok ? acc[r] : 0.f);
+        }
       }
     }
   };
 
-  const int qz = rswz<C::QRB>(l32), oz = rswz<C::ORB>(l32);  // this lane's row swizzles (rows 32 sb + l32)
-  const int kr = 32 * w + l32;                                // this lane's dS^T row (its key)
-  if (nsteps > 0) issue(0);
-  for (int step = 0; step < nsteps; ++step) {
+  // ---- one query step; PAR = step & 1 (the stage and dS^T buffer), a
+  // compile-time constant so every LDS address is a lane offset plus an
+  // immediate.
+  auto do_step = [&](auto PARc, int step) {
+    constexpr int PAR = decltype(PARc)::value;
     // this step's tiles have landed (the atomics of step - 2, issued after
     // them, may still be in flight) and this wave's dS^T writes are done
     if (step >= 2)
@@ -806,32 +881,30 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ q
       wait_vmcnt_lgkm0<0>();
     __builtin_amdgcn_s_barrier();
     if (step + 1 < nsteps) issue(step + 1);  // its stage last served step - 1
-    if (step >= 1) dq_load(step - 1);
+    if (step >= 1) dq_load(sdS[PAR ^ 1]);
 
     const int qs = qstart + step * C::QT;
-    const char* tQ = stg + (step & 1) * C::STAGE;
+    const char* tQ = stg + PAR * C::STAGE;
     const char* tO = tQ + C::OOFF;
     const char* tA = tQ + C::AOFF;
-    char* tS = sdS[step & 1] + kr * C::SRB;  // this lane's key row
+    char* tS = sdS[PAR];
 #pragma unroll
     for (int sb = 0; sb < C::NSB; ++sb) {
       const int q0 = qs + 32 * sb;
       f16x8 ds16[2] = {f16x8{}, f16x8{}};
       if (!((causal && kw0 > q0 + 31) || kw0 >= N || q0 >= N)) {  // wave-uniform: something unmasked
         // S = Q~ K~^T (rows: queries in swap23 order; lane: key)
-        const char* qrow = tQ + (32 * sb + l32) * C::QRB;
+        const char* qsb = tQ + 32 * sb * C::QRB;
         f32x16 s = {};
 #pragma unroll
-        for (int c = 0; c < C::NCH; ++c)
-          s = mfma16(*reinterpret_cast<const f16x8*>(qrow + 16 * ((chunk_off<M>(c) / 8 + h32) ^ qz)), kf[c], s);
-        s = mfma8(*reinterpret_cast<const f16x4*>(qrow + 16 * ((M / 8) ^ qz) + 8 * h32), kaug, s);
+        for (int c = 0; c < C::NCH; ++c) s = mfma16(*reinterpret_cast<const f16x8*>(qsb + r_q[c]), kf[c], s);
+        s = mfma8(*reinterpret_cast<const f16x4*>(qsb + r_qa), kaug, s);
         // dP - delta = dO~ V~^T
-        const char* orow = tO + (32 * sb + l32) * C::ORB;
+        const char* osb = tO + 32 * sb * C::ORB;
         f32x16 dp = {};
 #pragma unroll
-        for (int c = 0; c < DV / 16; ++c)
-          dp = mfma16(*reinterpret_cast<const f16x8*>(orow + 16 * ((2 * c + h32) ^ oz)), vf[c], dp);
-        dp = mfma8(*reinterpret_cast<const f16x4*>(tA + (32 * sb + l32) * 16 + 8 * h32), vaug, dp);
+        for (int c = 0; c < DV / 16; ++c) dp = mfma16(*reinterpret_cast<const f16x8*>(osb + r_o[c]), vf[c], dp);
+        dp = mfma8(*reinterpret_cast<const f16x4*>(tA + 32 * sb * 16 + r_oa), vaug, dp);
         const bool need_mask = (q0 + 32 > N) || (kw0 + 31 >= N) || (causal && kw0 + 31 > q0);
         if (need_mask) {  // wave-uniform; masked scores become -inf (P = 0)
 #pragma unroll
@@ -852,23 +925,32 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ q
         for (int c = 0; c < 2; ++c) {
 #pragma unroll
           for (int dvb = 0; dvb < DV / 32; ++dvb)
-            dva[dvb] = mfma16(tfrag32<C::ORB>(tO, 32 * sb + 16 * c, 32 * dvb, lane), p16[c], dva[dvb]);
+            dva[dvb] = mfma16(tfrag(tO, t_o[dvb], (32 * sb + 16 * c) * C::ORB), p16[c], dva[dvb]);
 #pragma unroll
           for (int mb = 0; mb < C::MB; ++mb)
-            dka[mb] = mfma16(tfrag32<C::QRB>(tQ, 32 * sb + 16 * c, 32 * mb, lane), ds16[c], dka[mb]);
+            dka[mb] = mfma16(tfrag(tQ, t_q[mb], (32 * sb + 16 * c) * C::QRB), ds16[c], dka[mb]);
         }
       }
-      // dS^T row of this key (zeros where nothing was computed)
+      // dS^T row of this key (zeros where nothing was computed): logical chunk
+      // 4 sb + 2 c + h32 at physical chunk (4 sb + 2 c + h32) ^ sz
 #pragma unroll
       for (int c = 0; c < 2; ++c)
-        *reinterpret_cast<f16x8*>(tS + 16 * ((4 * sb + 2 * c + h32) ^ rswz<C::SRB>(kr))) = ds16[c];
+        *reinterpret_cast<f16x8*>(tS + kr * C::SRB + 16 * ((4 * sb + 2 * c + h32) ^ sz)) = ds16[c];
     }
     if (step >= 1) dq_finish(step - 1);
+  };
+
+  if (nsteps > 0) issue(0);
+  int step = 0;
+  for (; step + 1 < nsteps; step += 2) {
+    do_step(std::integral_constant<int, 0>{}, step);
+    do_step(std::integral_constant<int, 1>{}, step + 1);
   }
+  if (step < nsteps) do_step(std::integral_constant<int, 0>{}, step);
   if (nsteps > 0) {
     wait_vmcnt_lgkm0<4 * C::DQT>();
     __builtin_amdgcn_s_barrier();  // dS^T of the last step from every wave
-    dq_load(nsteps - 1);
+    dq_load(sdS[(nsteps - 1) & 1]);
     dq_finish(nsteps - 1);
   }
 
