@@ -308,11 +308,10 @@ __device__ __forceinline__ void fwd_pass(const f16* __restrict__ ka, const f16* 
         }
         continue;
       }
-      // Software pipeline over the tile's two 32-key blocks: block 1's score
-      // MFMAs run while block 0's exponentials are on the VALU, and block 0's
-      // P.V MFMAs while block 1's exponentials are:
-      //   A: K reads, block 0 scores;  B: block 1 scores | exp(block 0), V reads
-      //   C: P.V block 0 | exp(block 1), V reads;  D: P.V block 1
+      // Both 32-key blocks of the tile in flight: block 1's score MFMAs are
+      // independent of block 0's exponentials, and block 0's P.V MFMAs of
+      // block 1's, so the scheduler can overlap them (explicit
+      // sched_group_barrier patterns measured 5% slower than its own order).
       f16x8 kf0[C::NCH], kf1[C::NCH];
       f16x4 kx0, kx1;
       kfrags(tile, 0, kf0, kx0);
@@ -334,25 +333,6 @@ __device__ __forceinline__ void fwd_pass(const f16* __restrict__ ka, const f16* 
       vfrags(tile, 1, vf1);
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) pv(vf1, qb, pb[qb][0], pb[qb][1]);
-      // instruction groups (mask: 0x008 MFMA, 0x002 VALU, 0x100 LDS read)
-      constexpr int KRD = C::NCH + 1, VRD = 4 * (DV / 32);  // LDS reads per block
-      constexpr int SMF = QB * (C::NCH + 1), PMF = QB * 4 * (DV / 32);  // MFMAs per block
-      constexpr int EXV = QB * 36;  // VALU per block's exponentials (exp, cvt, dot2, adds)
-      __builtin_amdgcn_sched_group_barrier(0x100, 2 * KRD, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, SMF, 0);
-#pragma unroll
-      for (int i = 0; i < SMF; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, EXV / SMF, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, (VRD + SMF - 1) / SMF, 0);
-      }
-#pragma unroll
-      for (int i = 0; i < PMF; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, (EXV + PMF - 1) / PMF, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, (VRD + PMF - 1) / PMF, 0);
-      }
-      __builtin_amdgcn_sched_group_barrier(0x008, PMF, 0);
     }
   }
   // ---- remaining tiles (masked ones; all of them in the exact-max pass)
