@@ -102,7 +102,8 @@ size_t proj_bytes(const Dims& d) {
   size_t s = 0;
   s += align_up(bhn * d.CW * 2);         // qa
   s += align_up(bhn * d.CW * 2);         // ka
-  s += align_up((size_t)d.B * d.H * d.NP * d.DV * 4);  // vt (hi | lo rows)
+  s += align_up((size_t)d.B * d.H * d.NP * d.DV * 2);  // vt (V_hi^T, fp16)
+  s += align_up((size_t)d.B * d.H * d.NP * d.DV);      // vlo (e4m3)
   s += align_up(bhn * 16);               // tstat
   s += align_up((size_t)(d.HM + d.D) * d.D * 2);  // wt
   s += align_up((size_t)(d.HM + d.D) * d.D * 2);  // wcat
@@ -115,7 +116,8 @@ ProjBuffers carve_proj(void* base, const Dims& d) {
   ProjBuffers b;
   b.qa = reinterpret_cast<_Float16*>(p); p += align_up(bhn * d.CW * 2);
   b.ka = reinterpret_cast<_Float16*>(p); p += align_up(bhn * d.CW * 2);
-  b.vt = reinterpret_cast<_Float16*>(p); p += align_up((size_t)d.B * d.H * d.NP * d.DV * 4);
+  b.vt = reinterpret_cast<_Float16*>(p); p += align_up((size_t)d.B * d.H * d.NP * d.DV * 2);
+  b.vlo = reinterpret_cast<uint8_t*>(p); p += align_up((size_t)d.B * d.H * d.NP * d.DV);
   b.tstat = reinterpret_cast<float4*>(p); p += align_up(bhn * 16);
   b.wt = reinterpret_cast<_Float16*>(p); p += align_up((size_t)(d.HM + d.D) * d.D * 2);
   b.wcat = reinterpret_cast<_Float16*>(p);

@@ -5,6 +5,12 @@
 //                            B: lane l holds B[8*(l/32) + j][l%32]
 //                            C: lane l, reg r holds C[8*(r/4) + 4*(l/32) + r%4][l%32]
 //   v_mfma_f32_32x32x8_f16   as above with 4 values per lane, k = 4*(l/32) + j.
+//   v_mfma_scale_f32_32x32x64_f8f6f4 (fp8 operands, 32 bytes per lane)
+//                            A: lane l holds A[l%32][32*(l/32) + j], j = 0..31
+//                            B: lane l holds B[32*(l/32) + j][l%32]; C as above.
+//                            Each operand's E8M0 scale s multiplies by 2^(s-127).
+//   fp8 formats are OCP: e4m3 (bias 7, 0x7f is NaN, so conversions of values
+//   beyond 448 must be clamped first) and e5m2 (bias 15, the high byte of fp16).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -19,6 +25,8 @@ typedef f16 f16x2 __attribute__((ext_vector_type(2)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegInf = -__builtin_inff();
@@ -29,6 +37,11 @@ __device__ __forceinline__ f32x16 mfma16(const f16x8& a, const f16x8& b, const f
 }
 __device__ __forceinline__ f32x16 mfma8(const f16x4& a, const f16x4& b, const f32x16& c) {
   return __builtin_amdgcn_mfma_f32_32x32x8f16(a, b, c, 0, 0, 0);
+}
+// C += 2^(SA - 127) A B for an e4m3 A [32 x 64] and an e5m2 B [64 x 32].
+template <int SA>
+__device__ __forceinline__ f32x16 mfma_f8bf8(const i32x8& a, const i32x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0 /*A e4m3*/, 1 /*B e5m2*/, 0, SA, 0, 127);
 }
 // v_mfma_f32_16x16x32_f16: A lane l holds A[l%16][8*(l/16) + j], B lane l holds
 // B[8*(l/16) + j][l%16], C lane l reg r holds C[4*(l/16) + r][l%16].

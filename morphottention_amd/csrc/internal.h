@@ -52,12 +52,22 @@ __host__ __device__ inline int proj_row(const Dims& d, int c) {
 struct ProjBuffers {
   _Float16* qa;    // [B*H, N, CW] query rows (columns 0..M-1 are phi_hi, M+8..2M+7 phi_lo)
   _Float16* ka;    // [B*H, N, CW] key rows
-  _Float16* vt;    // [B*H, 2*DV, NP] values X W_V per head, transposed: rows V_hi^T then V_lo^T,
+  _Float16* vt;    // [B*H, DV, NP] values X W_V per head, transposed, rounded to fp16 (V_hi);
                    // zero for tokens N..NP-1
+  uint8_t* vlo;    // [B*H, NP/64, DV, 64] the rounding remainders V - V_hi, times 2^kVloExp, as
+                   // e4m3 bytes rounded toward zero; one [DV][64] block per 64-key tile, whose row holds key
+                   // 16 q + 8 h + r at byte 32 h + 8 q + r (h < 2, q < 4, r < 8); zero past N
   float4* tstat;   // [B*H, N] {b, R, gap, 0}: token bias, softmax reference, bound gap (base 2)
   _Float16* wt;    // [H*M + D, D] transposed [W_phi | W_V]
   _Float16* wcat;  // [D, H*M + D] [W_phi | W_V] as one row-major matrix
 };
+
+// V_lo is stored as e4m3 of V_lo * 2^kVloExp (|V_lo| <= 2^-11 |V|, so the
+// stored magnitude is about 2|V|, clamped to the e4m3 range at 448), and the
+// P.V_lo product undoes the factor through the MFMA's operand scale.
+constexpr int kVloExp = 12;
+// Byte position of key k (0..63) within a 64-byte V_lo row.
+__host__ __device__ inline int vlo_pos(int k) { return 32 * ((k >> 3) & 1) + 8 * (k >> 4) + (k & 7); }
 
 struct BwdBuffers {
   _Float16* aug;   // [B*H, N, 8] per query: the dO rows' affine block {-delta hi, lo, 0 x6}

@@ -86,24 +86,27 @@ struct FwdCfg {
   static constexpr int WAVES = 8 / QB;
   static constexpr int QW = 32 * QB * WAVES;  // 256 queries per workgroup
   // A stage holds one key tile [KT][CW] (rows in swap23 order within each 32,
-  // unpadded: CW = 8 (mod 16) halves keeps b128 reads conflict-free) and one
-  // V^T tile [2 DV][KT] (V_hi^T rows, then V_lo^T rows, chunk-swizzled), both
-  // filled by 1 KiB DMA chunks: each wave issues NKW key chunks (the key slots
-  // are padded to a multiple of the wave count; padding slots repeat the last
-  // chunk) and NVW V^T chunks, so every wave's i-th chunk kind is fixed.
+  // unpadded: CW = 8 (mod 16) halves keeps b128 reads conflict-free), one
+  // V_hi^T tile [DV][KT] fp16 (chunk-swizzled) and one V_lo block [DV][64]
+  // e4m3 (chunk-swizzled), all filled by 1 KiB DMA chunks: each wave issues
+  // NKW key chunks and NVW value chunks (both kinds' slots are padded to a
+  // multiple of the wave count; padding slots repeat the last chunk), so every
+  // wave's i-th chunk is fixed.
   static constexpr int KCH = CW / 8;      // key tile chunks
-  static constexpr int VCH = DV / 4;      // V^T tile chunks
+  static constexpr int VHC = DV / 8;      // V_hi^T chunks (8 rows of 64 keys)
+  static constexpr int VLC = DV / 16;     // V_lo chunks (16 rows of 64 bytes)
+  static constexpr int VCH = VHC + VLC;
   static constexpr int NKW = (KCH + WAVES - 1) / WAVES;  // key chunks per wave
-  static constexpr int NVW = VCH / WAVES;                // V^T chunks per wave
-  static_assert(VCH % WAVES == 0, "V^T chunks must split evenly over the waves");
+  static constexpr int NVW = (VCH + WAVES - 1) / WAVES;  // value chunks per wave
   static constexpr int NPW = NKW + NVW;   // chunks per wave per tile
   static constexpr int NPW_K = NKW;       // key-only tiles (exact-max pass)
-  static constexpr int VOFF = NKW * WAVES * 512;  // V^T offset in a stage (halves)
+  static constexpr int VOFF = NKW * WAVES * 512;  // V_hi^T offset in a stage (halves)
+  static constexpr int LOFF = VOFF + VHC * 512;   // V_lo offset in a stage (halves)
   static constexpr int STAGE = WAVES * NPW * 512; // halves, incl. padding slots
-  // Two workgroups per CU when two stages of each fit in half the 160 KiB LDS
-  // (less 1 KiB for the rest) and, with one query block per wave, the code is
-  // narrow enough for 128 VGPRs; otherwise one workgroup per CU.
-  static constexpr bool TWO = 2 * STAGE * 2 <= 79 * 1024 && (QB == 2 || M == 16);
+  // Two workgroups per CU (four waves each, 256 VGPRs) when two stages of each
+  // fit in half the 160 KiB LDS (less 1 KiB for the rest); the eight-wave
+  // shapes (one query block per wave) would have to fit 128 VGPRs and spill.
+  static constexpr bool TWO = 2 * STAGE * 2 <= 79 * 1024 && QB == 2;
   static constexpr int WG_PER_CU = TWO ? 2 : 1;
   static constexpr int WAVES_PER_EU = WG_PER_CU * WAVES / 4;
   static constexpr int LDS_BUDGET = (TWO ? 79 : 158) * 1024;
@@ -120,8 +123,9 @@ struct FwdCfg {
 // to arrive; one barrier per tile.
 // MAXPASS: key tiles only, track the row max of the exponent (exact path).
 template <int M, int DV, bool MAXPASS>
-__device__ __forceinline__ void fwd_pass(const f16* __restrict__ ka, const f16* __restrict__ vt, int64_t rowbase,
-                                         int64_t vbase, int N, int NP, int causal, int kend, int q0, int qw0,
+__device__ __forceinline__ void fwd_pass(const f16* __restrict__ ka, const f16* __restrict__ vt,
+                                         const uint8_t* __restrict__ vlo, int64_t rowbase, int64_t vbase,
+                                         int N, int NP, int causal, int kend, int q0, int qw0,
                                          f16* smem, const f16x8 (&qf)[FwdCfg<M, DV>::QB][FwdCfg<M, DV>::NCH],
                                          const f16x4 (&qaug)[FwdCfg<M, DV>::QB],
                                          f32x16 (&o)[FwdCfg<M, DV>::QB][DV / 32], float (&lsum)[FwdCfg<M, DV>::QB],
@@ -136,10 +140,11 @@ __device__ __forceinline__ void fwd_pass(const f16* __restrict__ ka, const f16* 
   // LDS byte address of the stage area (the DMA takes raw LDS addresses)
   const unsigned sbase = (unsigned)(uintptr_t)(__attribute__((address_space(3))) f16*)smem;
   // Per-lane byte offsets of this wave's chunks from the tile's key base
-  // ka + (rowbase + k0) CW and V^T base vt + vbase + k0 (both wave-uniform),
-  // computed once: key chunk w + WAVES i (slots past KCH repeat the last
-  // chunk), V^T chunk w + WAVES j.
-  unsigned koff[C::NKW], voff[C::NVW > 0 ? C::NVW : 1];
+  // ka + (rowbase + k0) CW, V_hi^T base vt + vbase + k0 and V_lo block base
+  // vlo + (vbase + 64 t) (all wave-uniform), computed once: key chunk
+  // w + WAVES i (slots past KCH repeat the last chunk), value chunk
+  // v = w + WAVES j: V_hi^T rows 8v.. for v < VHC, else V_lo rows 16(v - VHC)..
+  unsigned koff[C::NKW], voff[C::NVW];
 #pragma unroll
   for (int i = 0; i < C::NKW; ++i) {
     const int p = 64 * min(w + C::WAVES * i, C::KCH - 1) + lane;
@@ -148,9 +153,15 @@ __device__ __forceinline__ void fwd_pass(const f16* __restrict__ ka, const f16* 
   }
 #pragma unroll
   for (int j = 0; j < C::NVW; ++j) {
-    const int pv = 64 * (w + C::WAVES * j) + lane;
-    const int r = pv >> 3, lc = (pv & 7) ^ vswz(r);
-    voff[j] = (unsigned)(((int64_t)r * NP + 8 * lc) * 2);
+    const int v = min(w + C::WAVES * j, C::VCH - 1);
+    if (v < C::VHC) {
+      const int pv = 64 * v + lane;
+      const int r = pv >> 3, lc = (pv & 7) ^ vswz(r);
+      voff[j] = (unsigned)(((int64_t)r * NP + 8 * lc) * 2);
+    } else {
+      const int r = 16 * (v - C::VHC) + (lane >> 2), c = (lane & 3) ^ ((r >> 2) & 3);
+      voff[j] = (unsigned)(64 * r + 16 * c);
+    }
   }
   auto issue = [&](int t) {
     const unsigned st = sbase + 2u * (unsigned)((t % C::NSTAGE) * C::STAGE);
@@ -170,10 +181,17 @@ __device__ __forceinline__ void fwd_pass(const f16* __restrict__ ka, const f16* 
       }
     }
     if (!MAXPASS) {
-      const f16* vb = vt + vbase + k0;  // V^T rows are zero from N to NP >= k0 + KT
+      // values are zero from N to NP >= k0 + KT
+      const f16* vb = vt + vbase + k0;
+      const uint8_t* lb = vlo + vbase + (int64_t)DV * k0;
 #pragma unroll
-      for (int j = 0; j < C::NVW; ++j)
-        lds_dma16_so(vb, voff[j], st + 2u * C::VOFF + 1024u * (unsigned)(w + C::WAVES * j));
+      for (int j = 0; j < C::NVW; ++j) {
+        const unsigned dst = st + 2u * C::VOFF + 1024u * (unsigned)(w + C::WAVES * j);
+        if (min(w + C::WAVES * j, C::VCH - 1) < C::VHC)  // wave-uniform
+          lds_dma16_so(vb, voff[j], dst);
+        else
+          lds_dma16_so(lb, voff[j], dst);
+      }
     }
   };
 
@@ -190,24 +208,43 @@ __device__ __forceinline__ void fwd_pass(const f16* __restrict__ ka, const f16* 
       for (int p = 0; p < 2; ++p)
         vofs[x][p] = C::VOFF + l32 * C::KT + 8 * (4 * (x ^ (z >> 2)) + 2 * (p ^ ((z >> 1) & 1)) + (h32 ^ (z & 1)));
   }
-  // V^T fragments of block kb: [part][dvb], part = (hi, k 0-15), (hi, k 16-31),
-  // (lo, k 0-15), (lo, k 16-31); A rows are value columns, k = key.
-  auto vfrags = [&](const f16* tile, int kb, f16x8 (&vf)[4][DV / 32]) {
+  // V_hi^T fragments of block kb: [part][dvb], part = k 0-15, k 16-31; A rows
+  // are value columns, k = key.
+  auto vfrags = [&](const f16* tile, int kb, f16x8 (&vf)[2][DV / 32]) {
 #pragma unroll
-    for (int part = 0; part < 4; ++part)
-#pragma unroll
-      for (int dvb = 0; dvb < DV / 32; ++dvb) {
-        const int j = (part >= 2 ? DV / 32 : 0) + dvb;  // 32-row block of the V^T tile
-        vf[part][dvb] = *reinterpret_cast<const f16x8*>(tile + vofs[kb ^ (j & 1)][part & 1] + 32 * C::KT * j);
-      }
-  };
-  // O^T += V^T P; the DV / 32 accumulators are independent and interleaved
-  auto pv = [&](const f16x8 (&vf)[4][DV / 32], int qb, const f16x8& p0, const f16x8& p1) {
-#pragma unroll
-    for (int part = 0; part < 4; ++part)
+    for (int part = 0; part < 2; ++part)
 #pragma unroll
       for (int dvb = 0; dvb < DV / 32; ++dvb)
-        o[qb][dvb] = mfma16(vf[part][dvb], (part & 1) ? p1 : p0, o[qb][dvb]);
+        vf[part][dvb] = *reinterpret_cast<const f16x8*>(tile + vofs[kb ^ (dvb & 1)][part] + 32 * C::KT * dvb);
+  };
+  // O^T += V_hi^T P; the DV / 32 accumulators are independent and interleaved
+  auto pv = [&](const f16x8 (&vf)[2][DV / 32], int qb, const f16x8& p0, const f16x8& p1) {
+#pragma unroll
+    for (int part = 0; part < 2; ++part)
+#pragma unroll
+      for (int dvb = 0; dvb < DV / 32; ++dvb)
+        o[qb][dvb] = mfma16(vf[part][dvb], part ? p1 : p0, o[qb][dvb]);
+  };
+  // V_lo fragments of the whole 64-key tile: lane (l32, h32) of value block dvb
+  // holds row 32 dvb + l32, bytes 32 h32 .. 32 h32 + 31 (logical 16-byte chunks
+  // 2 h32, 2 h32 + 1, stored at chunk ^ ((row >> 2) & 3)), i.e. keys
+  // 16 q + 8 h32 + r at byte 8 q + r: the order in which the P bytes below
+  // are packed.
+  const unsigned lofs0 = 2 * C::LOFF + 64 * l32 + 16 * ((2 * h32) ^ ((l32 >> 2) & 3));
+  const unsigned lofs1 = 2 * C::LOFF + 64 * l32 + 16 * ((2 * h32 + 1) ^ ((l32 >> 2) & 3));
+  auto lfrags = [&](const f16* tile, i32x8 (&lf)[DV / 32]) {
+    const char* tb = reinterpret_cast<const char*>(tile);
+#pragma unroll
+    for (int dvb = 0; dvb < DV / 32; ++dvb) {
+      const i32x4 a = *reinterpret_cast<const i32x4*>(tb + lofs0 + 2048 * dvb);
+      const i32x4 b = *reinterpret_cast<const i32x4*>(tb + lofs1 + 2048 * dvb);
+      lf[dvb] = __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+    }
+  };
+  // O^T += 2^-kVloExp (V_lo 2^kVloExp)^T P over the 64 keys of a tile (fp8)
+  auto pvlo = [&](const i32x8 (&lf)[DV / 32], int qb, const i32x8& p8) {
+#pragma unroll
+    for (int dvb = 0; dvb < DV / 32; ++dvb) o[qb][dvb] = mfma_f8bf8<127 - kVloExp>(lf[dvb], p8, o[qb][dvb]);
   };
   auto kfrags = [&](const f16* tile, int kb, f16x8 (&kf)[C::NCH], f16x4& kx) {
     const f16* krow = tile + (32 * kb + l32) * C::CW;
@@ -221,18 +258,32 @@ __device__ __forceinline__ void fwd_pass(const f16* __restrict__ ka, const f16* 
     for (int c = 0; c < C::NCH; ++c) sc = mfma16(kf[c], qf[qb][c], sc);
     return mfma8(kx, qaug[qb], sc);
   };
-  auto expo = [&](const f32x16& sc, int qb, f16x8& p0, f16x8& p1) {
+  // P of one 32-key block: fp16 p0 (keys 8 h32 + r), p1 (keys 16 + 8 h32 + r),
+  // and their e5m2 bytes (the high byte of each fp16 value, i.e. rounded
+  // toward zero to 2 mantissa bits: relative error < 2^-2 on the 2^-11-relative
+  // V_lo term) into dwords 4 kb .. 4 kb + 3 of the tile's fp8 B operand.
+  auto expo = [&](const f32x16& sc, int qb, f16x8& p0, f16x8& p1, i32x8& p8, int kb) {
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
       p0[r] = (f16)fast_exp2(sc[r]);
       p1[r] = (f16)fast_exp2(sc[r + 8]);
     }
     lsum[qb] += sum8(p0) + sum8(p1);
+    const i32x4 u0 = __builtin_bit_cast(i32x4, p0), u1 = __builtin_bit_cast(i32x4, p1);
+    p8[4 * kb + 0] = (int)__builtin_amdgcn_perm((unsigned)u0[1], (unsigned)u0[0], 0x07050301u);
+    p8[4 * kb + 1] = (int)__builtin_amdgcn_perm((unsigned)u0[3], (unsigned)u0[2], 0x07050301u);
+    p8[4 * kb + 2] = (int)__builtin_amdgcn_perm((unsigned)u1[1], (unsigned)u1[0], 0x07050301u);
+    p8[4 * kb + 3] = (int)__builtin_amdgcn_perm((unsigned)u1[3], (unsigned)u1[2], 0x07050301u);
   };
   auto stage = [&](int t) { return smem + (t % C::NSTAGE) * C::STAGE; };
 
-  // Any tile: per 32-key block and query block, with masks where needed.
+  // Any tile: per 32-key block and query block, with masks where needed; the
+  // P.V_lo product follows once per query block over the whole tile (the P
+  // bytes of skipped blocks stay zero).
   auto compute = [&](const f16* tile, int k0) {
+    i32x8 p8[QB];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) p8[qb] = i32x8{};
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       const int kbase = k0 + 32 * kb;
@@ -240,7 +291,7 @@ __device__ __forceinline__ void fwd_pass(const f16* __restrict__ ka, const f16* 
       f16x8 kf[C::NCH];
       f16x4 kx;
       kfrags(tile, kb, kf, kx);
-      f16x8 vf[4][DV / 32];
+      f16x8 vf[2][DV / 32];
       if (!MAXPASS) vfrags(tile, kb, vf);
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) {
@@ -260,9 +311,16 @@ __device__ __forceinline__ void fwd_pass(const f16* __restrict__ ka, const f16* 
           continue;
         }
         f16x8 p0, p1;
-        expo(sc, qb, p0, p1);
+        expo(sc, qb, p0, p1, p8[qb], kb);
         pv(vf, qb, p0, p1);
       }
+    }
+    if (!MAXPASS && k0 < N) {
+      i32x8 lf[DV / 32];
+      lfrags(tile, lf);
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb)
+        if (!(causal && k0 > qw0 + 32 * qb + 31)) pvlo(lf, qb, p8[qb]);  // wave-uniform
     }
   };
 
@@ -289,6 +347,7 @@ __device__ __forceinline__ void fwd_pass(const f16* __restrict__ ka, const f16* 
       issue_upto(t + C::NSTAGE - 1);
       const f16* tile = stage(t);
       if (!C::PIPE) {  // registers too tight for two blocks in flight: one block at a time
+        i32x8 p8[QB];
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
           f16x8 kf[C::NCH];
@@ -297,15 +356,19 @@ __device__ __forceinline__ void fwd_pass(const f16* __restrict__ ka, const f16* 
           f32x16 sc[QB];
 #pragma unroll
           for (int qb = 0; qb < QB; ++qb) sc[qb] = score(kf, kx, qb);
-          f16x8 vf[4][DV / 32];
+          f16x8 vf[2][DV / 32];
           vfrags(tile, kb, vf);
 #pragma unroll
           for (int qb = 0; qb < QB; ++qb) {
             f16x8 p0, p1;
-            expo(sc[qb], qb, p0, p1);
+            expo(sc[qb], qb, p0, p1, p8[qb], kb);
             pv(vf, qb, p0, p1);
           }
         }
+        i32x8 lf[DV / 32];
+        lfrags(tile, lf);
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) pvlo(lf, qb, p8[qb]);
         continue;
       }
       // Both 32-key blocks of the tile in flight: block 1's score MFMAs are
@@ -322,17 +385,22 @@ __device__ __forceinline__ void fwd_pass(const f16* __restrict__ ka, const f16* 
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) sc1[qb] = score(kf1, kx1, qb);
       f16x8 pa[QB][2], pb[QB][2];
+      i32x8 p8[QB];
 #pragma unroll
-      for (int qb = 0; qb < QB; ++qb) expo(sc0[qb], qb, pa[qb][0], pa[qb][1]);
-      f16x8 vf0[4][DV / 32], vf1[4][DV / 32];
+      for (int qb = 0; qb < QB; ++qb) expo(sc0[qb], qb, pa[qb][0], pa[qb][1], p8[qb], 0);
+      f16x8 vf0[2][DV / 32], vf1[2][DV / 32];
       vfrags(tile, 0, vf0);
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) pv(vf0, qb, pa[qb][0], pa[qb][1]);
 #pragma unroll
-      for (int qb = 0; qb < QB; ++qb) expo(sc1[qb], qb, pb[qb][0], pb[qb][1]);
+      for (int qb = 0; qb < QB; ++qb) expo(sc1[qb], qb, pb[qb][0], pb[qb][1], p8[qb], 1);
       vfrags(tile, 1, vf1);
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) pv(vf1, qb, pb[qb][0], pb[qb][1]);
+      i32x8 lf[DV / 32];
+      lfrags(tile, lf);
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) pvlo(lf, qb, p8[qb]);
     }
   }
   // ---- remaining tiles (masked ones; all of them in the exact-max pass)
@@ -347,6 +415,7 @@ template <int M, int DV>
 __global__ __launch_bounds__((64 * FwdCfg<M, DV>::WAVES))
 __attribute__((amdgpu_waves_per_eu(FwdCfg<M, DV>::WAVES_PER_EU)))
 void attn_fwd_kernel(f16* __restrict__ qa, const f16* __restrict__ ka, const f16* __restrict__ vt,
+                     const uint8_t* __restrict__ vlo,
                      const float4* __restrict__ tstat, f16* __restrict__ out, float* __restrict__ lse, int N, int NP,
                      int H, int D, int BH, int causal) {
   using C = FwdCfg<M, DV>;
@@ -361,7 +430,7 @@ void attn_fwd_kernel(f16* __restrict__ qa, const f16* __restrict__ ka, const f16
   const int q0 = qblk * C::QW, qw0 = q0 + 32 * QB * w;
   const int b = bh / H, h = bh - b * H;
   const int64_t rowbase = (int64_t)bh * N;
-  const int64_t vbase = (int64_t)bh * 2 * DV * NP;
+  const int64_t vbase = (int64_t)bh * DV * NP;  // V_hi^T rows (halves) and V_lo blocks (bytes) of the head
 
   f16x8 qf[QB][C::NCH];
   f16x4 qaug[QB];
@@ -400,7 +469,7 @@ void attn_fwd_kernel(f16* __restrict__ qa, const f16* __restrict__ ka, const f16
       qa0[qb] = qaug[qb];
       if (h32 == 0) { qa0[qb][2] = (f16)0.f; qa0[qb][3] = (f16)0.f; }
     }
-    fwd_pass<M, DV, true>(ka, vt, rowbase, vbase, N, NP, causal, kend, q0, qw0, smem, qf, qa0, o, lsum, rmax);
+    fwd_pass<M, DV, true>(ka, vt, vlo, rowbase, vbase, N, NP, causal, kend, q0, qw0, smem, qf, qa0, o, lsum, rmax);
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
       const float m = fmaxf(rmax[qb], __shfl_xor(rmax[qb], 32));
@@ -411,7 +480,7 @@ void attn_fwd_kernel(f16* __restrict__ qa, const f16* __restrict__ ka, const f16
     }
     __syncthreads();  // every wave is done with the stages before they are refilled
   }
-  fwd_pass<M, DV, false>(ka, vt, rowbase, vbase, N, NP, causal, kend, q0, qw0, smem, qf, qaug, o, lsum, rmax);
+  fwd_pass<M, DV, false>(ka, vt, vlo, rowbase, vbase, N, NP, causal, kend, q0, qw0, smem, qf, qaug, o, lsum, rmax);
 
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
@@ -446,7 +515,7 @@ template <int M, int DV>
 static hipError_t launch_attn_fwd_t(const Dims& d, const ProjBuffers& p, f16* out, float* lse, hipStream_t s) {
   using C = FwdCfg<M, DV>;
   const dim3 grid(xcd_grid((d.N + C::QW - 1) / C::QW, d.B * d.H));
-  hipLaunchKernelGGL((attn_fwd_kernel<M, DV>), grid, dim3(64 * C::WAVES), 0, s, p.qa, p.ka, p.vt, p.tstat, out, lse,
+  hipLaunchKernelGGL((attn_fwd_kernel<M, DV>), grid, dim3(64 * C::WAVES), 0, s, p.qa, p.ka, p.vt, p.vlo, p.tstat, out, lse,
                      d.N, d.NP, d.H, d.D, d.B * d.H, d.causal);
   return hipGetLastError();
 }
@@ -664,7 +733,7 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ q
     kaug = *reinterpret_cast<const f16x4*>(krow + M + 4 * h32);
     // V_hi[key][16c + 8 h32 + j] from the transposed layout (a wave reads 32
     // consecutive keys of each value column)
-    const f16* vcol = vt + (int64_t)bh * 2 * DV * NP + key;
+    const f16* vcol = vt + (int64_t)bh * DV * NP + key;
 #pragma unroll
     for (int c = 0; c < DV / 16; ++c)
 #pragma unroll

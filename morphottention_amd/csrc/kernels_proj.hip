@@ -78,6 +78,26 @@ template <int BN>
 using ProjGemm = Gemm<256, BN, 4, true, true, 64, 2>;
 constexpr int kProjBM = 256;
 
+// e4m3 byte(s) of V_lo * 2^kVloExp, clamped to the format's range (e4m3 has
+// no infinity: an overflowing conversion gives NaN) and rounded toward zero:
+// the stored remainder is never larger than V - V_hi, so V_hi + remainder
+// rounds back to V_hi in fp16 (a single key's output is then exactly V_hi,
+// the value the backward's dP = dO V_hi^T sees).
+__device__ __forceinline__ unsigned vlo_code(float r) {
+  const float x = fminf(fmaxf(r * (float)(1 << kVloExp), -448.f), 448.f);
+  unsigned c = (unsigned)__builtin_amdgcn_cvt_pk_fp8_f32(x, 0.f, 0, false) & 0xffu;  // nearest
+  if (fabsf(__builtin_amdgcn_cvt_f32_fp8((int)c, 0)) > fabsf(x)) c -= 1u;  // one code toward zero
+  return c;
+}
+__device__ __forceinline__ uint2 vlo_pack8(const float (&r)[8]) {
+  unsigned w[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+    w[i] = vlo_code(r[4 * i]) | (vlo_code(r[4 * i + 1]) << 8) | (vlo_code(r[4 * i + 2]) << 16) |
+           (vlo_code(r[4 * i + 3]) << 24);
+  return make_uint2(w[0], w[1]);
+}
+
 template <int M, int DV, int BN>
 __global__ __launch_bounds__(kGemmThreads) void proj_fwd_kernel(const f16* __restrict__ X,
                                                                const f16* __restrict__ gate_q,
@@ -170,12 +190,14 @@ __global__ __launch_bounds__(kGemmThreads) void proj_fwd_kernel(const f16* __res
       *reinterpret_cast<f16x8*>(krow + M) = f16x8{bh_, bl_, one, one, zero, zero, zero, zero};
       p.tstat[bhn] = make_float4(bias, R, Ub - t_ii, 0.f);
     }
-    // values, transposed: vt[bh][dd][n] = V_hi, vt[bh][DV + dd][n] = V_lo.
-    // One item = one column x 8 consecutive tokens; 8 neighbouring threads
-    // cover the slab's 64 consecutive tokens of a column (128 contiguous
-    // bytes), a wave 8 columns.
+    // values, transposed: vt[bh][dd][n] = V_hi, and the remainder V - V_hi as
+    // e4m3 in vlo's tile-major, key-permuted rows. One item = one column x 8
+    // consecutive tokens; 8 neighbouring threads cover the slab's 64
+    // consecutive tokens of a column (128 contiguous bytes of vt, one 64-byte
+    // row of vlo), a wave 8 columns.
     if (proj_col(d, tn, BN - 1) >= d.HM) {  // the tile has value columns (uniform)
       const bool vec = d.N % 8 == 0;
+      const int ntile = d.NP / 64;
       for (int idx = tid; idx < 8 * BN; idx += kGemmThreads) {
         const int rg = idx & 7, cc = idx >> 3;
         const int col = proj_col(d, tn, cc), tb = row0 + 8 * rg;
@@ -183,37 +205,41 @@ __global__ __launch_bounds__(kGemmThreads) void proj_fwd_kernel(const f16* __res
         const int vcol = col - d.HM, h = vcol / DV, dd = vcol % DV;
         const float* src = stage + 8 * rg * SS + cc;
         if (vec) {
-          // N % 8 == 0 and tb % 8 == 0: the 8 tokens share one batch row
+          // N % 8 == 0 and tb % 8 == 0: the 8 tokens share one batch row and
+          // land on 8 consecutive bytes of a vlo row
           const int b = tb / d.N, n = tb - b * d.N;
-          f16x8 vh, vl;
+          const int64_t bh = (int64_t)(b * d.H + h);
+          f16x8 vh;
+          float vl[8];
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
             const float x = src[e * SS];
             vh[e] = (f16)x;
-            vl[e] = (f16)(x - (float)vh[e]);
+            vl[e] = x - (float)vh[e];
           }
-          f16* dst = p.vt + ((int64_t)(b * d.H + h) * 2 * DV + dd) * d.NP + n;
-          const int64_t lo = (int64_t)DV * d.NP;
+          f16* dst = p.vt + (bh * DV + dd) * d.NP + n;
+          uint8_t* lrow = p.vlo + ((bh * ntile + n / 64) * DV + dd) * 64;
           *reinterpret_cast<f16x8*>(dst) = vh;
-          *reinterpret_cast<f16x8*>(dst + lo) = vl;
+          *reinterpret_cast<uint2*>(lrow + vlo_pos(n % 64)) = vlo_pack8(vl);
           if (n + 8 == d.N)
             for (int z = 8; n + z < d.NP; z += 8) {
               *reinterpret_cast<f16x8*>(dst + z) = f16x8{};
-              *reinterpret_cast<f16x8*>(dst + lo + z) = f16x8{};
+              *reinterpret_cast<uint2*>(lrow + vlo_pos((n + z) % 64)) = make_uint2(0u, 0u);
             }
         } else {
           for (int e = 0; e < 8 && tb + e < T; ++e) {
             const int t = tb + e, b = t / d.N, n = t - b * d.N;
+            const int64_t bh = (int64_t)(b * d.H + h);
             const float x = src[e * SS];
-            const f16 vh = (f16)x, vl = (f16)(x - (float)vh);
-            f16* dst = p.vt + ((int64_t)(b * d.H + h) * 2 * DV + dd) * d.NP + n;
-            const int64_t lo = (int64_t)DV * d.NP;
+            const f16 vh = (f16)x;
+            f16* dst = p.vt + (bh * DV + dd) * d.NP + n;
+            uint8_t* lrow = p.vlo + ((bh * ntile + n / 64) * DV + dd) * 64;
             dst[0] = vh;
-            dst[lo] = vl;
+            lrow[vlo_pos(n % 64)] = (uint8_t)vlo_code(x - (float)vh);
             if (n == d.N - 1)
               for (int z = 1; n + z < d.NP; ++z) {
                 dst[z] = (f16)0.f;
-                dst[lo + z] = (f16)0.f;
+                lrow[vlo_pos((n + z) % 64)] = 0;
               }
           }
         }

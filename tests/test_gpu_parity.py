@@ -194,6 +194,40 @@ def test_scale_zero_is_a_mean():
 
 
 @pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("m,dv", [(16, 32), (16, 64), (16, 128), (64, 32), (64, 64), (64, 128)])
+def test_value_remainder_is_carried(m, dv, causal):
+    """With scale = 0 every weight is exactly 1, so the output is the (prefix)
+    mean of V and its only errors are the carried precision of V and the final
+    fp16 rounding. V enters as fp16 V_hi plus the remainder V - V_hi in e4m3
+    rounded toward zero (relative error < 2^-3 of a term <= 2^-11 |V|), so the
+    error beyond half an fp16 ulp of the output is below 2^-14 max|V| in the
+    worst case and, on these inputs, at most 2^-18 max|V| (measured). The bar
+    is 2^-16 max|V|: with the remainder dropped the excess reaches 2^-13, with
+    the remainders paired with the wrong keys of each 64-key tile (visible in
+    the masked diagonal tiles) 2^-15 (both measured with the mistake planted
+    in a scratch build). The shapes cover the one- and two-block-per-wave
+    forwards, the pipelined and one-block tile bodies and the padded
+    value-chunk layouts."""
+    B, N, H = 2, 200, 2
+    x, params, dout = make_inputs(B, N, H * dv, H, m, seed=310 + m + dv)
+    from morphottention_amd import morpho_attention
+    _say(f"[case] value remainder m={m} dv={dv} causal={causal} N={N}")
+    with torch.no_grad():
+        out = morpho_attention(x, *params, H, m, scale=0.0, causal=causal).float()
+    V = (x.double() @ params[3].double())
+    if causal:
+        ref = torch.cumsum(V, dim=1) / torch.arange(1, N + 1, device=V.device, dtype=V.dtype)[None, :, None]
+    else:
+        ref = V.mean(dim=1, keepdim=True).expand_as(V)
+    ref = ref.float()
+    excess = ((out - ref).abs() - half_ulp(ref)).clamp_min(0).max().item()
+    bound = 2.0 ** -16 * V.abs().max().item()
+    _say(f"[parity] value remainder m={m} dv={dv} causal={causal}: beyond rounding {excess:.3e} "
+         f"(bound {bound:.3e}, max|V| {V.abs().max().item():.2f})")
+    assert excess <= bound
+
+
+@pytest.mark.parametrize("causal", [False, True])
 def test_exact_max_path_with_large_signed_gates(causal):
     """Gates large and of both signs make the closed-form score bound loose,
     which routes rows through the exact two-pass maximum."""
