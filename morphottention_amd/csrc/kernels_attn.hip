@@ -460,6 +460,9 @@ void attn_fwd_kernel(f16* __restrict__ qa, const f16* __restrict__ ka, const f16
     for (int i = 0; i < DV / 32; ++i) o[qb][i] = f32x16{};
   }
   const int kend = causal ? min(N, q0 + C::QW) : N;
+  // the query operands are loaded under a condition: wait on every path, or the
+  // compiler waits for them inside the tile loop, draining the in-flight DMA
+  wait_vmcnt<0>();
 
   if (__syncthreads_or(any_gap)) {
     // pass 1: exact row max of the base-2 exponent without the reference
@@ -869,6 +872,11 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ q
       d_s[t][hh] = row * C::SRB + 16 * ((col >> 3) ^ rswz<C::SRB>(row)) + 2 * (col & 7);
     }
   }
+  // The key-side operands above are loaded under a condition; without a wait
+  // on every path the compiler treats them as possibly pending inside the step
+  // loop and waits for vmcnt there, which then also drains the next step's DMA
+  // and the dq atomics on every sub-block.
+  wait_vmcnt<0>();
   __syncthreads();  // sPk is complete
 #pragma unroll
   for (int t = 0; t < C::DQT; ++t) {
