@@ -78,7 +78,7 @@ int make_dims(int64_t B, int64_t N, int64_t D, int64_t H, int64_t M, float scale
   d.DV = (int)DV;
   d.T = T;
   d.HM = (int)(H * M);
-  d.CW = 3 * (int)M + 8;
+  d.CW = 2 * (int)M + 8;
   d.scale = scale;
   d.causal = causal ? 1 : 0;
   // projection tiles: 320 columns when that divides H*M + D, else 256; the

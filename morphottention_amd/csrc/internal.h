@@ -37,17 +37,18 @@ __host__ __device__ inline int proj_row(const Dims& d, int c) {
 
 // Products of the forward projection; the forward workspace holds exactly these.
 //
-// Code rows carry each code as an fp16 hi/lo pair laid out so that one MFMA
-// contraction over CW columns yields (to ~2^-22) the exact base-2 exponent:
-//   query row  [phi_hi | 1, 1, -R_hi, -R_lo, 0 x4 | phi_lo | phi_hi]
+// Code rows carry each code as an fp16 hi/lo pair (CW = 2M + 8 columns):
+//   query row  [phi_hi | 1, 1, -R_hi, -R_lo, 0 x4 | phi_lo]
 //              (after the forward: [.. | 1, 1, -(lse - b) hi, lo, 0 x4 | ..],
 //               the backward's row reference)
-//   key row    [kc_hi  | b_hi, b_lo, 1, 1, 0 x4   | kc_hi  | kc_lo ]
-// (the 8-wide affine block sits right after the first M codes so that a
-// 32-row transposed read of the query row starting at column 32*floor(M/32)
-// sees the constant-1 column at row M, which the backward uses to form
-// column sums of dS in the same MFMA as the key-side code gradient).
-// with kc = c1 * G * phi, c1 = 2 scale log2e, G = gate_q * gate_k, b the token
+//   key row    [kc_hi  | b_hi, b_lo, 1, 1, 0 x4   | kc_lo ]
+// The attention kernels contract the chunk pairs (kc_hi, phi_hi), (kc_hi,
+// phi_lo), (kc_lo, phi_hi) and the affine blocks in one MFMA accumulator,
+// which yields (to ~2^-22) the exact base-2 exponent. The 8-wide affine block
+// sits right after the first M codes so that a 32-row transposed read of the
+// query row starting at column 32*floor(M/32) sees the constant-1 column at
+// row M, which the backward uses to form column sums of dS in the same MFMA
+// as the key-side code gradient. Here kc = c1 * G * phi, c1 = 2 scale log2e, G = gate_q * gate_k, b the token
 // bias -scale log2e sum_c G_c phi_c and R the per-query softmax reference.
 struct ProjBuffers {
   _Float16* qa;    // [B*H, N, CW] query rows (columns 0..M-1 are phi_hi, M+8..2M+7 phi_lo)

@@ -11,10 +11,11 @@
 //                      drops is completed here)
 //
 // MI355X design:
-//  * The exponent is produced by one MFMA contraction over a code row of
-//    width 3m + 8 (see ProjBuffers): fp16 hi/lo code pairs make the score exact
-//    to ~2^-22, and the 8-wide affine block adds the key bias and subtracts the
-//    row reference, so exp2 reads the accumulator directly.
+//  * The exponent is produced by one MFMA accumulator over the code rows
+//    [hi | affine(8) | lo] (see ProjBuffers): the chunk products hi.hi, hi.lo
+//    and lo.hi of fp16 code pairs make the score exact to ~2^-22, and the
+//    8-wide affine block adds the key bias and subtracts the row reference,
+//    so exp2 reads the accumulator directly.
 //  * Forward softmax uses a per-row reference R >= (row max - 15) computed by
 //    the projection from a closed-form bound on the soft Hamming score, so no
 //    running max or rescaling is needed; rows whose bound is loose (gap > 25,
@@ -42,11 +43,28 @@ __device__ __forceinline__ float sum8(const f16x8& v) {
   return s;
 }
 
-// Column offset of the c-th 16-wide code chunk of a code row (the 8-wide
-// affine block sits at [M, M + 8)).
+// Column offset of the c-th 16-wide code chunk of a code row: chunks 0 ..
+// M/16 - 1 hold the hi parts, M/16 .. M/8 - 1 the lo parts (the 8-wide affine
+// block sits at [M, M + 8)).
 template <int M>
 __device__ __forceinline__ constexpr int chunk_off(int c) {
   return c < M / 16 ? 16 * c : 16 * c + 8;
+}
+// The exponent's code part, sum_c kc_c phi_c to ~2^-22, from the hi / lo
+// chunks of a key (kf) and a query (qf) operand: hi.hi + hi.lo + lo.hi.
+// KEY_A: the key chunks are the A operand (forward: rows = keys), else the
+// query chunks are (backward: rows = queries).
+template <int M, bool KEY_A>
+__device__ __forceinline__ f32x16 code_dot(const f16x8 (&kf)[M / 8], const f16x8 (&qf)[M / 8], f32x16 acc) {
+  constexpr int HC = M / 16;
+  auto mm = [&](const f16x8& k, const f16x8& q) { acc = KEY_A ? mfma16(k, q, acc) : mfma16(q, k, acc); };
+#pragma unroll
+  for (int i = 0; i < HC; ++i) mm(kf[i], qf[i]);
+#pragma unroll
+  for (int i = 0; i < HC; ++i) mm(kf[i], qf[HC + i]);
+#pragma unroll
+  for (int i = 0; i < HC; ++i) mm(kf[HC + i], qf[i]);
+  return acc;
 }
 
 // Workgroups are dispatched round-robin over the 8 XCDs (id % 8), each with
@@ -77,12 +95,13 @@ __device__ __forceinline__ int vswz(int r) { return (r ^ (r >> 3)) & 7; }
 
 template <int M, int DV>
 struct FwdCfg {
-  static constexpr int CW = 3 * M + 8;    // code row width
-  static constexpr int NCH = 3 * M / 16;  // 16-wide code chunks
+  static constexpr int CW = 2 * M + 8;    // code row width
+  static constexpr int NCH = M / 8;       // 16-wide code chunks (hi, then lo)
   static constexpr int KT = 64;           // keys per tile
   // Each wave owns QB blocks of 32 queries: every K / V fragment read from LDS
-  // then feeds QB MFMAs. Two blocks where the registers allow it.
-  static constexpr int QB = (M <= 32 && DV <= 64) ? 2 : 1;
+  // then feeds QB MFMAs. Two blocks where the registers allow it (m dv <=
+  // 1024; at m = 32, dv = 64 two blocks spill).
+  static constexpr int QB = (M <= 32 && DV <= 64 && M * DV <= 1024) ? 2 : 1;
   static constexpr int WAVES = 8 / QB;
   static constexpr int QW = 32 * QB * WAVES;  // 256 queries per workgroup
   // A stage holds one key tile [KT][CW] (rows in swap23 order within each 32,
@@ -253,10 +272,7 @@ __device__ __forceinline__ void fwd_pass(const f16* __restrict__ ka, const f16* 
     kx = *reinterpret_cast<const f16x4*>(krow + M + 4 * h32);
   };
   auto score = [&](const f16x8 (&kf)[C::NCH], const f16x4& kx, int qb) {
-    f32x16 sc = {};
-#pragma unroll
-    for (int c = 0; c < C::NCH; ++c) sc = mfma16(kf[c], qf[qb][c], sc);
-    return mfma8(kx, qaug[qb], sc);
+    return mfma8(kx, qaug[qb], code_dot<M, true>(kf, qf[qb], f32x16{}));
   };
   // P of one 32-key block: fp16 p0 (keys 8 h32 + r), p1 (keys 16 + 8 h32 + r),
   // and their e5m2 bytes (the high byte of each fp16 value, i.e. rounded
@@ -413,7 +429,7 @@ __device__ __forceinline__ void fwd_pass(const f16* __restrict__ ka, const f16* 
 
 template <int M, int DV>
 __global__ __launch_bounds__((64 * FwdCfg<M, DV>::WAVES))
-__attribute__((amdgpu_waves_per_eu(FwdCfg<M, DV>::WAVES_PER_EU)))
+__attribute__((amdgpu_waves_per_eu(FwdCfg<M, DV>::WAVES_PER_EU, FwdCfg<M, DV>::WAVES_PER_EU)))
 void attn_fwd_kernel(f16* __restrict__ qa, const f16* __restrict__ ka, const f16* __restrict__ vt,
                      const uint8_t* __restrict__ vlo,
                      const float4* __restrict__ tstat, f16* __restrict__ out, float* __restrict__ lse, int N, int NP,
@@ -557,7 +573,7 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(const f16* __restrict__ g
                                                        f16* __restrict__ qa, int write_q, float* __restrict__ dq,
                                                        int64_t T, int N, int H, int D) {
   constexpr int G = DV / 8;  // lanes per (head, token): 4, 8 or 16, aligned within the wave
-  constexpr int CW = 3 * M + 8;
+  constexpr int CW = 2 * M + 8;
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int64_t nvec = T * (D / 8);
   const int64_t bhn = idx / G;  // (b * H + h) * N + n
@@ -658,8 +674,8 @@ __device__ __forceinline__ f16x8 tfrag16(const char* tile, int k0, int mn0, int 
 
 template <int M, int DV>
 struct BwdCfg {
-  static constexpr int CW = 3 * M + 8;
-  static constexpr int NCH = 3 * M / 16;
+  static constexpr int CW = 2 * M + 8;
+  static constexpr int NCH = M / 8;             // 16-wide code chunks (hi, then lo)
   static constexpr int MB = M / 32 + 1;         // 32-row blocks of dk^T (codes + the ones row at row M)
   static constexpr int QT = M <= 32 ? 64 : 32;  // queries per step
   static constexpr int NSB = QT / 32;           // 32-query sub-blocks per step
@@ -952,9 +968,10 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ q
       if (!((causal && kw0 > q0 + 31) || kw0 >= N || q0 >= N)) {  // wave-uniform: something unmasked
         // S = Q~ K~^T (rows: queries in swap23 order; lane: key)
         const char* qsb = tQ + 32 * sb * C::QRB;
-        f32x16 s = {};
+        f16x8 qfr[C::NCH];
 #pragma unroll
-        for (int c = 0; c < C::NCH; ++c) s = mfma16(*reinterpret_cast<const f16x8*>(qsb + r_q[c]), kf[c], s);
+        for (int c = 0; c < C::NCH; ++c) qfr[c] = *reinterpret_cast<const f16x8*>(qsb + r_q[c]);
+        f32x16 s = code_dot<M, false>(kf, qfr, f32x16{});
         s = mfma8(*reinterpret_cast<const f16x4*>(qsb + r_qa), kaug, s);
         // dP - delta = dO~ V~^T
         const char* osb = tO + 32 * sb * C::ORB;

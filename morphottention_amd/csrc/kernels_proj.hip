@@ -106,7 +106,7 @@ __global__ __launch_bounds__(kGemmThreads) void proj_fwd_kernel(const f16* __res
   constexpr int SS = BN + 1;  // stage row stride (floats)
   static_assert(64 * SS * 4 <= G::kLdsBytes, "epilogue slab must fit the main loop's LDS");
   __shared__ __align__(16) char smem[G::kLdsBytes];
-  constexpr int CW = 3 * M + 8;
+  constexpr int CW = 2 * M + 8;
 
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = w / G::WN, wn = w % G::WN;
@@ -167,13 +167,11 @@ __global__ __launch_bounds__(kGemmThreads) void proj_fwd_kernel(const f16* __res
           tii += wgt * phi * (2.f * phi - 1.f);
           U += fmaxf(0.f, wgt * (2.f * phi - 1.f));
         }
-        // rows: [phi_hi | aug | phi_lo | phi_hi] and [kc_hi | aug | kc_hi | kc_lo]
+        // rows: [phi_hi | aug | phi_lo] and [kc_hi | aug | kc_lo]
         *reinterpret_cast<f16x8*>(qrow + c8) = phh;
         *reinterpret_cast<f16x8*>(qrow + M + 8 + c8) = phl;
-        *reinterpret_cast<f16x8*>(qrow + 2 * M + 8 + c8) = phh;
         *reinterpret_cast<f16x8*>(krow + c8) = kch;
-        *reinterpret_cast<f16x8*>(krow + M + 8 + c8) = kch;
-        *reinterpret_cast<f16x8*>(krow + 2 * M + 8 + c8) = kcl;
+        *reinterpret_cast<f16x8*>(krow + M + 8 + c8) = kcl;
       }
       // base-2 quantities: token bias b = -log2e * sum_c w_c phi_c; self score
       // t_ii and the upper bound U of any score in this query's row (without
