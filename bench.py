@@ -32,6 +32,9 @@ CONFIGS = {
 }
 PEAK_FP16_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
 PEAK_HBM_GBS = 8000.0
+# v_exp_f32 throughput measured on the box: 128 exps x 64 lanes per 475 ns per
+# SIMD (two waves), x 1024 SIMDs
+PEAK_EXP_PER_S = 17.7e12
 
 
 def log(*a):
@@ -60,6 +63,26 @@ def step_flops(B, N, D, H, m, causal):
     f_fwd = 2.0 * T * D * (HM + D) + 2.0 * P * (m + dv)
     f_bwd = 4.0 * T * D * (HM + D) + 2.0 * P * (3 * m + 2 * dv)
     return f_fwd, f_bwd
+
+
+def compulsory_bytes(B, N, D, H, m):
+    """HBM bytes the step cannot avoid: fwd reads X and the weights and writes
+    out and lse; bwd reads dO, X, out, lse and the weights and writes dX and
+    the weight gradients (fp16 tensors, fp32 lse)."""
+    x = B * N * D * 2
+    wts = (D * H * m + D * D + 2 * H * m) * 2
+    lse = B * H * N * 4
+    fwd = x + wts + x + lse
+    bwd = 3 * x + lse + wts + x + wts
+    return fwd, bwd
+
+
+def roofline_terms(flops, exps, nbytes):
+    """Time bounds (ms) of one pass: MFMA, exp2 and HBM; the largest binds."""
+    t = {"mfma": flops / (PEAK_FP16_TFLOPS * 1e12) * 1e3, "exp": exps / PEAK_EXP_PER_S * 1e3,
+         "hbm": nbytes / (PEAK_HBM_GBS * 1e9) * 1e3}
+    bound = max(t, key=t.get)
+    return bound, {k: round(v, 4) for k, v in t.items()}
 
 
 def make_inputs(cfg, device):
@@ -212,6 +235,9 @@ def main():
     dom_flops = kernel_flops(dominant, B, N, D, H, m, causal)
     achieved = dom_flops / (dom_avg * 1e-3) / 1e12
     f_fwd, f_bwd = step_flops(B, N, D, H, m, causal)
+    b_fwd, _ = compulsory_bytes(B, N, D, H, m)
+    bound, terms = roofline_terms(f_fwd, pairs(B, N, H, causal), b_fwd)
+    fwd_roof = {"bound": bound, "terms_ms": terms, "frac": round(terms[bound] / ms_fwd, 4)}
     for k, v in sorted(kernels.items(), key=lambda kv: -kv[1]["avg_ms"]):
         log(f"  {k:18s} {v['avg_ms']:8.4f} ms  x{v['launches_per_step']:.0f}/step  {v['tflops']} TFLOP/s")
     log(f"step {ms_step:.4f} ms  fwd {ms_fwd:.4f} ms  step-level {(f_fwd + f_bwd) / (ms_step * 1e-3) / 1e12:.1f} "
@@ -235,6 +261,7 @@ def main():
         "fwd_ms": round(ms_fwd, 4),
         "fwd_tokens_per_s": round(B * N / (ms_fwd * 1e-3), 1),
         "step_roofline_frac": round((f_fwd + f_bwd) / 2.5e15 / (ms_step * 1e-3), 4),
+        "fwd_roofline": fwd_roof,
         "roofline": {"bound": "mfma", "kernel": dominant, "achieved": round(achieved, 2),
                      "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
                      "traffic": load_traffic(dominant, args.config)},
