@@ -11,7 +11,10 @@ names, default initialisation and errors. Differences, all deliberate:
 * the Function calls ``forward_train`` / ``backward_train``, which carry the
   forward's projection workspace to the backward instead of recomputing it;
   the reference ops ``forward`` / ``backward`` remain available with their
-  original schemas (``backward`` then recomputes the projection).
+  original schemas (``backward`` then recomputes the projection);
+* the op ``forward`` is itself differentiable (``torch.library.register_autograd``,
+  backward through the reference-schema ``backward`` op), and every op has a
+  fake, so ``torch.compile`` traces the module without graph breaks.
 """
 
 from __future__ import annotations
@@ -52,6 +55,33 @@ def _morpho_backward_fake(grad_out, X, W_phi, gate_q, gate_k, W_V, out, lse, H, 
 def _morpho_backward_train_fake(grad_out, X, W_phi, gate_q, gate_k, W_V, out, lse, workspace, H, cube_m, scale,
                                 causal):
     return _grads_fake(X, W_phi, gate_q, gate_k, W_V)
+
+
+# Autograd of the reference-schema op itself, so that
+# torch.ops.morphottention.forward is differentiable without the Function
+# (torch.compile / AOT autograd trace it through the fakes above). Its backward
+# is the reference-schema ``backward`` op, which recomputes the projection; lse
+# is treated as a non-differentiable statistic (its gradient is ignored).
+def _forward_setup_context(ctx, inputs, output):
+    x, W_phi, gate_q, gate_k, W_V, H, cube_m, scale, causal = inputs
+    out, lse = output
+    ctx.save_for_backward(x, W_phi, gate_q, gate_k, W_V, out, lse)
+    ctx.meta = (H, cube_m, scale, causal)
+
+
+def _forward_backward(ctx, grads):
+    grad_out = grads[0]
+    x, W_phi, gate_q, gate_k, W_V, out, lse = ctx.saved_tensors
+    H, cube_m, scale, causal = ctx.meta
+    if grad_out is None:
+        grad_out = torch.zeros_like(out)
+    dX, dW_phi, d_gate_q, d_gate_k, dW_V = ops.backward(grad_out.contiguous(), x, W_phi, gate_q, gate_k, W_V, out,
+                                                        lse, H, cube_m, scale, causal)
+    return dX, dW_phi, d_gate_q, d_gate_k, dW_V, None, None, None, None
+
+
+torch.library.register_autograd(add_op_namespace_prefix("forward"), _forward_backward,
+                                setup_context=_forward_setup_context)
 
 
 class MorphoAttentionFunction(torch.autograd.Function):

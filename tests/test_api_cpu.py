@@ -156,3 +156,43 @@ def test_raw_op_on_cpu_tensors_is_not_silently_computed():
     V = torch.randn(64, 64, dtype=torch.float16)
     with pytest.raises((NotImplementedError, RuntimeError)):
         torch.ops.morphottention.forward(X, W, g, g, V, 2, 16, 1.0, False)
+
+
+def test_forward_op_is_differentiable_under_fake_tensors():
+    """torch.ops.morphottention.forward carries its own autograd formula (the
+    reference-schema backward op); under fake tensors the graph forms and
+    every differentiable input receives a gradient of its own shape."""
+    import morphottention_amd  # noqa: F401
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    with FakeTensorMode():
+        B, N, D, H, m = 2, 64, 128, 2, 16
+        x = torch.empty(B, N, D, dtype=torch.float16).requires_grad_()
+        W = torch.empty(D, H * m, dtype=torch.float16).requires_grad_()
+        gq = torch.empty(H, m, dtype=torch.float16).requires_grad_()
+        gk = torch.empty(H, m, dtype=torch.float16).requires_grad_()
+        V = torch.empty(D, D, dtype=torch.float16).requires_grad_()
+        out, lse = torch.ops.morphottention.forward(x, W, gq, gk, V, H, m, 1.0, True)
+        assert out.grad_fn is not None
+        out.sum().backward()
+        for t in (x, W, gq, gk, V):
+            assert t.grad is not None and t.grad.shape == t.shape
+
+
+def test_multihead_self_attention_wrapper_contract():
+    """attn-bench's MultiHeadSelfAttention (attn-bench/src/layers/attention/
+    morpho_attention.py:9-41): constructor defaults, attributes, parameters."""
+    from morphottention_amd.layers import MultiHeadSelfAttention
+    layer = MultiHeadSelfAttention(256, 4)
+    assert layer.name == "morpho_attention"
+    assert (layer.num_heads, layer.head_dim, layer.cube_m, layer.causal) == (4, 64, 64, False)
+    assert layer.scale == 64 ** -0.5
+    assert MultiHeadSelfAttention.HEAD_DIM == 64 and MultiHeadSelfAttention.CUBE_M == 64
+    assert set(dict(layer.named_parameters())) == {"attn.W_phi", "attn.gate_q", "attn.gate_k", "attn.W_V",
+                                                   "proj.weight", "proj.bias"}
+    assert layer.attn.W_phi.dtype == torch.float16 and layer.proj.weight.dtype == torch.float32
+    layer2 = MultiHeadSelfAttention(128, 2, 0.1, cube_m=16, scale=0.5, causal=True, unused_option=3)
+    assert (layer2.cube_m, layer2.scale, layer2.causal) == (16, 0.5, True)
+    assert layer2.attn.W_phi.shape == (128, 32) and layer2.dropout.p == 0.1
+    x = torch.randn(1, 8, 128)
+    with pytest.raises(ValueError, match="CUDA tensor"):
+        layer2(x, x, x)
