@@ -152,6 +152,47 @@ def cpu_baseline(cfg, budget_s=20.0):
     }
 
 
+def bench_layer(args):
+    """fwd+bwd of morphottention_amd.layers.MultiHeadSelfAttention on fp32
+    activations at a config's shape: the attn-bench caller (fp16 casts around
+    the fused op, then the fp32 output projection). One JSON line."""
+    from morphottention_amd.layers import MultiHeadSelfAttention
+    B, N, D, H, m, scale, causal, seed, xm = CONFIGS[args.config]
+    dev = torch.device("cuda:0")
+    torch.manual_seed(seed)
+    layer = MultiHeadSelfAttention(D, H, cube_m=m, scale=scale, causal=causal).to(dev)
+    x = (xm * torch.randn(B, N, D, device=dev)).requires_grad_(True)
+    dout = torch.randn(B, N, D, device=dev)
+    leaves = [x, *layer.parameters()]
+
+    def step():
+        out, _ = layer(x, x, x)
+        return torch.autograd.grad(out, leaves, dout)
+
+    for _ in range(args.warmup):
+        step()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    f_fwd, f_bwd = step_flops(B, N, D, H, m, causal)
+    f_proj = 3 * 2.0 * B * N * D * D  # output projection: forward and both backward products
+    log(f"layer step {ms:.4f} ms ({(f_fwd + f_bwd + f_proj) / (ms * 1e-3) / 1e12:.1f} TFLOP/s incl. projection)")
+    print(json.dumps({
+        "metric": "MultiHeadSelfAttention fwd+bwd tokens/s (attn-bench caller, fp32 activations)",
+        "value": round(B * N / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp16 attention, fp32 projection", "data": "synthetic",
+        "config": {"workload": f"{args.config} shape through MultiHeadSelfAttention", "global_batch": B,
+                   "seq_len": N},
+        "step_tflops_incl_projection": round((f_fwd + f_bwd + f_proj) / (ms * 1e-3) / 1e12, 1),
+    }), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -161,6 +202,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--timing-steps", type=int, default=5, help="steps re-run with per-kernel HIP events")
     ap.add_argument("--calib-copy", action="store_true", help="run one 256 MiB copy first (PMC calibration)")
+    ap.add_argument("--layer", choices=["mhsa"], default=None,
+                    help="time the attn-bench MultiHeadSelfAttention layer (fp32 in/out) instead of the bare op")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; the path is sharded over "
@@ -172,6 +215,8 @@ def main():
 
     from morphottention_amd import MorphoAttentionFunction, capi
 
+    if args.layer:
+        return bench_layer(args)
     cfg = CONFIGS[args.config]
     B, N, D, H, m, scale, causal, seed, xm = cfg
     dev = torch.device("cuda:0")
