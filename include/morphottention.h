@@ -9,6 +9,7 @@
  *
  * Differences from the reference launchers, all deliberate:
  *   - `causal` is honoured at run time (the reference drops it, attention.cpp:46-54);
+ *     its other bits select the reference's compile-time variants (see morpho_mode);
  *   - cube_m in {16, 32, 64} and head_dim_v = D / H in {32, 64, 128} are accepted
  *     (the reference accepts only 64 / 64, attention.cu:494,535);
  *   - the backward returns the complete gradient, including the query-side code
@@ -40,6 +41,20 @@ extern "C" {
 
 typedef struct ihipStream_t* morpho_stream_t; /* identical to hipStream_t */
 
+/* Bits of the `causal` argument of morpho_forward / morpho_backward. 0 and 1
+ * keep their plain meaning (non-causal / causal, sigmoid cube projection, the
+ * diagonal kept). The other bits select variants that the reference defines
+ * at compile time but never wires: MASK_DIAG (declarations.cuh:79-82) drops
+ * key j == query i; HardTanh01 (phi = clamp((z + 1) / 2, 0, 1)) and Identity
+ * (phi = z) replace the sigmoid cube projection (cube.cuh:9-17,29-35). Pass
+ * the same bits to the backward as to the forward. */
+enum morpho_mode {
+  MORPHO_MODE_CAUSAL = 1,
+  MORPHO_MODE_MASK_DIAG = 2,
+  MORPHO_MODE_PROJ_HARDTANH01 = 4,
+  MORPHO_MODE_PROJ_IDENTITY = 8
+};
+
 enum morpho_status {
   MORPHO_OK = 0,
   MORPHO_ERR_INVALID_ARGUMENT = 1, /* bad shape, null pointer, unsupported size */
@@ -67,7 +82,8 @@ size_t morpho_forward_workspace_size(int64_t B, int64_t N, int64_t D, int64_t H,
 /* Forward. Replaces attention_forward_kernel_launcher (attention.cuh:28-31) and
  * the launch part of morpho_forward (attention.cpp:15-57).
  * Writes out [B, N, D] (float16) and lse [B*H, N] (float32, base 2;
- * -FLT_MAX for a row without unmasked keys, which cannot occur for N >= 1). */
+ * -FLT_MAX, with out = 0, for a row without unmasked keys: only query 0 under
+ * MORPHO_MODE_CAUSAL | MORPHO_MODE_MASK_DIAG, or N = 1 with MASK_DIAG). */
 int morpho_forward(const void* X, const void* W_phi, const void* gate_q, const void* gate_k, const void* W_V,
                    void* out, float* lse, int64_t B, int64_t N, int64_t D, int64_t H, int64_t cube_m, float scale,
                    int causal, void* workspace, size_t workspace_bytes, morpho_stream_t stream);

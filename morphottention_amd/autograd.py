@@ -35,7 +35,7 @@ def _morpho_forward_fake(X, W_phi, gate_q, gate_k, W_V, H, cube_m, scale, causal
 
 
 @torch.library.register_fake(add_op_namespace_prefix("forward_train"))
-def _morpho_forward_train_fake(X, W_phi, gate_q, gate_k, W_V, H, cube_m, scale, causal):
+def _morpho_forward_train_fake(X, W_phi, gate_q, gate_k, W_V, H, cube_m, scale, causal, variant=0):
     B, N, D = X.shape
     ws = X.new_empty((capi.forward_workspace_size(B, N, D, H, cube_m),), dtype=torch.uint8)
     return [torch.empty_like(X), X.new_empty((B * H, N), dtype=torch.float32), ws]
@@ -53,7 +53,7 @@ def _morpho_backward_fake(grad_out, X, W_phi, gate_q, gate_k, W_V, out, lse, H, 
 
 @torch.library.register_fake(add_op_namespace_prefix("backward_train"))
 def _morpho_backward_train_fake(grad_out, X, W_phi, gate_q, gate_k, W_V, out, lse, workspace, H, cube_m, scale,
-                                causal):
+                                causal, variant=0):
     return _grads_fake(X, W_phi, gate_q, gate_k, W_V)
 
 
@@ -84,20 +84,37 @@ torch.library.register_autograd(add_op_namespace_prefix("forward"), _forward_bac
                                 setup_context=_forward_setup_context)
 
 
+# Variant bits of the *_train ops (the C ABI's morpho_mode without the causal
+# bit): the reference's compile-time MASK_DIAG (declarations.cuh:79-82) and
+# cube projections (cube.cuh:9-17), which it never wires to its API.
+_MASK_DIAG = 2
+_PROJECTIONS = {"sigmoid": 0, "hardtanh01": 4, "identity": 8}
+
+
+def variant_bits(projection: str = "sigmoid", mask_diag: bool = False) -> int:
+    """Variant argument for ``forward_train`` / ``backward_train``."""
+    if projection not in _PROJECTIONS:
+        raise ValueError(f"projection must be one of {sorted(_PROJECTIONS)} (got {projection!r})")
+    return _PROJECTIONS[projection] | (_MASK_DIAG if mask_diag else 0)
+
+
 class MorphoAttentionFunction(torch.autograd.Function):
-    """Bridges the HIP attention kernels into autograd."""
+    """Bridges the HIP attention kernels into autograd. The optional trailing
+    ``variant`` (see :func:`variant_bits`) defaults to the reference's
+    behaviour: sigmoid projection, diagonal kept."""
 
     @staticmethod
-    def forward(ctx, x, W_phi, gate_q, gate_k, W_V, H, cube_m, scale, causal):
+    def forward(ctx, x, W_phi, gate_q, gate_k, W_V, H, cube_m, scale, causal, variant=0):
         if not x.is_cuda:
             raise ValueError("MorphoAttention expects a CUDA tensor")
         x = x.contiguous()
-        out, lse, ws = ops.forward_train(x, W_phi, gate_q, gate_k, W_V, H, cube_m, scale, causal)
+        out, lse, ws = ops.forward_train(x, W_phi, gate_q, gate_k, W_V, H, cube_m, scale, causal, variant)
         ctx.save_for_backward(x, W_phi, gate_q, gate_k, W_V, out, lse, ws)
         ctx.H = H
         ctx.cube_m = cube_m
         ctx.scale = scale
         ctx.causal = causal
+        ctx.variant = variant
         return out
 
     @staticmethod
@@ -105,8 +122,9 @@ class MorphoAttentionFunction(torch.autograd.Function):
         x, W_phi, gate_q, gate_k, W_V, out, lse, ws = ctx.saved_tensors
         grad_out = grad_out.contiguous()
         dX, dW_phi, d_gate_q, d_gate_k, dW_V = ops.backward_train(
-            grad_out, x, W_phi, gate_q, gate_k, W_V, out, lse, ws, ctx.H, ctx.cube_m, ctx.scale, ctx.causal)
-        return dX, dW_phi, d_gate_q, d_gate_k, dW_V, None, None, None, None
+            grad_out, x, W_phi, gate_q, gate_k, W_V, out, lse, ws, ctx.H, ctx.cube_m, ctx.scale, ctx.causal,
+            ctx.variant)
+        return dX, dW_phi, d_gate_q, d_gate_k, dW_V, None, None, None, None, None
 
 
 class MorphoAttention(nn.Module):
@@ -118,13 +136,22 @@ class MorphoAttention(nn.Module):
         16, 32 or 64.
     :param scale: softmax temperature.
     :param causal: whether to apply causal masking.
+    :param projection: cube projection ``"sigmoid"`` (the reference's
+        default), ``"hardtanh01"`` or ``"identity"`` (the reference's unwired
+        compile-time variants).
+    :param mask_diag: drop each query's own key (the reference's unwired
+        ``MASK_DIAG``).
     """
 
     def __init__(self, dim: int, num_heads: int, cube_m: int, *, scale: float = 1.0, causal: bool = False,
-                 dtype: torch.dtype = torch.float16, device: torch.device | str | None = None) -> None:
+                 dtype: torch.dtype = torch.float16, device: torch.device | str | None = None,
+                 projection: str = "sigmoid", mask_diag: bool = False) -> None:
         super().__init__()
         if dim % num_heads != 0:
             raise ValueError(f"dim ({dim}) must be divisible by num_heads ({num_heads})")
+        self.variant = variant_bits(projection, mask_diag)
+        self.projection = projection
+        self.mask_diag = mask_diag
         self.dim = dim
         self.num_heads = num_heads
         self.cube_m = cube_m
@@ -147,14 +174,17 @@ class MorphoAttention(nn.Module):
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         return MorphoAttentionFunction.apply(x, self.W_phi, self.gate_q, self.gate_k, self.W_V, self.num_heads,
-                                             self.cube_m, self.scale, self.causal)
+                                             self.cube_m, self.scale, self.causal, self.variant)
 
 
 def morpho_attention(x, W_phi, gate_q, gate_k, W_V, num_heads: int, cube_m: int, *, scale: float = 1.0,
-                     causal: bool = False) -> torch.Tensor:
+                     causal: bool = False, projection: str = "sigmoid", mask_diag: bool = False) -> torch.Tensor:
     """Apply Morphottention attention with autograd support.
 
     :param x: input activations of shape (B, N, D) on a ROCm device.
+    :param projection: ``"sigmoid"`` (default), ``"hardtanh01"`` or ``"identity"``.
+    :param mask_diag: drop each query's own key.
     :returns: the attention output, differentiable w.r.t. ``x`` and the parameters.
     """
-    return MorphoAttentionFunction.apply(x, W_phi, gate_q, gate_k, W_V, num_heads, cube_m, scale, causal)
+    return MorphoAttentionFunction.apply(x, W_phi, gate_q, gate_k, W_V, num_heads, cube_m, scale, causal,
+                                         variant_bits(projection, mask_diag))

@@ -69,6 +69,8 @@ int make_dims(int64_t B, int64_t N, int64_t D, int64_t H, int64_t M, float scale
   if (T > (int64_t)1 << 30 || D > 65536 || H * M > 65536)
     return fail(MORPHO_ERR_INVALID_ARGUMENT, "problem too large for 32-bit token indexing");
   if (!(scale == scale)) return fail(MORPHO_ERR_INVALID_ARGUMENT, "scale must be a finite number");
+  if ((causal & ~15) != 0 || (causal & 12) == 12)
+    return fail(MORPHO_ERR_INVALID_ARGUMENT, "invalid mode bits 0x%x (causal | mask_diag | one projection)", causal);
   d.B = (int)B;
   d.N = (int)N;
   d.NP = (int)((N + 63) / 64 * 64);
@@ -80,7 +82,11 @@ int make_dims(int64_t B, int64_t N, int64_t D, int64_t H, int64_t M, float scale
   d.HM = (int)(H * M);
   d.CW = 2 * (int)M + 8;
   d.scale = scale;
-  d.causal = causal ? 1 : 0;
+  d.causal = causal & MORPHO_MODE_CAUSAL ? 1 : 0;
+  d.mask_diag = causal & MORPHO_MODE_MASK_DIAG ? 1 : 0;
+  d.proj = causal & MORPHO_MODE_PROJ_HARDTANH01 ? kProjHardTanh01
+           : causal & MORPHO_MODE_PROJ_IDENTITY ? kProjIdentity
+                                                : kProjSigmoid;
   // projection tiles: 320 columns when that divides H*M + D, else 256; the
   // interleaved column order needs whole heads and 8-column pieces per tile
   const int NC = d.HM + d.D;

@@ -100,12 +100,21 @@ __device__ __forceinline__ f16x4 frag4_kcontig(const f16* tile, int stride, int 
   return *reinterpret_cast<const f16x4*>(tile + row * stride + k0 + 4 * (lane >> 5));
 }
 
-// Split x into two halves with hi + lo == x to ~2^-22 relative; |x| is clamped
-// to 60000 so neither part overflows.
-__device__ __forceinline__ void split_hi_lo(float x, f16& hi, f16& lo) {
-  x = fminf(fmaxf(x, -60000.f), 60000.f);
+// hi = fp16(x), lo = fp16(x - hi): hi + lo carries x to ~2^-22. The pair is
+// only consistent if hi and lo are formed from one and the same fp32 x, so x
+// is made opaque to the compiler: it may otherwise evaluate x twice (e.g. a
+// product once fused into the subtraction, once rounded, or a branch
+// duplicated), and at an exact fp16 rounding tie the two evaluations land on
+// different sides (hi + lo then misses x by one fp16 ulp). The fp16
+// conversions themselves (v_cvt_f16_f32, v_cvt_pk_f16_f32) round ties alike.
+__device__ __forceinline__ void split_exact(float x, f16& hi, f16& lo) {
+  asm("" : "+v"(x));  // not volatile: an opaque copy, free to be scheduled
   hi = (f16)x;
   lo = (f16)(x - (float)hi);
+}
+// as split_exact, with x clamped to the fp16 range first
+__device__ __forceinline__ void split_hi_lo(float x, f16& hi, f16& lo) {
+  split_exact(fminf(fmaxf(x, -60000.f), 60000.f), hi, lo);
 }
 
 __device__ __forceinline__ f16x8 pack8(const f32x16& v, int base) {
@@ -154,6 +163,22 @@ __device__ __forceinline__ void wait_vmcnt_lgkm0() {
   __builtin_amdgcn_s_waitcnt((CNT & 15) | (7 << 4) | (0 << 8) | ((CNT >> 4) << 14));
 }
 
-__device__ __forceinline__ float sigmoidf_(float z) { return 1.0f / (1.0f + __expf(-z)); }
+// 1 / (1 + e^-z) with the hardware reciprocal (1 ulp; the argument is >= 1
+// or +inf, whose reciprocal is 0) instead of the ten-instruction IEEE division
+__device__ __forceinline__ float sigmoidf_(float z) { return __builtin_amdgcn_rcpf(1.0f + __expf(-z)); }
+
+// Cube projection phi(z) and its derivative written in terms of phi: sigmoid,
+// phi (1 - phi); clamp((z + 1) / 2, 0, 1), 1/2 where the clamp is inactive
+// (0 < phi < 1, i.e. -1 < z < 1); identity, 1. `proj` is uniform.
+__device__ __forceinline__ float cube_project(float z, int proj) {
+  if (proj == 0) return sigmoidf_(z);
+  if (proj == 1) return fminf(1.0f, fmaxf(0.0f, 0.5f * (z + 1.0f)));
+  return z;
+}
+__device__ __forceinline__ float cube_project_grad(float phi, int proj) {
+  if (proj == 0) return phi * (1.0f - phi);
+  if (proj == 1) return (phi > 0.0f && phi < 1.0f) ? 0.5f : 0.0f;
+  return 1.0f;
+}
 
 }  // namespace morpho

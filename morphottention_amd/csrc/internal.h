@@ -7,14 +7,20 @@
 
 namespace morpho {
 
+// Cube projections phi(z) (cube.cuh:9-17 of the reference): sigmoid (the
+// default), clamp((z + 1) / 2, 0, 1), and z itself.
+constexpr int kProjSigmoid = 0, kProjHardTanh01 = 1, kProjIdentity = 2;
+
 struct Dims {
   int B, N, D, H, M, DV;  // batch, tokens, model dim, heads, cube_m, head_dim_v
   int NP;                 // N rounded up to a multiple of 64: row length of the V^T layout
   int64_t T;              // B * N tokens
   int HM;                 // H * M projection columns
-  int CW;                 // 3 * M + 8: code row width (hi/lo split codes + affine augmentation)
+  int CW;                 // 2 * M + 8: code row width (hi/lo split codes + affine augmentation)
   float scale;
   int causal;
+  int mask_diag;          // drop key j == query i
+  int proj;               // cube projection: kProjSigmoid, kProjHardTanh01 or kProjIdentity
   // Column order of the forward projection's B operand (wt rows): tiles of
   // PBN columns; when PCPT > 0 tile j holds code columns [j PCPT, (j+1) PCPT)
   // then value columns [j PVPT, (j+1) PVPT), so every tile does the same

@@ -141,7 +141,8 @@ struct FwdCfg {
 // finished before that barrier), so each tile has NSTAGE - 1 tiles of compute
 // to arrive; one barrier per tile.
 // MAXPASS: key tiles only, track the row max of the exponent (exact path).
-template <int M, int DV, bool MAXPASS>
+// MD: the diagonal (key == query) is masked.
+template <int M, int DV, bool MAXPASS, bool MD>
 __device__ __forceinline__ void fwd_pass(const f16* __restrict__ ka, const f16* __restrict__ vt,
                                          const uint8_t* __restrict__ vlo, int64_t rowbase, int64_t vbase,
                                          int N, int NP, int causal, int kend, int q0, int qw0,
@@ -314,11 +315,12 @@ __device__ __forceinline__ void fwd_pass(const f16* __restrict__ ka, const f16* 
         const int qb0 = qw0 + 32 * qb;
         if (causal && kbase > qb0 + 31) continue;  // wave-uniform
         f32x16 sc = score(kf, kx, qb);
-        if ((kbase + 31 >= N) || (causal && kbase + 31 > qb0)) {
+        if ((kbase + 31 >= N) || (causal && kbase + 31 > qb0) ||
+            (MD && kbase <= qb0 + 31 && kbase + 31 >= qb0)) {
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int key = kbase + swap23(acc_row(r, lane));
-            if (key >= N || (causal && key > qb0 + l32)) sc[r] = kNegInf;
+            if (key >= N || (causal && key > qb0 + l32) || (MD && key == qb0 + l32)) sc[r] = kNegInf;
           }
         }
         if (MAXPASS) {
@@ -357,7 +359,9 @@ __device__ __forceinline__ void fwd_pass(const f16* __restrict__ ka, const f16* 
   issue_upto(1);
   if (!MAXPASS) {
     // ---- tiles whose 64 keys are unmasked for every query of the workgroup
-    const int nfull = min(nkt, (causal ? q0 : N) / C::KT);
+    // (with the diagonal masked, the tiles from the workgroup's first query on
+    // take the masked path)
+    const int nfull = min(nkt, ((causal || MD) ? q0 : N) / C::KT);
     for (; t < nfull; ++t) {
       publish(t);
       issue_upto(t + C::NSTAGE - 1);
@@ -427,7 +431,7 @@ __device__ __forceinline__ void fwd_pass(const f16* __restrict__ ka, const f16* 
   }
 }
 
-template <int M, int DV>
+template <int M, int DV, bool MD>
 __global__ __launch_bounds__((64 * FwdCfg<M, DV>::WAVES))
 __attribute__((amdgpu_waves_per_eu(FwdCfg<M, DV>::WAVES_PER_EU, FwdCfg<M, DV>::WAVES_PER_EU)))
 void attn_fwd_kernel(f16* __restrict__ qa, const f16* __restrict__ ka, const f16* __restrict__ vt,
@@ -488,18 +492,18 @@ void attn_fwd_kernel(f16* __restrict__ qa, const f16* __restrict__ ka, const f16
       qa0[qb] = qaug[qb];
       if (h32 == 0) { qa0[qb][2] = (f16)0.f; qa0[qb][3] = (f16)0.f; }
     }
-    fwd_pass<M, DV, true>(ka, vt, vlo, rowbase, vbase, N, NP, causal, kend, q0, qw0, smem, qf, qa0, o, lsum, rmax);
+    fwd_pass<M, DV, true, MD>(ka, vt, vlo, rowbase, vbase, N, NP, causal, kend, q0, qw0, smem, qf, qa0, o, lsum, rmax);
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
       const float m = fmaxf(rmax[qb], __shfl_xor(rmax[qb], 32));
-      R[qb] = qw0 + 32 * qb + l32 < N ? m : 0.f;
+      R[qb] = (qw0 + 32 * qb + l32 < N && m > kNegInf) ? m : 0.f;  // a row without keys keeps 0
       f16 rh, rl;
       split_hi_lo(-R[qb], rh, rl);
       if (h32 == 0) { qaug[qb][2] = rh; qaug[qb][3] = rl; }
     }
     __syncthreads();  // every wave is done with the stages before they are refilled
   }
-  fwd_pass<M, DV, false>(ka, vt, vlo, rowbase, vbase, N, NP, causal, kend, q0, qw0, smem, qf, qaug, o, lsum, rmax);
+  fwd_pass<M, DV, false, MD>(ka, vt, vlo, rowbase, vbase, N, NP, causal, kend, q0, qw0, smem, qf, qaug, o, lsum, rmax);
 
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
@@ -521,9 +525,10 @@ void attn_fwd_kernel(f16* __restrict__ qa, const f16* __restrict__ ka, const f16
         const float l2 = ltot > 0.f ? R[qb] + fast_log2(ltot) : -kFltMax;  // lse - b
         lse[rowbase + q] = ltot > 0.f ? l2 + ts[qb].x : -kFltMax;
         // the query row's affine block becomes the backward's {1, 1, -(lse - b)}:
-        // this wave was its only reader
+        // this wave was its only reader (0 for a row without keys, whose
+        // scores the backward masks)
         f16 bh_, bl_;
-        split_hi_lo(-l2, bh_, bl_);
+        split_hi_lo(ltot > 0.f ? -l2 : 0.f, bh_, bl_);
         *reinterpret_cast<f16x2*>(qa + (rowbase + q) * C::CW + M + 2) = f16x2{bh_, bl_};
       }
     }
@@ -534,8 +539,12 @@ template <int M, int DV>
 static hipError_t launch_attn_fwd_t(const Dims& d, const ProjBuffers& p, f16* out, float* lse, hipStream_t s) {
   using C = FwdCfg<M, DV>;
   const dim3 grid(xcd_grid((d.N + C::QW - 1) / C::QW, d.B * d.H));
-  hipLaunchKernelGGL((attn_fwd_kernel<M, DV>), grid, dim3(64 * C::WAVES), 0, s, p.qa, p.ka, p.vt, p.vlo, p.tstat, out, lse,
-                     d.N, d.NP, d.H, d.D, d.B * d.H, d.causal);
+  if (d.mask_diag)
+    hipLaunchKernelGGL((attn_fwd_kernel<M, DV, true>), grid, dim3(64 * C::WAVES), 0, s, p.qa, p.ka, p.vt, p.vlo,
+                       p.tstat, out, lse, d.N, d.NP, d.H, d.D, d.B * d.H, d.causal);
+  else
+    hipLaunchKernelGGL((attn_fwd_kernel<M, DV, false>), grid, dim3(64 * C::WAVES), 0, s, p.qa, p.ka, p.vt, p.vlo,
+                       p.tstat, out, lse, d.N, d.NP, d.H, d.D, d.B * d.H, d.causal);
   return hipGetLastError();
 }
 
@@ -596,7 +605,8 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(const f16* __restrict__ g
     *reinterpret_cast<f16x8*>(aug + bhn * 8) = f16x8{dh, dl, zero, zero, zero, zero, zero, zero};
     if (write_q) {
       f16 lh, ll;
-      split_hi_lo(-(lse[bhn] - tstat[bhn].x), lh, ll);
+      const float l = lse[bhn];
+      split_hi_lo(l > -kFltMax ? -(l - tstat[bhn].x) : 0.f, lh, ll);  // a row without keys: masked anyway
       *reinterpret_cast<f16x2*>(qa + bhn * CW + M + 2) = f16x2{lh, ll};
     }
   }
@@ -711,7 +721,7 @@ struct BwdCfg {
 // holds {1, 1, -(lse - b)} by now (written by the forward, or by bwd_prep when
 // the backward computed the projection itself); the dO rows come from
 // grad_out and their affine block {-delta} from bwd_prep's aug rows.
-template <int M, int DV>
+template <int M, int DV, bool MD>
 __global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ qa, const f16* __restrict__ ka,
                                                        const f16* __restrict__ vt, const f16* __restrict__ aug,
                                                        const f16* __restrict__ grad_out, float* __restrict__ dq,
@@ -979,12 +989,20 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ q
 #pragma unroll
         for (int c = 0; c < DV / 16; ++c) dp = mfma16(*reinterpret_cast<const f16x8*>(osb + r_o[c]), vf[c], dp);
         dp = mfma8(*reinterpret_cast<const f16x4*>(tA + 32 * sb * 16 + r_oa), vaug, dp);
-        const bool need_mask = (q0 + 32 > N) || (kw0 + 31 >= N) || (causal && kw0 + 31 > q0);
+        const bool need_mask = (q0 + 32 > N) || (kw0 + 31 >= N) || (causal && kw0 + 31 > q0) ||
+                               (MD && kw0 <= q0 + 31 && kw0 + 31 >= q0);
         if (need_mask) {  // wave-uniform; masked scores become -inf (P = 0)
+          // one select per score from a mask built with bitwise operators:
+          // written as a conditional store after a short-circuit ||, the
+          // MD instances compiled to divergent blocks whose stores were
+          // dropped for in-range lanes (causal and diagonal masks lost)
+          const int kx = kvalid ? key : (1 << 30);  // a key past N exceeds every limit
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int qq = q0 + swap23(acc_row(r, lane));
-            if (qq >= N || !kvalid || (causal && key > qq)) s[r] = kNegInf;
+            const int klim = causal ? qq : N - 1;  // the largest key this query sees
+            const bool drop = (qq >= N) | (kx > klim) | (MD && kx == qq);
+            s[r] = drop ? kNegInf : s[r];
           }
         }
         f16x8 p16[2];
@@ -1057,8 +1075,12 @@ static hipError_t launch_attn_bwd_t(const Dims& d, const ProjBuffers& p, const f
                                     hipStream_t s) {
   using C = BwdCfg<M, DV>;
   const dim3 grid(xcd_grid((d.N + C::KW - 1) / C::KW, d.B * d.H));
-  hipLaunchKernelGGL((attn_bwd_kernel<M, DV>), grid, dim3(256), 0, s, p.qa, p.ka, p.vt, g.aug, grad_out, g.dq, g.dk,
-                     g.dcb, g.dzv, d.N, d.NP, d.H, d.D, d.HM, d.B * d.H, d.causal);
+  if (d.mask_diag)
+    hipLaunchKernelGGL((attn_bwd_kernel<M, DV, true>), grid, dim3(256), 0, s, p.qa, p.ka, p.vt, g.aug, grad_out, g.dq,
+                       g.dk, g.dcb, g.dzv, d.N, d.NP, d.H, d.D, d.HM, d.B * d.H, d.causal);
+  else
+    hipLaunchKernelGGL((attn_bwd_kernel<M, DV, false>), grid, dim3(256), 0, s, p.qa, p.ka, p.vt, g.aug, grad_out, g.dq,
+                       g.dk, g.dcb, g.dzv, d.N, d.NP, d.H, d.D, d.HM, d.B * d.H, d.causal);
   return hipGetLastError();
 }
 

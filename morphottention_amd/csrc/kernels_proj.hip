@@ -98,7 +98,9 @@ __device__ __forceinline__ uint2 vlo_pack8(const float (&r)[8]) {
   return make_uint2(w[0], w[1]);
 }
 
-template <int M, int DV, int BN>
+// GEN: a cube projection other than the sigmoid, or the masked diagonal (the
+// variants take the projection from d.proj and the exact row maximum)
+template <int M, int DV, int BN, bool GEN>
 __global__ __launch_bounds__(kGemmThreads) void proj_fwd_kernel(const f16* __restrict__ X,
                                                                const f16* __restrict__ gate_q,
                                                                const f16* __restrict__ gate_k, Dims d, ProjBuffers p) {
@@ -155,14 +157,24 @@ __global__ __launch_bounds__(kGemmThreads) void proj_fwd_kernel(const f16* __res
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const int c = c8 + e;
-          const float phi = sigmoidf_(z[c]);
+          const float phi = GEN ? cube_project(z[c], d.proj) : sigmoidf_(z[c]);
           const float G = (float)gate_q[h * M + c] * (float)gate_k[h * M + c];
           const float wgt = d.scale * G;
-          const float kc = c1 * G * phi;
-          phh[e] = (f16)phi;
-          phl[e] = (f16)(phi - (float)phh[e]);
-          kch[e] = (f16)kc;
-          kcl[e] = (f16)(kc - (float)kch[e]);
+          const float cg = c1 * G;
+          f16 a, b;
+          if (GEN) {  // HardTanh01's clamped fma could convert to fp16 in one rounding
+            split_exact(phi, a, b);
+            phh[e] = a;
+            phl[e] = b;
+          } else {  // a quotient: nothing to fuse the conversion with
+            phh[e] = (f16)phi;
+            phl[e] = (f16)(phi - (float)phh[e]);
+          }
+          // kc = cg phi: lo is the exact product minus hi, so hi + lo carries
+          // kc to ~2^-22 however the compiler rounds hi (it may convert the
+          // product to fp16 in one rounding, v_fma_mixlo_f16)
+          kch[e] = (f16)(cg * phi);
+          kcl[e] = (f16)__builtin_fmaf(cg, phi, -(float)kch[e]);
           sumb += wgt * phi;
           tii += wgt * phi * (2.f * phi - 1.f);
           U += fmaxf(0.f, wgt * (2.f * phi - 1.f));
@@ -175,18 +187,23 @@ __global__ __launch_bounds__(kGemmThreads) void proj_fwd_kernel(const f16* __res
       }
       // base-2 quantities: token bias b = -log2e * sum_c w_c phi_c; self score
       // t_ii and the upper bound U of any score in this query's row (without
-      // the row constant, which cancels in the softmax).
+      // the row constant, which cancels in the softmax). U bounds the row only
+      // for phi in [0, 1], and R >= U - 15 keeps the row's largest weight
+      // representable only while the diagonal term is in the row: the
+      // identity projection and the masked diagonal take the exact two-pass
+      // maximum (an infinite gap).
       const float bias = -kLog2e * sumb;
       const float t_ii = kLog2e * tii;
       const float Ub = kLog2e * U;
       const float R = fmaxf(t_ii, Ub - 15.f);
+      const float gap = (GEN && (d.proj == kProjIdentity || d.mask_diag)) ? kFltMax : Ub - t_ii;
       f16 rh, rl, bh_, bl_;
       split_hi_lo(-R, rh, rl);
       split_hi_lo(bias, bh_, bl_);
       const f16 one = (f16)1.f, zero = (f16)0.f;
       *reinterpret_cast<f16x8*>(qrow + M) = f16x8{one, one, rh, rl, zero, zero, zero, zero};
       *reinterpret_cast<f16x8*>(krow + M) = f16x8{bh_, bl_, one, one, zero, zero, zero, zero};
-      p.tstat[bhn] = make_float4(bias, R, Ub - t_ii, 0.f);
+      p.tstat[bhn] = make_float4(bias, R, gap, 0.f);
     }
     // values, transposed: vt[bh][dd][n] = V_hi, and the remainder V - V_hi as
     // e4m3 in vlo's tile-major, key-permuted rows. One item = one column x 8
@@ -211,7 +228,7 @@ __global__ __launch_bounds__(kGemmThreads) void proj_fwd_kernel(const f16* __res
           float vl[8];
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
-            const float x = src[e * SS];
+            const float x = src[e * SS];  // a value read from LDS: one evaluation for V_hi and the remainder
             vh[e] = (f16)x;
             vl[e] = x - (float)vh[e];
           }
@@ -250,12 +267,18 @@ template <int M, int DV>
 static hipError_t launch_proj_fwd_t(const Dims& d, const f16* X, const f16* gq, const f16* gk, const ProjBuffers& p,
                                     hipStream_t s) {
   const int NC = d.HM + d.D, nrows = (int)((d.T + kProjBM - 1) / kProjBM);
+  const bool gen = d.proj != kProjSigmoid || d.mask_diag;
+  const dim3 g320(gemm_tile_grid(nrows, NC / 320)), g256(gemm_tile_grid(nrows, (NC + 255) / 256));
   if (d.PBN == 320) {
-    hipLaunchKernelGGL((proj_fwd_kernel<M, DV, 320>), dim3(gemm_tile_grid(nrows, NC / 320)), dim3(kGemmThreads), 0,
-                       s, X, gq, gk, d, p);
+    if (gen)
+      hipLaunchKernelGGL((proj_fwd_kernel<M, DV, 320, true>), g320, dim3(kGemmThreads), 0, s, X, gq, gk, d, p);
+    else
+      hipLaunchKernelGGL((proj_fwd_kernel<M, DV, 320, false>), g320, dim3(kGemmThreads), 0, s, X, gq, gk, d, p);
   } else {
-    hipLaunchKernelGGL((proj_fwd_kernel<M, DV, 256>), dim3(gemm_tile_grid(nrows, (NC + 255) / 256)),
-                       dim3(kGemmThreads), 0, s, X, gq, gk, d, p);
+    if (gen)
+      hipLaunchKernelGGL((proj_fwd_kernel<M, DV, 256, true>), g256, dim3(kGemmThreads), 0, s, X, gq, gk, d, p);
+    else
+      hipLaunchKernelGGL((proj_fwd_kernel<M, DV, 256, false>), g256, dim3(kGemmThreads), 0, s, X, gq, gk, d, p);
   }
   return hipGetLastError();
 }
@@ -321,7 +344,7 @@ __global__ __launch_bounds__(256) void proj_bwd_elem_kernel(const f16* __restric
       for (int e = 0; e < 8; ++e) {
         const float phi = (float)ph[e] + (float)pl[e];
         const float dphi = sG[e] * (2.f * (dq[e] + dk[e]) - dcb);
-        dz[e] = (f16)(dphi * phi * (1.f - phi));
+        dz[e] = (f16)(dphi * cube_project_grad(phi, d.proj));
         sg[e] += phi * (2.f * dk[e] - dcb);
       }
       *reinterpret_cast<f16x8*>(g.dzv + t * NC + col) = dz;

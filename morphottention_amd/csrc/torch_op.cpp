@@ -1,7 +1,8 @@
 // torch.ops.morphottention.{forward, backward}: the reference op schemas
 // (packages/morphottention/csrc/cuda/binder.cpp:6-15) registered on the CUDA
-// dispatch key, which PyTorch-ROCm uses for HIP tensors, plus two variants used
-// by the autograd Function that carry the forward projection to the backward.
+// dispatch key, which PyTorch-ROCm uses for HIP tensors, plus two ops used by
+// the autograd Function that carry the forward projection to the backward and
+// take the variant bits (masked diagonal, cube projection).
 //
 // Checks and messages follow packages/morphottention/csrc/cuda/attention/attention.cpp:9-38,64-91.
 // Unlike the reference this layer sets a device guard (the reference launches
@@ -51,6 +52,15 @@ morpho_stream_t current_stream(const at::Tensor& X) {
   return reinterpret_cast<morpho_stream_t>(c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(X.device().index()).stream());
 }
 
+// The ABI's mode word: bit 0 causal, the other bits the variant
+// (MORPHO_MODE_MASK_DIAG, MORPHO_MODE_PROJ_*), which only the *_train ops take.
+int mode_of(bool causal, int64_t variant) {
+  TORCH_CHECK((variant & ~(int64_t)(MORPHO_MODE_MASK_DIAG | MORPHO_MODE_PROJ_HARDTANH01 | MORPHO_MODE_PROJ_IDENTITY)) == 0,
+              "variant must combine MORPHO_MODE_MASK_DIAG (2) with at most one of MORPHO_MODE_PROJ_HARDTANH01 (4) "
+              "and MORPHO_MODE_PROJ_IDENTITY (8), got ", variant);
+  return (causal ? MORPHO_MODE_CAUSAL : 0) | (int)variant;
+}
+
 void raise_on(int status, const char* what) {
   TORCH_CHECK(status == MORPHO_OK, "morphottention ", what, " failed (", morpho_status_string(status),
               "): ", morpho_last_error());
@@ -58,7 +68,8 @@ void raise_on(int status, const char* what) {
 
 std::vector<at::Tensor> forward_impl(const at::Tensor& X, const at::Tensor& W_phi, const at::Tensor& gate_q,
                                      const at::Tensor& gate_k, const at::Tensor& W_V, int64_t H, int64_t cube_m,
-                                     double scale, bool causal, bool keep_workspace) {
+                                     double scale, bool causal, int64_t variant, bool keep_workspace) {
+  const int mode = mode_of(causal, variant);
   const Shape s = check_inputs(X, W_phi, gate_q, gate_k, W_V, H, cube_m);
   const c10::hip::HIPGuardMasqueradingAsCUDA guard(X.device());
   auto out = at::empty_like(X);
@@ -68,8 +79,8 @@ std::vector<at::Tensor> forward_impl(const at::Tensor& X, const at::Tensor& W_ph
               "D / H must be 32, 64 or 128)");
   auto ws = at::empty({(int64_t)ws_bytes}, X.options().dtype(at::kByte));
   raise_on(morpho_forward(X.data_ptr(), W_phi.data_ptr(), gate_q.data_ptr(), gate_k.data_ptr(), W_V.data_ptr(),
-                          out.data_ptr(), lse.data_ptr<float>(), s.B, s.N, s.D, s.H, s.M, (float)scale,
-                          causal ? 1 : 0, ws.data_ptr(), ws_bytes, current_stream(X)),
+                          out.data_ptr(), lse.data_ptr<float>(), s.B, s.N, s.D, s.H, s.M, (float)scale, mode,
+                          ws.data_ptr(), ws_bytes, current_stream(X)),
            "forward");
   if (keep_workspace) return {out, lse, ws};
   return {out, lse};
@@ -78,7 +89,8 @@ std::vector<at::Tensor> forward_impl(const at::Tensor& X, const at::Tensor& W_ph
 std::vector<at::Tensor> backward_impl(const at::Tensor& grad_out, const at::Tensor& X, const at::Tensor& W_phi,
                                       const at::Tensor& gate_q, const at::Tensor& gate_k, const at::Tensor& W_V,
                                       const at::Tensor& out, const at::Tensor& lse, const at::Tensor* fwd_ws,
-                                      int64_t H, int64_t cube_m, double scale, bool causal) {
+                                      int64_t H, int64_t cube_m, double scale, bool causal, int64_t variant) {
+  const int mode = mode_of(causal, variant);
   check(grad_out, "grad_out");
   const Shape s = check_inputs(X, W_phi, gate_q, gate_k, W_V, H, cube_m);
   check(out, "out");
@@ -108,7 +120,7 @@ std::vector<at::Tensor> backward_impl(const at::Tensor& grad_out, const at::Tens
   raise_on(morpho_backward(grad_out.data_ptr(), X.data_ptr(), W_phi.data_ptr(), gate_q.data_ptr(), gate_k.data_ptr(),
                            W_V.data_ptr(), out.data_ptr(), lse.data_ptr<float>(), dX.data_ptr(), dW_phi.data_ptr(),
                            d_gate_q.data_ptr(), d_gate_k.data_ptr(), dW_V.data_ptr(), s.B, s.N, s.D, s.H, s.M,
-                           (float)scale, causal ? 1 : 0, fwd_ptr, ws.data_ptr(), ws_bytes, current_stream(X)),
+                           (float)scale, mode, fwd_ptr, ws.data_ptr(), ws_bytes, current_stream(X)),
            "backward");
   return {dX, dW_phi, d_gate_q, d_gate_k, dW_V};
 }
@@ -116,27 +128,28 @@ std::vector<at::Tensor> backward_impl(const at::Tensor& grad_out, const at::Tens
 std::vector<at::Tensor> op_forward(const at::Tensor& X, const at::Tensor& W_phi, const at::Tensor& gate_q,
                                    const at::Tensor& gate_k, const at::Tensor& W_V, int64_t H, int64_t cube_m,
                                    double scale, bool causal) {
-  return forward_impl(X, W_phi, gate_q, gate_k, W_V, H, cube_m, scale, causal, false);
+  return forward_impl(X, W_phi, gate_q, gate_k, W_V, H, cube_m, scale, causal, 0, false);
 }
 
 std::vector<at::Tensor> op_forward_train(const at::Tensor& X, const at::Tensor& W_phi, const at::Tensor& gate_q,
                                          const at::Tensor& gate_k, const at::Tensor& W_V, int64_t H, int64_t cube_m,
-                                         double scale, bool causal) {
-  return forward_impl(X, W_phi, gate_q, gate_k, W_V, H, cube_m, scale, causal, true);
+                                         double scale, bool causal, int64_t variant) {
+  return forward_impl(X, W_phi, gate_q, gate_k, W_V, H, cube_m, scale, causal, variant, true);
 }
 
 std::vector<at::Tensor> op_backward(const at::Tensor& grad_out, const at::Tensor& X, const at::Tensor& W_phi,
                                     const at::Tensor& gate_q, const at::Tensor& gate_k, const at::Tensor& W_V,
                                     const at::Tensor& out, const at::Tensor& lse, int64_t H, int64_t cube_m,
                                     double scale, bool causal) {
-  return backward_impl(grad_out, X, W_phi, gate_q, gate_k, W_V, out, lse, nullptr, H, cube_m, scale, causal);
+  return backward_impl(grad_out, X, W_phi, gate_q, gate_k, W_V, out, lse, nullptr, H, cube_m, scale, causal, 0);
 }
 
 std::vector<at::Tensor> op_backward_train(const at::Tensor& grad_out, const at::Tensor& X, const at::Tensor& W_phi,
                                           const at::Tensor& gate_q, const at::Tensor& gate_k, const at::Tensor& W_V,
                                           const at::Tensor& out, const at::Tensor& lse, const at::Tensor& workspace,
-                                          int64_t H, int64_t cube_m, double scale, bool causal) {
-  return backward_impl(grad_out, X, W_phi, gate_q, gate_k, W_V, out, lse, &workspace, H, cube_m, scale, causal);
+                                          int64_t H, int64_t cube_m, double scale, bool causal, int64_t variant) {
+  return backward_impl(grad_out, X, W_phi, gate_q, gate_k, W_V, out, lse, &workspace, H, cube_m, scale, causal,
+                       variant);
 }
 
 }  // namespace
@@ -147,10 +160,10 @@ TORCH_LIBRARY(morphottention, m) {
   m.def("backward(Tensor grad_out, Tensor X, Tensor W_phi, Tensor gate_q, Tensor gate_k, "
         "Tensor W_V, Tensor out, Tensor lse, int H, int cube_m, float scale, bool causal) -> Tensor[]");
   m.def("forward_train(Tensor X, Tensor W_phi, Tensor gate_q, Tensor gate_k, Tensor W_V, "
-        "int H, int cube_m, float scale, bool causal) -> Tensor[]");
+        "int H, int cube_m, float scale, bool causal, int variant=0) -> Tensor[]");
   m.def("backward_train(Tensor grad_out, Tensor X, Tensor W_phi, Tensor gate_q, Tensor gate_k, "
-        "Tensor W_V, Tensor out, Tensor lse, Tensor workspace, int H, int cube_m, float scale, bool causal) "
-        "-> Tensor[]");
+        "Tensor W_V, Tensor out, Tensor lse, Tensor workspace, int H, int cube_m, float scale, bool causal, "
+        "int variant=0) -> Tensor[]");
 }
 
 TORCH_LIBRARY_IMPL(morphottention, CUDA, m) {

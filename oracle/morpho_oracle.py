@@ -11,7 +11,11 @@ reference CUDA extension (paths relative to the reference repo root):
 * projection   ``packages/morphottention/csrc/cuda/sm120/project.cuh:26-45``
   (``Z = X W_phi_h``; ``phi = sigmoid(Z)``; ``code = g_self * phi``;
   ``bias = sum_c g_partner,c * code_c`` with fp32 gates)
-* sigmoid      ``packages/morphottention/csrc/cuda/morfology/cube.cuh:12-14``
+* sigmoid      ``packages/morphottention/csrc/cuda/morfology/cube.cuh:12-14``; the
+  unwired variants HardTanh01 ``clamp((z + 1) / 2, 0, 1)`` and Identity
+  (``cube.cuh:15-17,29-35``) and the ``MASK_DIAG`` flag
+  (``packages/morphottention/csrc/cuda/utils/declarations.cuh:79-82``), which
+  drops key ``j == i``
 * scores/mask/online softmax/epilogue
                ``packages/morphottention/csrc/cuda/attention/attention.cu:113-188``
   (``s = (2 S_raw - qb_i - cb_j) * scale * log2e``, causal drop ``k > q``,
@@ -61,15 +65,30 @@ def init_params(dim: int, num_heads: int, cube_m: int, *, dtype=torch.float32, d
     return W_phi.to(dtype), gate_q.to(dtype), gate_k.to(dtype), W_V.to(dtype)
 
 
-def project(x, W_phi, gate_q, gate_k, num_heads: int, cube_m: int):
-    """Per-head soft-hypercube projection (``project.cuh:26-45``, ``cube.cuh:12-14``).
+PROJECTIONS = ("sigmoid", "hardtanh01", "identity")
+
+
+def cube_project(z, projection: str = "sigmoid"):
+    """Cube projection phi(z) (``cube.cuh:12-17``): ``1 / (1 + e^-z)``,
+    ``clamp((z + 1) / 2, 0, 1)`` or ``z``."""
+    if projection == "sigmoid":
+        return torch.sigmoid(z)
+    if projection == "hardtanh01":
+        return torch.clamp(0.5 * (z + 1.0), 0.0, 1.0)
+    if projection == "identity":
+        return z
+    raise ValueError(f"unknown projection {projection!r}")
+
+
+def project(x, W_phi, gate_q, gate_k, num_heads: int, cube_m: int, projection: str = "sigmoid"):
+    """Per-head soft-hypercube projection (``project.cuh:26-45``, ``cube.cuh:12-17``).
 
     Returns ``phi, q, k, qb, cb`` with ``phi, q, k`` shaped ``[B, H, N, m]`` and
     ``qb, cb`` shaped ``[B, H, N]``.
     """
     B, N, _ = x.shape
     z = x @ W_phi                                               # [B, N, H*m]
-    phi = torch.sigmoid(z).view(B, N, num_heads, cube_m).permute(0, 2, 1, 3)
+    phi = cube_project(z, projection).view(B, N, num_heads, cube_m).permute(0, 2, 1, 3)
     gq = gate_q.to(phi.dtype)[None, :, None, :]
     gk = gate_k.to(phi.dtype)[None, :, None, :]
     q = gq * phi                                                # code = g_self * phi
@@ -91,38 +110,65 @@ def causal_mask(N: int, device) -> torch.Tensor:
     return idx[None, :] > idx[:, None]
 
 
+def drop_mask(N: int, device, causal: bool, mask_diag: bool):
+    """True where key ``j`` is dropped from query ``i``'s row: ``j > i`` when
+    causal, ``j == i`` with ``MASK_DIAG`` (``attention.cu:126-133``); ``None``
+    when nothing is dropped."""
+    idx = torch.arange(N, device=device)
+    mask = torch.zeros(N, N, dtype=torch.bool, device=device)
+    if causal:
+        mask |= idx[None, :] > idx[:, None]
+    if mask_diag:
+        mask |= idx[None, :] == idx[:, None]
+    return mask if (causal or mask_diag) else None
+
+
 def morpho_attention_ref(x, W_phi, gate_q, gate_k, W_V, num_heads: int, cube_m: int, *,
-                         scale: float = 1.0, causal: bool = False, return_lse: bool = False):
+                         scale: float = 1.0, causal: bool = False, return_lse: bool = False,
+                         projection: str = "sigmoid", mask_diag: bool = False):
     """Forward of the fused op in the dtype of ``x`` (use fp32 or fp64).
 
     Returns ``out [B, N, D]`` and, if ``return_lse``, the base-2 row
     log-sum-exp ``lse [B*H, N]`` exactly as ``morphottention::forward`` returns
-    it (``attention.cu:173-188``).
+    it (``attention.cu:173-188``): a row without unmasked keys has ``out = 0``
+    and ``lse = -FLT_MAX``.
     """
     B, N, D = x.shape
     H, m = num_heads, cube_m
     dv = W_V.shape[1] // H          # D // H; a head slice of W_V is also accepted
     W_phi = W_phi.to(x.dtype)
     W_V = W_V.to(x.dtype)
-    _, q, k, qb, cb = project(x, W_phi, gate_q, gate_k, H, m)
+    _, q, k, qb, cb = project(x, W_phi, gate_q, gate_k, H, m, projection)
     s = scores(q, k, qb, cb, scale)                             # [B, H, N, N]
-    if causal:
-        s = s.masked_fill(causal_mask(N, x.device), float("-inf"))
+    mask = drop_mask(N, x.device, causal, mask_diag)
+    empty = None
+    if mask is not None:
+        s = s.masked_fill(mask, float("-inf"))
+        empty = mask.all(dim=-1)                                # rows without keys
+        if bool(empty.any()):
+            s = s.masked_fill(empty[:, None], 0.0)              # finite, so no NaN reaches autograd
+        else:
+            empty = None
     lse_nat = torch.logsumexp(s, dim=-1)                        # [B, H, N]
     P = torch.exp(s - lse_nat[..., None])
+    if empty is not None:
+        P = P.masked_fill(empty[:, None], 0.0)
     V = (x @ W_V).view(B, N, H, dv).permute(0, 2, 1, 3)         # [B, H, N, dv]
     O = P @ V
     out = O.permute(0, 2, 1, 3).reshape(B, N, H * dv)
     if not return_lse:
         return out
-    lse = (lse_nat * LOG2E).reshape(B * H, N)
-    return out, lse
+    lse = lse_nat * LOG2E
+    if empty is not None:
+        lse = lse.masked_fill(empty, -FLT_MAX)
+    return out, lse.reshape(B * H, N)
 
 
 def morpho_attention_ref_grads(x, W_phi, gate_q, gate_k, W_V, num_heads: int, cube_m: int, *,
                                scale: float = 1.0, causal: bool = False, dout=None,
                                dtype=torch.float32, batch_chunk: int | None = None,
-                               head_chunk: int | None = None):
+                               head_chunk: int | None = None, projection: str = "sigmoid",
+                               mask_diag: bool = False):
     """Forward + autograd backward of the restatement, chunked over batch and heads.
 
     Inputs are upcast to ``dtype``. ``dout`` defaults to ones (i.e. the
@@ -151,7 +197,8 @@ def morpho_attention_ref_grads(x, W_phi, gate_q, gate_k, W_V, num_heads: int, cu
             h1 = min(H, h0 + hc)
             o, l = morpho_attention_ref(xb, params[0][:, h0 * m:h1 * m], params[1][h0:h1], params[2][h0:h1],
                                         params[3][:, h0 * dv:h1 * dv], h1 - h0, m,
-                                        scale=scale, causal=causal, return_lse=True)
+                                        scale=scale, causal=causal, return_lse=True,
+                                        projection=projection, mask_diag=mask_diag)
             o.backward(g_full[:, :, h0 * dv:h1 * dv])
             out[b0:b1, :, h0 * dv:h1 * dv] = o.detach()
             lse[b0:b1, h0:h1] = l.detach().view(b1 - b0, h1 - h0, N)

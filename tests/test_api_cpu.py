@@ -67,10 +67,10 @@ def test_workspace_sizes():
     assert capi.forward_workspace_size(4, 4096, 256, 16, 16) == 0       # head_dim_v 16 unsupported
 
 
-def _call_forward(L, ptr, *, M=16, D=64, H=2, ws=1 << 20):
+def _call_forward(L, ptr, *, M=16, D=64, H=2, ws=1 << 20, mode=0):
     vp = ctypes.c_void_p(ptr)
     lse = ctypes.c_void_p(ptr)
-    return L.morpho_forward(vp, vp, vp, vp, vp, vp, lse, 2, 8, D, H, M, 1.0, 0, vp, ws, None)
+    return L.morpho_forward(vp, vp, vp, vp, vp, vp, lse, 2, 8, D, H, M, 1.0, mode, vp, ws, None)
 
 
 def test_forward_validation_never_reaches_the_device():
@@ -86,6 +86,9 @@ def test_forward_validation_never_reaches_the_device():
     assert _call_forward(L, 4096, ws=16) == 3
     assert b"workspace" in L.morpho_last_error()
     assert _call_forward(L, 4100) == 1  # misaligned
+    for bad in (16, 12, 13, 0x100):  # an unknown bit; both projections
+        assert _call_forward(L, 4096, mode=bad) == 1
+        assert b"invalid mode bits" in L.morpho_last_error()
     st = L.morpho_backward(*([vp] * 13), 2, 8, 64, 2, 16, 1.0, 0, None, vp, 0, None)
     assert st == 1 and L.morpho_last_error() == b"Null input pointer"
 

@@ -74,17 +74,23 @@ def check(name, out, lse, grads, ref_out, ref_lse, ref_grads, ill_conditioned=()
     excess = (err - half_ulp(ref_out)).clamp_min(0).max().item()
     fwd = err.max().item()
     lse_err = (lse.float() - ref_lse.float()).abs().max().item()
+    # lse is a sum of O(|score|) terms: beyond |lse| ~ 200 (identity projection
+    # with wide inputs) fp32 rounding of the projection alone exceeds 1e-2, so
+    # the bar grows as 5e-5 |lse| there
+    finite = ref_lse.float()[ref_lse.float() > -1e38]
+    lse_max = finite.abs().max().item() if finite.numel() else 0.0
+    lse_bar = max(1e-2, 5e-5 * lse_max)
     rels = []
     for gname, g, gr in zip(GRAD_NAMES, grads, ref_grads):
         gr = gr.float()
         rels.append((g.float() - gr).abs().max().item() / max(gr.abs().max().item(), 1e-30))
     _say(f"[parity] {name}: fwd max-abs {fwd:.3e} (fp16 floor {floor:.3e}, beyond rounding {excess:.3e}) "
-         f"lse {lse_err:.3e} grads " + " ".join(f"{n}={r:.2e}" for n, r in zip(GRAD_NAMES, rels)))
+         f"lse {lse_err:.3e} (max |lse| {lse_max:.1f}) grads " + " ".join(f"{n}={r:.2e}" for n, r in zip(GRAD_NAMES, rels)))
     assert torch.isfinite(out).all() and all(torch.isfinite(g).all() for g in grads)
     if floor <= 1e-3:
         assert fwd <= FWD_TOL, f"{name}: forward error {fwd}"
     assert excess <= FWD_TOL, f"{name}: forward error beyond fp16 rounding {excess}"
-    assert lse_err <= 1e-2, f"{name}: lse error {lse_err}"
+    assert lse_err <= lse_bar, f"{name}: lse error {lse_err} (max |lse| {lse_max})"
     for n, r, g in zip(GRAD_NAMES, rels, grads):
         if zero_phi_path and n in PHI_PATH:
             scale = ref_grads[GRAD_NAMES.index("dW_V")].abs().max().item()
@@ -225,6 +231,41 @@ def test_value_remainder_is_carried(m, dv, causal):
     _say(f"[parity] value remainder m={m} dv={dv} causal={causal}: beyond rounding {excess:.3e} "
          f"(bound {bound:.3e}, max|V| {V.abs().max().item():.2f})")
     assert excess <= bound
+
+
+def _run_variant(x, params, H, m, scale, causal, dout, projection, mask_diag):
+    from morphottention_amd import morpho_attention
+    from morphottention_amd.autograd import variant_bits
+    leaves = [t.detach().clone().requires_grad_(True) for t in (x, *params)]
+    out = morpho_attention(leaves[0], *leaves[1:], H, m, scale=scale, causal=causal, projection=projection,
+                           mask_diag=mask_diag)
+    out.backward(dout)
+    _, lse, _ = torch.ops.morphottention.forward_train(x, *params, H, m, scale, causal,
+                                                       variant_bits(projection, mask_diag))
+    torch.cuda.synchronize()
+    return out.detach(), lse, [t.grad for t in leaves]
+
+
+# The reference's compile-time variants that it never wires (cube.cuh:9-17,
+# declarations.cuh:79-82): HardTanh01 and Identity cube projections, and the
+# masked diagonal (which empties query 0's row under causal masking: out 0,
+# lse -FLT_MAX). N = 300 spans two forward query blocks and three backward key
+# blocks, so unmasked, diagonal and ragged tiles all occur.
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+@pytest.mark.parametrize("projection,mask_diag,m,dv", [
+    ("hardtanh01", False, 16, 64), ("identity", False, 16, 64), ("hardtanh01", False, 32, 64),
+    ("sigmoid", True, 16, 64), ("sigmoid", True, 32, 32), ("sigmoid", True, 64, 128),
+    ("identity", True, 16, 32)])
+def test_unwired_reference_variants(projection, mask_diag, m, dv, causal):
+    B, N, H = 2, 300, 2
+    _say(f"[case] variant projection={projection} mask_diag={mask_diag} m={m} dv={dv} causal={causal} N={N}")
+    x, params, dout = make_inputs(B, N, H * dv, H, m, seed=1000 + m + dv, x_mult=2.0)
+    out, lse, grads = _run_variant(x, params, H, m, 0.7, causal, dout, projection, mask_diag)
+    ref = mo.morpho_attention_ref_grads(x, *params, H, m, scale=0.7, causal=causal, dout=dout,
+                                        dtype=torch.float32, projection=projection, mask_diag=mask_diag)
+    check(f"variant {projection} mask_diag={mask_diag} m={m} dv={dv} causal={causal}", out, lse, grads, *ref)
+    if causal and mask_diag:
+        assert bool((out[:, 0] == 0).all()) and bool((lse[:, 0] == -3.4028234663852886e38).all())
 
 
 @pytest.mark.parametrize("causal", [False, True])

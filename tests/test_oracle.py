@@ -248,8 +248,8 @@ def test_planted_partner_gate_mistake_is_caught(monkeypatch):
     x, W_phi, gq, gk, W_V = _inputs(1, 7, 8, 2, 3, seed=14)
     real_project = mo.project
 
-    def wrong(x, W_phi, gate_q, gate_k, H, m):
-        phi, q, k, qb, _ = real_project(x, W_phi, gate_q, gate_k, H, m)
+    def wrong(x, W_phi, gate_q, gate_k, H, m, projection="sigmoid"):
+        phi, q, k, qb, _ = real_project(x, W_phi, gate_q, gate_k, H, m, projection)
         cb = (gate_k.to(phi.dtype)[None, :, None, :] * k).sum(-1)
         return phi, q, k, qb, cb
 
@@ -284,3 +284,77 @@ def test_fp32_oracle_conditioning():
     assert rel["dX"] < 1e-5 and rel["dW_V"] < 1e-5
     assert rel["dW_phi"] > 1e-2 and rel["d_gate_q"] > 1e-2
     assert np.abs(d["dW_phi"]).max() < 1e-5 * np.abs(d["dW_V"]).max()
+
+
+# ---------------------------------------------------------------- unwired reference variants
+def _centred_sdpa(x, W_phi, gq, gk, W_V, H, m, scale, phi_fn, keep):
+    """The attention written as plain SDPA on centred codes, from the identity
+    2 a b - a - b = 2 (a - 1/2)(b - 1/2) - 1/2: s_ij equals
+    2 scale sum_c G_c (phi_ic - 1/2)(phi_jc - 1/2) up to a constant per
+    (head) that cancels in the softmax. phi comes from library routines, not
+    from the oracle's projection; `keep` is SDPA's boolean mask."""
+    import torch.nn.functional as F
+    B, N, D = x.shape
+    phi = phi_fn(x @ W_phi).view(B, N, H, m).permute(0, 2, 1, 3) - 0.5
+    G = (gq * gk)[None, :, None, :]
+    V = (x @ W_V).view(B, N, H, D // H).permute(0, 2, 1, 3)
+    O = F.scaled_dot_product_attention(2.0 * scale * G * phi, phi, V, attn_mask=keep, scale=1.0)
+    return O.permute(0, 2, 1, 3).reshape(B, N, D)
+
+
+def _phi_fn(projection):
+    import torch.nn.functional as F
+    return {"sigmoid": torch.sigmoid, "hardtanh01": lambda z: F.hardtanh(0.5 * z + 0.5, 0.0, 1.0),
+            "identity": lambda z: z}[projection]
+
+
+@pytest.mark.parametrize("projection", ["sigmoid", "hardtanh01", "identity"])
+@pytest.mark.parametrize("causal,mask_diag", [(False, False), (True, False), (False, True), (True, True)])
+def test_variants_match_centred_sdpa(projection, causal, mask_diag):
+    """Cube projections (cube.cuh:12-17) and MASK_DIAG (declarations.cuh:79-82)
+    against library SDPA with an explicit mask; a row without keys (query 0,
+    causal with the diagonal dropped) gives out = 0 and lse = -FLT_MAX."""
+    B, N, D, H, m, scale = 2, 13, 12, 3, 4, 0.8
+    x, W_phi, gq, gk, W_V = _inputs(B, N, D, H, m, seed=40, x_mult=2.0)
+    out, lse = mo.morpho_attention_ref(x, W_phi, gq, gk, W_V, H, m, scale=scale, causal=causal,
+                                       mask_diag=mask_diag, projection=projection, return_lse=True)
+    idx = torch.arange(N)
+    keep = torch.ones(N, N, dtype=torch.bool)
+    if causal:
+        keep &= idx[None, :] <= idx[:, None]
+    if mask_diag:
+        keep &= idx[None, :] != idx[:, None]
+    rows = keep.any(-1)
+    ref = _centred_sdpa(x, W_phi, gq, gk, W_V, H, m, scale, _phi_fn(projection), keep)
+    assert torch.allclose(out[:, rows], ref[:, rows], atol=1e-12, rtol=0)
+    if not bool(rows.all()):
+        assert bool((out[:, ~rows] == 0).all())
+        assert bool((lse.view(B, H, N)[..., ~rows] == -mo.FLT_MAX).all())
+
+
+@pytest.mark.parametrize("projection,mask_diag", [("hardtanh01", False), ("identity", False), ("sigmoid", True),
+                                                  ("identity", True)])
+def test_variant_gradcheck_fp64(projection, mask_diag):
+    x, W_phi, gq, gk, W_V = _inputs(2, 5, 6, 2, 3, seed=41, x_mult=2.0)
+    args = [t.clone().requires_grad_(True) for t in (x, W_phi, gq, gk, W_V)]
+
+    def f(x, W_phi, gq, gk, W_V):
+        return mo.morpho_attention_ref(x, W_phi, gq, gk, W_V, 2, 3, scale=0.7, causal=True,
+                                       projection=projection, mask_diag=mask_diag)
+
+    assert torch.autograd.gradcheck(f, args, eps=1e-6, atol=1e-7, rtol=1e-5)
+
+
+def test_planted_hardtanh_slope_mistake_is_caught(monkeypatch):
+    """clamp(z + 1, 0, 1) in place of clamp((z + 1) / 2, 0, 1) fails the
+    centred-SDPA pin."""
+    x, W_phi, gq, gk, W_V = _inputs(1, 9, 8, 2, 4, seed=42, x_mult=2.0)
+    real = mo.cube_project
+
+    def wrong(z, projection="sigmoid"):
+        return torch.clamp(z + 1.0, 0.0, 1.0) if projection == "hardtanh01" else real(z, projection)
+
+    monkeypatch.setattr(mo, "cube_project", wrong)
+    out = mo.morpho_attention_ref(x, W_phi, gq, gk, W_V, 2, 4, projection="hardtanh01")
+    ref = _centred_sdpa(x, W_phi, gq, gk, W_V, 2, 4, 1.0, _phi_fn("hardtanh01"), None)
+    assert not torch.allclose(out, ref, atol=1e-9, rtol=0)
