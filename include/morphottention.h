@@ -106,6 +106,41 @@ int morpho_backward(const void* grad_out, const void* X, const void* W_phi, cons
                     float scale, int causal, const void* forward_workspace, void* workspace, size_t workspace_bytes,
                     morpho_stream_t stream);
 
+/* Soft tropical aggregation: the morpho scores s_ij combine with the values
+ * in a soft max-plus (sgn = +1, dilation) or min-plus (sgn = -1, erosion)
+ * product instead of the softmax-weighted sum,
+ *     out_ic = sgn * tau * ln sum_j exp(sgn * (s_ij + V_jc) / tau),
+ * built from the accumulators of packages/morphottention/csrc/cuda/morfology/
+ * soft_morph.cuh:21-69 (lse_update, morph_accumulate, lse_merge,
+ * lse_finalize), which the reference defines but never calls; it has no
+ * launcher or op for them, so these entry points have no counterpart to
+ * replace. Shapes, dtypes, `mode` bits and workspace rules are those of
+ * morpho_forward / morpho_backward (the forward workspace size is
+ * morpho_forward_workspace_size). `tau` points to one float32 in device
+ * memory (> 0; read by the kernels, so it may be a learnable parameter).
+ * zb [B*H, N, D/H] float32 receives log2 sum_j 2^(log2e sgn (s_ij + V_jc) /
+ * tau), so out = sgn tau ln2 zb (-FLT_MAX, with out = 0, for a row without
+ * keys); the backward needs it. */
+int morpho_soft_forward(const void* X, const void* W_phi, const void* gate_q, const void* gate_k, const void* W_V,
+                        const float* tau, void* out, float* zb, int64_t B, int64_t N, int64_t D, int64_t H,
+                        int64_t cube_m, float scale, int mode, int sgn, void* workspace, size_t workspace_bytes,
+                        morpho_stream_t stream);
+
+/* Bytes of device workspace morpho_soft_backward needs (as
+ * morpho_backward_workspace_size, plus the dtau partial sums). */
+size_t morpho_soft_backward_workspace_size(int64_t B, int64_t N, int64_t D, int64_t H, int64_t cube_m,
+                                           int have_forward_workspace);
+
+/* Backward of morpho_soft_forward: dX, dW_phi, d_gate_q, d_gate_k, dW_V as in
+ * morpho_backward, and dtau (one float32 in device memory) from
+ * morph_dtau_term (soft_morph.cuh:77-80) summed over every output. */
+int morpho_soft_backward(const void* grad_out, const void* X, const void* W_phi, const void* gate_q,
+                         const void* gate_k, const void* W_V, const float* tau, const float* zb, void* dX,
+                         void* dW_phi, void* d_gate_q, void* d_gate_k, void* dW_V, float* dtau, int64_t B, int64_t N,
+                         int64_t D, int64_t H, int64_t cube_m, float scale, int mode, int sgn,
+                         const void* forward_workspace, void* workspace, size_t workspace_bytes,
+                         morpho_stream_t stream);
+
 /* Per-kernel timing for measurement harnesses. No reference counterpart.
  * When enabled (process-wide), every kernel the library launches, from any
  * thread, is bracketed by HIP events on its stream. morpho_timing_read

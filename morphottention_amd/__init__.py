@@ -5,5 +5,7 @@ Drop-in for the reference package ``morphottention``
 """
 
 from .autograd import MorphoAttention, MorphoAttentionFunction, morpho_attention
+from .soft_morph import SoftMorphAttention, SoftMorphAttentionFunction, soft_morph_attention
 
-__all__ = ["MorphoAttention", "MorphoAttentionFunction", "morpho_attention"]
+__all__ = ["MorphoAttention", "MorphoAttentionFunction", "morpho_attention", "SoftMorphAttention",
+           "SoftMorphAttentionFunction", "soft_morph_attention"]

@@ -309,6 +309,109 @@ MORPHO_EXPORT int morpho_backward(const void* grad_out, const void* X, const voi
   return MORPHO_OK;
 }
 
+// ---------------------------------------------------------------- soft tropical aggregation
+namespace {
+size_t soft_part_bytes(const Dims& d) {
+  return align_up((size_t)(soft_prep_blocks(d) + 2 * soft_bwd_slots(d)) * sizeof(float));
+}
+int check_soft_args(const float* tau, int sgn) {
+  if (!tau) return fail(MORPHO_ERR_INVALID_ARGUMENT, "Null tau pointer");
+  if ((reinterpret_cast<uintptr_t>(tau) & 3) != 0)
+    return fail(MORPHO_ERR_INVALID_ARGUMENT, "tau must be 4-byte aligned");
+  if (sgn != 1 && sgn != -1) return fail(MORPHO_ERR_INVALID_ARGUMENT, "sgn must be +1 (dilation) or -1 (erosion)");
+  return MORPHO_OK;
+}
+}  // namespace
+
+MORPHO_EXPORT size_t morpho_soft_backward_workspace_size(int64_t B, int64_t N, int64_t D, int64_t H, int64_t cube_m,
+                                                         int have_forward_workspace) {
+  Dims d;
+  std::string keep = g_last_error;
+  const int st = make_dims(B, N, D, H, cube_m, 1.0f, 0, d);
+  g_last_error = keep;
+  if (st != MORPHO_OK) return 0;
+  return bwd_bytes(d) + soft_part_bytes(d) + (have_forward_workspace ? 0 : proj_bytes(d));
+}
+
+MORPHO_EXPORT int morpho_soft_forward(const void* X, const void* W_phi, const void* gate_q, const void* gate_k,
+                                      const void* W_V, const float* tau, void* out, float* zb, int64_t B, int64_t N,
+                                      int64_t D, int64_t H, int64_t cube_m, float scale, int mode, int sgn,
+                                      void* workspace, size_t workspace_bytes, morpho_stream_t stream) {
+  g_last_error.clear();
+  Dims d;
+  int st = make_dims(B, N, D, H, cube_m, scale, mode, d);
+  if (st != MORPHO_OK) return st;
+  if (!X || !W_phi || !gate_q || !gate_k || !W_V || !out || !zb) return fail(MORPHO_ERR_INVALID_ARGUMENT, "Null pointer");
+  if ((st = check_soft_args(tau, sgn)) != MORPHO_OK) return st;
+  if (misaligned(X) || misaligned(W_phi) || misaligned(W_V) || misaligned(out) || misaligned(zb))
+    return fail(MORPHO_ERR_INVALID_ARGUMENT, "tensor pointers must be 16-byte aligned");
+  const size_t need = proj_bytes(d);
+  if (!workspace || workspace_bytes < need)
+    return fail(MORPHO_ERR_WORKSPACE, "forward workspace needs %zu bytes (got %zu)", need, workspace_bytes);
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255) != 0)
+    return fail(MORPHO_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const ProjBuffers p = carve_proj(workspace, d);
+  st = run_projection(d, X, W_phi, gate_q, gate_k, W_V, p, s);
+  if (st != MORPHO_OK) return st;
+  MORPHO_LAUNCH("soft_fwd", launch_soft_fwd(d, p, tau, sgn, static_cast<_Float16*>(out), zb, s));
+  return MORPHO_OK;
+}
+
+MORPHO_EXPORT int morpho_soft_backward(const void* grad_out, const void* X, const void* W_phi, const void* gate_q,
+                                       const void* gate_k, const void* W_V, const float* tau, const float* zb,
+                                       void* dX, void* dW_phi, void* d_gate_q, void* d_gate_k, void* dW_V, float* dtau,
+                                       int64_t B, int64_t N, int64_t D, int64_t H, int64_t cube_m, float scale,
+                                       int mode, int sgn, const void* forward_workspace, void* workspace,
+                                       size_t workspace_bytes, morpho_stream_t stream) {
+  g_last_error.clear();
+  Dims d;
+  int st = make_dims(B, N, D, H, cube_m, scale, mode, d);
+  if (st != MORPHO_OK) return st;
+  if (!grad_out || !X || !W_phi || !gate_q || !gate_k || !W_V || !zb)
+    return fail(MORPHO_ERR_INVALID_ARGUMENT, "Null input pointer");
+  if (!dX || !dW_phi || !d_gate_q || !d_gate_k || !dW_V || !dtau)
+    return fail(MORPHO_ERR_INVALID_ARGUMENT, "Null grad pointer");
+  if ((st = check_soft_args(tau, sgn)) != MORPHO_OK) return st;
+  if (misaligned(grad_out) || misaligned(X) || misaligned(W_phi) || misaligned(W_V) || misaligned(zb) ||
+      misaligned(dX) || misaligned(dW_phi) || misaligned(dW_V))
+    return fail(MORPHO_ERR_INVALID_ARGUMENT, "tensor pointers must be 16-byte aligned");
+  const bool have_fwd = forward_workspace != nullptr;
+  const size_t need = bwd_bytes(d) + soft_part_bytes(d) + (have_fwd ? 0 : proj_bytes(d));
+  if (!workspace || workspace_bytes < need)
+    return fail(MORPHO_ERR_WORKSPACE, "backward workspace needs %zu bytes (got %zu)", need, workspace_bytes);
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255) != 0 ||
+      (have_fwd && (reinterpret_cast<uintptr_t>(forward_workspace) & 255) != 0))
+    return fail(MORPHO_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  ProjBuffers p;
+  if (have_fwd) {
+    p = carve_proj(const_cast<void*>(forward_workspace), d);
+  } else {
+    p = carve_proj(ws, d);
+    st = run_projection(d, X, W_phi, gate_q, gate_k, W_V, p, s);
+    if (st != MORPHO_OK) return st;
+    ws += proj_bytes(d);
+  }
+  const BwdBuffers g = carve_bwd(ws, d);
+  float* prep_part = reinterpret_cast<float*>(ws + bwd_bytes(d));
+  float* bwd_part = prep_part + soft_prep_blocks(d);
+  const auto* go = static_cast<const _Float16*>(grad_out);
+  MORPHO_LAUNCH("soft_bwd_prep", launch_soft_bwd_prep(d, go, zb, g, prep_part, s));
+  MORPHO_LAUNCH("soft_bwd", launch_soft_bwd(d, p, go, zb, tau, sgn, g, bwd_part, s));
+  MORPHO_LAUNCH("proj_bwd_elem", launch_proj_bwd_elem(d, static_cast<const _Float16*>(gate_q),
+                                                      static_cast<const _Float16*>(gate_k), p, g, s));
+  MORPHO_LAUNCH("bwd_gemm", launch_bwd_gemm(d, p, g, static_cast<const _Float16*>(X), static_cast<_Float16*>(dX), s));
+  MORPHO_LAUNCH("dw_reduce", launch_dw_reduce(d, g, static_cast<const _Float16*>(gate_q),
+                                              static_cast<const _Float16*>(gate_k), static_cast<_Float16*>(dW_phi),
+                                              static_cast<_Float16*>(dW_V), static_cast<_Float16*>(d_gate_q),
+                                              static_cast<_Float16*>(d_gate_k), s));
+  MORPHO_LAUNCH("soft_tau_reduce", launch_soft_tau_reduce(prep_part, soft_prep_blocks(d), bwd_part,
+                                                          soft_bwd_slots(d), tau, sgn, dtau, s));
+  return MORPHO_OK;
+}
+
 MORPHO_EXPORT int morpho_timing_enable(int enable) {
   g_timing.store(enable != 0);
   return MORPHO_OK;

@@ -110,8 +110,37 @@ hipError_t launch_bwd_prep(const Dims& d, const ProjBuffers& p, const _Float16* 
 hipError_t launch_attn_bwd(const Dims& d, const ProjBuffers& p, const _Float16* grad_out, const BwdBuffers& g,
                            hipStream_t s);
 
+// kernels_soft.hip: soft tropical aggregation (out = sgn tau ln sum_j
+// exp(sgn (s + v) / tau)). `tau` is a device pointer to one float; sgn is +1
+// (dilation) or -1 (erosion); zb is the fp32 base-2 normaliser [B*H, N, DV].
+hipError_t launch_soft_fwd(const Dims& d, const ProjBuffers& p, const float* tau, int sgn, _Float16* out, float* zb,
+                           hipStream_t s);
+hipError_t launch_soft_bwd_prep(const Dims& d, const _Float16* grad_out, const float* zb, const BwdBuffers& g,
+                                float* part, hipStream_t s);
+hipError_t launch_soft_bwd(const Dims& d, const ProjBuffers& p, const _Float16* grad_out, const float* zb,
+                           const float* tau, int sgn, const BwdBuffers& g, float* part, hipStream_t s);
+hipError_t launch_soft_tau_reduce(const float* prep, int nprep, const float* bwd, int nbwd, const float* tau, int sgn,
+                                  float* dtau, hipStream_t s);
+int soft_prep_blocks(const Dims& d);  // partial sums written by the prep (one float each)
+int soft_bwd_slots(const Dims& d);    // workgroup slots of the backward (two floats each)
+
 // Timing hooks (capi.hip): bracket one launch with events when enabled.
 void timing_begin(const char* name, hipStream_t s);
 void timing_end(hipStream_t s);
+
+// Instantiations of a launcher template FN<M, DV> for every supported shape.
+#define MORPHO_MDV_DISPATCH(FN, ...)                                                         \
+  do {                                                                                       \
+    if (d.M == 16 && d.DV == 32) return FN<16, 32>(__VA_ARGS__);                             \
+    if (d.M == 16 && d.DV == 64) return FN<16, 64>(__VA_ARGS__);                             \
+    if (d.M == 16 && d.DV == 128) return FN<16, 128>(__VA_ARGS__);                           \
+    if (d.M == 32 && d.DV == 32) return FN<32, 32>(__VA_ARGS__);                             \
+    if (d.M == 32 && d.DV == 64) return FN<32, 64>(__VA_ARGS__);                             \
+    if (d.M == 32 && d.DV == 128) return FN<32, 128>(__VA_ARGS__);                           \
+    if (d.M == 64 && d.DV == 32) return FN<64, 32>(__VA_ARGS__);                             \
+    if (d.M == 64 && d.DV == 64) return FN<64, 64>(__VA_ARGS__);                             \
+    if (d.M == 64 && d.DV == 128) return FN<64, 128>(__VA_ARGS__);                           \
+    return hipErrorInvalidValue;                                                             \
+  } while (0)
 
 }  // namespace morpho

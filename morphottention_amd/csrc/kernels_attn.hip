@@ -43,50 +43,6 @@ __device__ __forceinline__ float sum8(const f16x8& v) {
   return s;
 }
 
-// Column offset of the c-th 16-wide code chunk of a code row: chunks 0 ..
-// M/16 - 1 hold the hi parts, M/16 .. M/8 - 1 the lo parts (the 8-wide affine
-// block sits at [M, M + 8)).
-template <int M>
-__device__ __forceinline__ constexpr int chunk_off(int c) {
-  return c < M / 16 ? 16 * c : 16 * c + 8;
-}
-// The exponent's code part, sum_c kc_c phi_c to ~2^-22, from the hi / lo
-// chunks of a key (kf) and a query (qf) operand: hi.hi + hi.lo + lo.hi.
-// KEY_A: the key chunks are the A operand (forward: rows = keys), else the
-// query chunks are (backward: rows = queries).
-template <int M, bool KEY_A>
-__device__ __forceinline__ f32x16 code_dot(const f16x8 (&kf)[M / 8], const f16x8 (&qf)[M / 8], f32x16 acc) {
-  constexpr int HC = M / 16;
-  auto mm = [&](const f16x8& k, const f16x8& q) { acc = KEY_A ? mfma16(k, q, acc) : mfma16(q, k, acc); };
-#pragma unroll
-  for (int i = 0; i < HC; ++i) mm(kf[i], qf[i]);
-#pragma unroll
-  for (int i = 0; i < HC; ++i) mm(kf[i], qf[HC + i]);
-#pragma unroll
-  for (int i = 0; i < HC; ++i) mm(kf[HC + i], qf[i]);
-  return acc;
-}
-
-// Workgroups are dispatched round-robin over the 8 XCDs (id % 8), each with
-// its own L2. Map a 1-D grid of 8 * ceil(BH / 8) * nblk workgroups so that all
-// blocks of one (batch, head) run on the same XCD and share its L2: XCD x
-// serves heads x, x + 8, ... in turn. Returns false for the padding slots.
-__device__ __forceinline__ bool xcd_map(int nblk, int BH, int& bh, int& blk) {
-  const int i = blockIdx.x, xcd = i & 7, slot = i >> 3;
-  bh = 8 * (slot / nblk) + xcd;
-  blk = slot % nblk;
-  return bh < BH;
-}
-// Same XCD per head, but block-major within an XCD: for causal problems block
-// 0 is the longest, so all heads' long blocks start first (longest processing
-// time first), and the short ones fill in at the end.
-__device__ __forceinline__ bool xcd_map_lpt(int nblk, int BH, int& bh, int& blk) {
-  const int i = blockIdx.x, xcd = i & 7, slot = i >> 3, hx = (BH + 7) / 8;
-  bh = 8 * (slot % hx) + xcd;
-  blk = slot / hx;
-  return bh < BH;
-}
-__host__ inline unsigned xcd_grid(int nblk, int BH) { return 8u * (unsigned)((BH + 7) / 8) * (unsigned)nblk; }
 
 // ============================================================ forward
 // XOR swizzle of the 16-byte chunk index within a 128-byte V^T tile row: the
@@ -548,19 +504,6 @@ static hipError_t launch_attn_fwd_t(const Dims& d, const ProjBuffers& p, f16* ou
   return hipGetLastError();
 }
 
-#define MORPHO_MDV_DISPATCH(FN, ...)                                                         \
-  do {                                                                                       \
-    if (d.M == 16 && d.DV == 32) return FN<16, 32>(__VA_ARGS__);                             \
-    if (d.M == 16 && d.DV == 64) return FN<16, 64>(__VA_ARGS__);                             \
-    if (d.M == 16 && d.DV == 128) return FN<16, 128>(__VA_ARGS__);                           \
-    if (d.M == 32 && d.DV == 32) return FN<32, 32>(__VA_ARGS__);                             \
-    if (d.M == 32 && d.DV == 64) return FN<32, 64>(__VA_ARGS__);                             \
-    if (d.M == 32 && d.DV == 128) return FN<32, 128>(__VA_ARGS__);                           \
-    if (d.M == 64 && d.DV == 32) return FN<64, 32>(__VA_ARGS__);                             \
-    if (d.M == 64 && d.DV == 64) return FN<64, 64>(__VA_ARGS__);                             \
-    if (d.M == 64 && d.DV == 128) return FN<64, 128>(__VA_ARGS__);                           \
-    return hipErrorInvalidValue;                                                             \
-  } while (0)
 
 hipError_t launch_attn_fwd(const Dims& d, const ProjBuffers& p, f16* out, float* lse, hipStream_t s) {
   MORPHO_MDV_DISPATCH(launch_attn_fwd_t, d, p, out, lse, s);

@@ -1,0 +1,603 @@
+// Soft tropical aggregation of the values with the morpho scores:
+//     out_ic = sgn tau ln sum_j exp(sgn (s_ij + V_jc) / tau)
+// (sgn = +1 soft max-plus / dilation, sgn = -1 soft min-plus / erosion).
+//
+// Reference: packages/morphottention/csrc/cuda/morfology/soft_morph.cuh
+//   lse_init / lse_update :21-32   running (max, sum) of exp
+//   morph_accumulate      :35-38   fold sgn (s + v) / tau
+//   lse_merge / warp red. :41-63   combine two accumulators
+//   lse_finalize          :66-69   sgn tau (m + log l)
+//   morph_weight          :71-75   P_ijc = exp(sgn ((s + v) - out_ic) / tau)
+//   morph_dtau_term       :77-80   dtau_ic = (out_ic - sum_j P (s + v)) / tau
+// The reference defines these and never calls them; the kernels below are
+// the aggregation built from them on top of this library's projection.
+//
+// MI355X design:
+//  * The work is N^2 dv exponentials (one per query, key and value column):
+//    it is bound by the VALU and the transcendental unit, not by MFMA or HBM.
+//    Scores come from the same code-row MFMA as the softmax path (one 32 x 32
+//    tile per wave and key block), with the query affine block set to the
+//    token bias so that the accumulator is exactly log2e s_ij.
+//  * Everything runs in base 2: y = sgn log2e (s + v) / tau, so each element
+//    costs an add, a max or subtract, one v_exp_f32 and an accumulate.
+//  * Forward: lane = query, 16 keys of each 32-key block per lane, 32 value
+//    columns per wave; an online (max, sum) per (query, column) kept in
+//    registers, merged across the two half-waves at the end (lse_merge).
+//    The values of a 32-key block are decoded once (V_hi + V_lo) into an fp32
+//    LDS tile already scaled by sgn log2e / tau and read as broadcasts.
+//  * Backward: lane = key, key-outer. P_ijc = 2^(y - zb_ic) from the forward's
+//    fp32 normaliser zb; dV accumulates in registers, ds_ij = sum_c dO_ic P_ijc
+//    in registers, and the code gradients dk, dcb (key side) and dq (query
+//    side, fp32 atomics) are formed from the ds tile in LDS. The query-side
+//    row sum of ds, sum_c dO_ic, which the softmax gradient does not have, is
+//    folded into dcb, so the projection backward is shared unchanged.
+//  * dtau = (sum dO out - sum ds s - sum dV V) / tau from per-workgroup
+//    partials, reduced in a fixed order.
+#include "common.h"
+#include "internal.h"
+
+namespace morpho {
+
+constexpr float kLn2 = 0.6931471805599453f;
+
+template <int M, int DV>
+struct SoftCfg {
+  static constexpr int CW = 2 * M + 8;
+  static constexpr int NCH = M / 8;
+  static constexpr int CG = DV / 32;     // 32-column groups, one per wave
+  static constexpr int QBW = 4 / CG;     // forward: 32-query blocks per workgroup
+  static constexpr int QW = 32 * QBW;
+  static constexpr int KB = 4 / CG;      // backward: 32-key blocks per workgroup
+  static constexpr int KW = 32 * KB;
+  static constexpr int WS = DV + 4;      // fp32 LDS row stride of value-column rows
+  static constexpr int QT = 32;          // backward: queries per step
+  static constexpr int PS = M + 4;       // fp32 LDS row stride of phi rows
+  static constexpr int DS = KW + 1;      // fp32 LDS row stride of ds rows (odd: conflict-free columns)
+};
+
+// V_hi + V_lo of key `key`, value column c of head bh (fp32; the remainder is
+// e4m3 times 2^kVloExp in the tile-major, key-permuted layout).
+__device__ __forceinline__ float load_value(const f16* __restrict__ vt, const uint8_t* __restrict__ vlo, int bh,
+                                            int DV, int NP, int c, int key) {
+  const float hi = (float)vt[((int64_t)bh * DV + c) * NP + key];
+  const uint8_t b = vlo[(((int64_t)bh * (NP / 64) + key / 64) * DV + c) * 64 + vlo_pos(key & 63)];
+  return hi + __builtin_amdgcn_cvt_f32_fp8((int)b, 0) * (1.0f / (float)(1 << kVloExp));
+}
+
+// The query operand of a code row with its affine block set to {1, 1, b_hi,
+// b_lo}: the score accumulator is then log2e s_ij (the projection's row
+// reference R is replaced by the token bias b).
+template <int M>
+__device__ __forceinline__ void load_query_operand(const f16* __restrict__ qrow, float b, int h32, f16x8 (&qf)[M / 8],
+                                                   f16x4& qaug) {
+#pragma unroll
+  for (int c = 0; c < M / 8; ++c) qf[c] = *reinterpret_cast<const f16x8*>(qrow + chunk_off<M>(c) + 8 * h32);
+  qaug = *reinterpret_cast<const f16x4*>(qrow + M + 4 * h32);
+  if (h32 == 0) {
+    f16 bh_, bl_;
+    split_hi_lo(b, bh_, bl_);
+    qaug[2] = bh_;
+    qaug[3] = bl_;
+  }
+}
+
+template <int M>
+__device__ __forceinline__ void load_key_operand(const f16* __restrict__ krow, int h32, f16x8 (&kf)[M / 8],
+                                                 f16x4& kaug) {
+#pragma unroll
+  for (int c = 0; c < M / 8; ++c) kf[c] = *reinterpret_cast<const f16x8*>(krow + chunk_off<M>(c) + 8 * h32);
+  kaug = *reinterpret_cast<const f16x4*>(krow + M + 4 * h32);
+}
+
+// ============================================================ forward
+// Workgroup: QBW blocks of 32 queries x CG groups of 32 value columns, one
+// wave each. Keys stream in 32-key blocks; the fp32 value tile of a block
+// (scaled by sgn log2e / tau) is written by all threads into one of two LDS
+// buffers while the other is read.
+template <int M, int DV, bool MD>
+__global__ __launch_bounds__(256) void soft_fwd_kernel(const f16* __restrict__ qa, const f16* __restrict__ ka,
+                                                       const f16* __restrict__ vt, const uint8_t* __restrict__ vlo,
+                                                       const float4* __restrict__ tstat, const float* __restrict__ tau_p,
+                                                       f16* __restrict__ out, float* __restrict__ zb, int N, int NP,
+                                                       int H, int D, int BH, int causal, float sgn) {
+  using C = SoftCfg<M, DV>;
+  __shared__ __align__(16) float sw[2][32 * C::WS];
+  const int tid = threadIdx.x, lane = tid & 63, h32 = lane >> 5, l32 = lane & 31;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nqb = (N + C::QW - 1) / C::QW;
+  int bh, blk;
+  if (!(causal ? xcd_map_lpt(nqb, BH, bh, blk) : xcd_map(nqb, BH, bh, blk))) return;
+  const int qblk = causal ? nqb - 1 - blk : blk;  // longest rows first
+  const int q0 = qblk * C::QW, qw0 = q0 + 32 * (w % C::QBW), c0 = 32 * (w / C::QBW);
+  const int b = bh / H, h = bh - b * H;
+  const int64_t rowbase = (int64_t)bh * N;
+  const float tau = *tau_p;
+  const float ks = sgn / tau, kw = sgn * kLog2e / tau;  // score and value scales of the base-2 exponent
+
+  const int q = qw0 + l32;
+  f16x8 qf[C::NCH];
+  f16x4 qaug = {};
+#pragma unroll
+  for (int c = 0; c < C::NCH; ++c) qf[c] = f16x8{};
+  if (q < N) load_query_operand<M>(qa + (rowbase + q) * C::CW, tstat[rowbase + q].x, h32, qf, qaug);
+
+  float mx[32], sm[32];  // running max and sum of 2^y per value column of this wave
+#pragma unroll
+  for (int c = 0; c < 32; ++c) {
+    mx[c] = kNegInf;
+    sm[c] = 0.f;
+  }
+  const int kend = causal ? min(N, q0 + C::QW) : N;
+  const int nkb = (kend + 31) / 32;
+
+  auto stage = [&](int kb, float* dst) {
+#pragma unroll 4
+    for (int e = tid; e < 32 * DV; e += 256) {
+      const int k = e & 31, c = e >> 5, key = 32 * kb + k;
+      dst[k * C::WS + c] = key < N ? kw * load_value(vt, vlo, bh, DV, NP, c, key) : 0.f;
+    }
+  };
+  if (nkb > 0) stage(0, sw[0]);
+  __syncthreads();
+  for (int kb = 0; kb < nkb; ++kb) {
+    const float* tile = sw[kb & 1];
+    if (kb + 1 < nkb) stage(kb + 1, sw[(kb + 1) & 1]);
+    // S^T block: rows = keys 32 kb + acc_row(r), column = this lane's query
+    const int key0 = 32 * kb;
+    f16x8 kf[C::NCH];
+    f16x4 kaug = {};
+#pragma unroll
+    for (int c = 0; c < C::NCH; ++c) kf[c] = f16x8{};
+    if (key0 + l32 < N) load_key_operand<M>(ka + (rowbase + key0 + l32) * C::CW, h32, kf, kaug);
+    f32x16 acc = code_dot<M, true>(kf, qf, f32x16{});
+    acc = mfma8(kaug, qaug, acc);
+    float u[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int key = key0 + acc_row(r, lane);
+      const bool drop = (key >= N) | (causal != 0 && key > q) | (MD && key == q);
+      u[r] = drop ? kNegInf : ks * acc[r];
+    }
+    // online (max, sum) per value column over this lane's 16 keys
+#pragma unroll
+    for (int c4 = 0; c4 < 8; ++c4) {
+      float y[16][4];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float4 w4 = *reinterpret_cast<const float4*>(tile + acc_row(r, lane) * C::WS + c0 + 4 * c4);
+        y[r][0] = u[r] + w4.x;
+        y[r][1] = u[r] + w4.y;
+        y[r][2] = u[r] + w4.z;
+        y[r][3] = u[r] + w4.w;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int c = 4 * c4 + j;
+        float bm = y[0][j];
+#pragma unroll
+        for (int r = 1; r < 16; ++r) bm = fmaxf(bm, y[r][j]);
+        const float mn = fmaxf(mx[c], bm);
+        const float ref = mn == kNegInf ? 0.f : mn;  // nothing unmasked yet: every term is 0
+        float add = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) add += fast_exp2(y[r][j] - ref);
+        sm[c] = sm[c] * fast_exp2(mx[c] - ref) + add;
+        mx[c] = mn;
+      }
+    }
+    __syncthreads();  // the next block's tile is staged; this block's tile is free again
+  }
+
+  // lse_merge of the two half-waves (same query, complementary keys), then
+  // lse_finalize; each half writes 16 of the wave's 32 columns
+  float zv[32];
+#pragma unroll
+  for (int c = 0; c < 32; ++c) {
+    const float m2 = __shfl_xor(mx[c], 32), s2 = __shfl_xor(sm[c], 32);
+    const float mn = fmaxf(mx[c], m2);
+    const float ref = mn == kNegInf ? 0.f : mn;
+    const float l = sm[c] * fast_exp2(mx[c] - ref) + s2 * fast_exp2(m2 - ref);
+    zv[c] = l > 0.f ? mn + fast_log2(l) : -kFltMax;
+  }
+  if (q < N) {
+    f16* orow = out + ((int64_t)b * N + q) * D + h * DV + c0 + 16 * h32;
+    float* zrow = zb + (rowbase + q) * DV + c0 + 16 * h32;
+    const float ko = sgn * tau * kLn2;
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      f16x8 o;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float z = h32 ? zv[16 + 8 * g + e] : zv[8 * g + e];
+        o[e] = (f16)(z > -kFltMax ? ko * z : 0.f);
+      }
+      *reinterpret_cast<f16x8*>(orow + 8 * g) = o;
+    }
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      float4 z4;
+      z4.x = h32 ? zv[16 + 4 * g] : zv[4 * g];
+      z4.y = h32 ? zv[17 + 4 * g] : zv[4 * g + 1];
+      z4.z = h32 ? zv[18 + 4 * g] : zv[4 * g + 2];
+      z4.w = h32 ? zv[19 + 4 * g] : zv[4 * g + 3];
+      *reinterpret_cast<float4*>(zrow + 4 * g) = z4;
+    }
+  }
+}
+
+template <int M, int DV>
+static hipError_t launch_soft_fwd_t(const Dims& d, const ProjBuffers& p, const float* tau, int sgn, f16* out,
+                                    float* zb, hipStream_t s) {
+  using C = SoftCfg<M, DV>;
+  const dim3 grid(xcd_grid((d.N + C::QW - 1) / C::QW, d.B * d.H));
+  if (d.mask_diag)
+    hipLaunchKernelGGL((soft_fwd_kernel<M, DV, true>), grid, dim3(256), 0, s, p.qa, p.ka, p.vt, p.vlo, p.tstat, tau,
+                       out, zb, d.N, d.NP, d.H, d.D, d.B * d.H, d.causal, (float)sgn);
+  else
+    hipLaunchKernelGGL((soft_fwd_kernel<M, DV, false>), grid, dim3(256), 0, s, p.qa, p.ka, p.vt, p.vlo, p.tstat, tau,
+                       out, zb, d.N, d.NP, d.H, d.D, d.B * d.H, d.causal, (float)sgn);
+  return hipGetLastError();
+}
+
+hipError_t launch_soft_fwd(const Dims& d, const ProjBuffers& p, const float* tau, int sgn, f16* out, float* zb,
+                           hipStream_t s) {
+  MORPHO_MDV_DISPATCH(launch_soft_fwd_t, d, p, tau, sgn, out, zb, s);
+}
+
+// ============================================================ backward prep
+// Per (head, token) row: dcb = sum_c dO_ic (the row sum of ds, for a row with
+// keys), the partial sum of dO . zb for dtau, and the zeroed dq accumulator.
+// DV / 8 consecutive lanes share a row, 8 columns each.
+template <int DV>
+__global__ __launch_bounds__(256) void soft_bwd_prep_kernel(const f16* __restrict__ grad_out,
+                                                            const float* __restrict__ zb, float* __restrict__ dcb,
+                                                            float* __restrict__ dq, float* __restrict__ part,
+                                                            int64_t T, int N, int H, int D, int M) {
+  constexpr int G = DV / 8;
+  __shared__ float red[4];
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t bhn = idx / G;
+  float rs = 0.f, dz = 0.f;
+  bool live = false;
+  if (idx < T * (D / 8)) {
+    const int64_t bh = bhn / N;
+    const int n = (int)(bhn - bh * N), b = (int)(bh / H), h = (int)(bh - (int64_t)b * H);
+    const int c = 8 * (int)(idx & (G - 1));
+    const f16x8 g = *reinterpret_cast<const f16x8*>(grad_out + ((int64_t)b * N + n) * D + h * DV + c);
+    const float4 z0 = *reinterpret_cast<const float4*>(zb + bhn * DV + c);
+    const float4 z1 = *reinterpret_cast<const float4*>(zb + bhn * DV + c + 4);
+    const float z[8] = {z0.x, z0.y, z0.z, z0.w, z1.x, z1.y, z1.z, z1.w};
+    live = z[0] > -kFltMax;  // every column of a row with keys is finite
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      rs += (float)g[e];
+      dz += (float)g[e] * z[e];
+    }
+    if (!live) rs = dz = 0.f;
+  }
+#pragma unroll
+  for (int sh = 1; sh < G; sh <<= 1) rs += __shfl_xor(rs, sh);
+  if (idx < T * (D / 8) && (threadIdx.x & (G - 1)) == 0) dcb[bhn] = rs;
+  // block partial of dO . zb in a fixed order
+#pragma unroll
+  for (int sh = 32; sh >= 1; sh >>= 1) dz += __shfl_xor(dz, sh);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = dz;
+  __syncthreads();
+  if (threadIdx.x == 0) part[blockIdx.x] = (red[0] + red[1]) + (red[2] + red[3]);
+  float4* zq = reinterpret_cast<float4*>(dq);
+  const int64_t nz = T * H * (M / 4);
+  for (int64_t i = idx; i < nz; i += (int64_t)gridDim.x * 256) zq[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+}
+
+int soft_prep_blocks(const Dims& d) { return (int)((d.T * (d.D / 8) + 255) / 256); }
+
+template <int M, int DV>
+static hipError_t launch_soft_bwd_prep_t(const Dims& d, const f16* grad_out, const float* zb, const BwdBuffers& g,
+                                         float* part, hipStream_t s) {
+  hipLaunchKernelGGL((soft_bwd_prep_kernel<DV>), dim3((unsigned)soft_prep_blocks(d)), dim3(256), 0, s, grad_out, zb,
+                     g.dcb, g.dq, part, d.T, d.N, d.H, d.D, d.M);
+  return hipGetLastError();
+}
+
+hipError_t launch_soft_bwd_prep(const Dims& d, const f16* grad_out, const float* zb, const BwdBuffers& g, float* part,
+                                hipStream_t s) {
+  MORPHO_MDV_DISPATCH(launch_soft_bwd_prep_t, d, grad_out, zb, g, part, s);
+}
+
+// ============================================================ backward
+// Workgroup: KB blocks of 32 keys x CG groups of 32 value columns, one wave
+// each; lane = key. Per 32-query step the workgroup stages -zb and dO of the
+// step's queries (fp32 [QT][DV]) and their phi (fp32 [QT][M]); each wave
+// recomputes its S block, accumulates dV and its partial ds over its value
+// columns, and stores the partial ds in LDS; then all threads form
+// dk, dcb += ds^T phi_q (key side, registers) and dq = ds phi_k (query side,
+// fp32 atomics) from the summed partials.
+template <int M, int DV, bool MD>
+__global__ __launch_bounds__(256) void soft_bwd_kernel(const f16* __restrict__ qa, const f16* __restrict__ ka,
+                                                       const f16* __restrict__ vt, const uint8_t* __restrict__ vlo,
+                                                       const float4* __restrict__ tstat, const float* __restrict__ tau_p,
+                                                       const f16* __restrict__ grad_out, const float* __restrict__ zb,
+                                                       float* __restrict__ dq, float* __restrict__ dk,
+                                                       float* __restrict__ dcb, f16* __restrict__ dzv,
+                                                       float* __restrict__ part, int N, int NP, int H, int D, int HM,
+                                                       int BH, int causal, float sgn) {
+  using C = SoftCfg<M, DV>;
+  constexpr int NG = 256 / C::KW;   // dk phase: thread groups per key
+  constexpr int CPT = M / NG;       // dk phase: codes per thread
+  constexpr int CPQ = M / 8;        // dq phase: codes per thread (8 groups per query)
+  __shared__ __align__(16) float snz[C::QT * C::WS];     // -zb of the step's queries
+  __shared__ __align__(16) float sdo[C::QT * C::WS];     // dO of the step's queries
+  __shared__ __align__(16) float sphq[C::QT * C::PS];    // phi of the step's queries
+  __shared__ __align__(16) float sphk[C::KW * C::PS];    // phi of the workgroup's keys
+  __shared__ __align__(16) float sds[C::CG][C::QT * C::DS];  // partial ds per column group: [query][key]
+  __shared__ float red[2][4];
+
+  const int tid = threadIdx.x, lane = tid & 63, h32 = lane >> 5, l32 = lane & 31;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nkb = (N + C::KW - 1) / C::KW;
+  int bh, kblk;
+  if (!(causal ? xcd_map_lpt(nkb, BH, bh, kblk) : xcd_map(nkb, BH, bh, kblk))) {
+    if (tid == 0) {
+      part[2 * blockIdx.x] = 0.f;
+      part[2 * blockIdx.x + 1] = 0.f;
+    }
+    return;
+  }
+  const int k0 = kblk * C::KW, kb = w % C::KB, cg = w / C::KB;
+  const int kw0 = k0 + 32 * kb, c0 = 32 * cg;
+  const int key = kw0 + l32;
+  const bool kvalid = key < N;
+  const int b = bh / H, h = bh - b * H;
+  const int64_t rowbase = (int64_t)bh * N, tokbase = (int64_t)b * N;
+  const float tau = *tau_p;
+  const float ks = sgn / tau, kw = sgn * kLog2e / tau;
+
+  // key operand and this lane's scaled values (fixed for the whole kernel)
+  f16x8 kf[C::NCH];
+  f16x4 kaug = {};
+#pragma unroll
+  for (int c = 0; c < C::NCH; ++c) kf[c] = f16x8{};
+  float wv[32], dv[32];
+#pragma unroll
+  for (int c = 0; c < 32; ++c) {
+    wv[c] = 0.f;
+    dv[c] = 0.f;
+  }
+  if (kvalid) {
+    load_key_operand<M>(ka + (rowbase + key) * C::CW, h32, kf, kaug);
+#pragma unroll
+    for (int c = 0; c < 32; ++c) wv[c] = kw * load_value(vt, vlo, bh, DV, NP, c0 + c, key);
+  }
+  // phi of the workgroup's keys (zero past N)
+  for (int e = tid; e < C::KW * M; e += 256) {
+    const int r = e / M, c = e % M, kk = k0 + r;
+    float v = 0.f;
+    if (kk < N) {
+      const f16* row = qa + (rowbase + kk) * C::CW;
+      v = (float)row[c] + (float)row[M + 8 + c];
+    }
+    sphk[r * C::PS + c] = v;
+  }
+
+  float dka[CPT], dcba = 0.f;
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) dka[i] = 0.f;
+  float st = 0.f;  // sum ds * acc (acc = log2e s)
+
+  const int qstart = causal ? k0 : 0;
+  for (int qs = qstart; qs < N; qs += C::QT) {
+    // ---- stage -zb, dO and phi of queries qs .. qs + QT - 1 (zero past N)
+    for (int e = tid; e < C::QT * DV; e += 256) {
+      const int r = e / DV, c = e % DV, qq = qs + r;
+      float nz = 0.f, g = 0.f;
+      if (qq < N) {
+        nz = -zb[(rowbase + qq) * DV + c];
+        g = (float)grad_out[(tokbase + qq) * D + h * DV + c];
+      }
+      snz[r * C::WS + c] = nz;
+      sdo[r * C::WS + c] = g;
+    }
+    for (int e = tid; e < C::QT * M; e += 256) {
+      const int r = e / M, c = e % M, qq = qs + r;
+      float v = 0.f;
+      if (qq < N) {
+        const f16* row = qa + (rowbase + qq) * C::CW;
+        v = (float)row[c] + (float)row[M + 8 + c];
+      }
+      sphq[r * C::PS + c] = v;
+    }
+    // ---- S block: rows = queries qs + acc_row(r), column = this lane's key
+    f16x8 qf[C::NCH];
+    f16x4 qaug = {};
+#pragma unroll
+    for (int c = 0; c < C::NCH; ++c) qf[c] = f16x8{};
+    if (qs + l32 < N) load_query_operand<M>(qa + (rowbase + qs + l32) * C::CW, tstat[rowbase + qs + l32].x, h32, qf,
+                                            qaug);
+    f32x16 acc = code_dot<M, false>(kf, qf, f32x16{});
+    acc = mfma8(qaug, kaug, acc);
+    float u[16], ds[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int qq = qs + acc_row(r, lane);
+      const bool drop = (qq >= N) | !kvalid | (causal != 0 && key > qq) | (MD && key == qq);
+      u[r] = drop ? kNegInf : ks * acc[r];
+      ds[r] = 0.f;
+    }
+    __syncthreads();  // staging complete
+    // ---- P = 2^(y - zb); ds_ij += dO P over this wave's columns; dV_jc += dO P
+#pragma unroll
+    for (int c4 = 0; c4 < 8; ++c4) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int qr = acc_row(r, lane);
+        const float4 n4 = *reinterpret_cast<const float4*>(snz + qr * C::WS + c0 + 4 * c4);
+        const float4 g4 = *reinterpret_cast<const float4*>(sdo + qr * C::WS + c0 + 4 * c4);
+        const float p0 = fast_exp2(u[r] + wv[4 * c4 + 0] + n4.x);
+        const float p1 = fast_exp2(u[r] + wv[4 * c4 + 1] + n4.y);
+        const float p2 = fast_exp2(u[r] + wv[4 * c4 + 2] + n4.z);
+        const float p3 = fast_exp2(u[r] + wv[4 * c4 + 3] + n4.w);
+        ds[r] = fmaf(p0, g4.x, ds[r]);
+        ds[r] = fmaf(p1, g4.y, ds[r]);
+        ds[r] = fmaf(p2, g4.z, ds[r]);
+        ds[r] = fmaf(p3, g4.w, ds[r]);
+        dv[4 * c4 + 0] = fmaf(p0, g4.x, dv[4 * c4 + 0]);
+        dv[4 * c4 + 1] = fmaf(p1, g4.y, dv[4 * c4 + 1]);
+        dv[4 * c4 + 2] = fmaf(p2, g4.z, dv[4 * c4 + 2]);
+        dv[4 * c4 + 3] = fmaf(p3, g4.w, dv[4 * c4 + 3]);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      st = fmaf(ds[r], acc[r], st);  // ds is 0 wherever the score is masked
+      sds[cg][acc_row(r, lane) * C::DS + 32 * kb + l32] = ds[r];
+    }
+    __syncthreads();  // every partial ds of the step is in LDS
+    // ---- key side: dk_j += sum_i ds_ij phi_i, dcb_j += sum_i ds_ij
+    {
+      const int kk = tid % C::KW, grp = tid / C::KW;
+#pragma unroll 4
+      for (int i = 0; i < C::QT; ++i) {
+        float dsv = 0.f;
+#pragma unroll
+        for (int g = 0; g < C::CG; ++g) dsv += sds[g][i * C::DS + kk];
+        const float* ph = sphq + i * C::PS + grp * CPT;
+#pragma unroll
+        for (int c = 0; c < CPT; ++c) dka[c] = fmaf(dsv, ph[c], dka[c]);
+        dcba += dsv;
+      }
+    }
+    // ---- query side: dq_i += sum_j ds_ij phi_j (fp32 atomics)
+    {
+      const int i = tid % C::QT, grp = tid / C::QT;
+      float dqa[CPQ];
+#pragma unroll
+      for (int c = 0; c < CPQ; ++c) dqa[c] = 0.f;
+#pragma unroll 4
+      for (int kk = 0; kk < C::KW; ++kk) {
+        float dsv = 0.f;
+#pragma unroll
+        for (int g = 0; g < C::CG; ++g) dsv += sds[g][i * C::DS + kk];
+        const float* ph = sphk + kk * C::PS + grp * CPQ;
+#pragma unroll
+        for (int c = 0; c < CPQ; ++c) dqa[c] = fmaf(dsv, ph[c], dqa[c]);
+      }
+      if (qs + i < N) {
+#pragma unroll
+        for (int c = 0; c < CPQ; ++c) unsafeAtomicAdd(dq + (rowbase + qs + i) * M + grp * CPQ + c, dqa[c]);
+      }
+    }
+    __syncthreads();  // LDS tiles are free for the next step
+  }
+
+  // ---- epilogue
+  // dV: the two half-waves hold the same key (different queries)
+  float sv = 0.f;  // sum dV * w over the columns this lane writes
+#pragma unroll
+  for (int c = 0; c < 32; ++c) dv[c] += __shfl_xor(dv[c], 32);
+  if (kvalid) {
+    f16* drow = dzv + (tokbase + key) * (int64_t)(HM + D) + HM + h * DV + c0 + 16 * h32;
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      f16x8 o;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float v = h32 ? dv[16 + 8 * g + e] : dv[8 * g + e];
+        const float wc = h32 ? wv[16 + 8 * g + e] : wv[8 * g + e];
+        o[e] = (f16)v;
+        sv = fmaf(v, wc, sv);
+      }
+      *reinterpret_cast<f16x8*>(drow + 8 * g) = o;
+    }
+  }
+  {
+    const int kk = tid % C::KW, grp = tid / C::KW;
+    if (k0 + kk < N) {
+#pragma unroll
+      for (int c = 0; c < CPT; ++c) dk[(rowbase + k0 + kk) * M + grp * CPT + c] = dka[c];
+      if (grp == 0) dcb[rowbase + k0 + kk] += dcba;  // the prep wrote the row sum
+    }
+  }
+  // dtau partials of the workgroup in a fixed order
+#pragma unroll
+  for (int sh = 32; sh >= 1; sh >>= 1) {
+    st += __shfl_xor(st, sh);
+    sv += __shfl_xor(sv, sh);
+  }
+  if (lane == 0) {
+    red[0][w] = st;
+    red[1][w] = sv;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    part[2 * blockIdx.x] = (red[0][0] + red[0][1]) + (red[0][2] + red[0][3]);
+    part[2 * blockIdx.x + 1] = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
+  }
+}
+
+template <int M, int DV>
+static int soft_bwd_slots_t(const Dims& d) {
+  return (int)xcd_grid((d.N + SoftCfg<M, DV>::KW - 1) / SoftCfg<M, DV>::KW, d.B * d.H);
+}
+int soft_bwd_slots(const Dims& d) { return (int)xcd_grid((d.N + 32 * (128 / d.DV) - 1) / (32 * (128 / d.DV)), d.B * d.H); }
+
+template <int M, int DV>
+static hipError_t launch_soft_bwd_t(const Dims& d, const ProjBuffers& p, const f16* grad_out, const float* zb,
+                                    const float* tau, int sgn, const BwdBuffers& g, float* part, hipStream_t s) {
+  const dim3 grid((unsigned)soft_bwd_slots_t<M, DV>(d));
+  if (d.mask_diag)
+    hipLaunchKernelGGL((soft_bwd_kernel<M, DV, true>), grid, dim3(256), 0, s, p.qa, p.ka, p.vt, p.vlo, p.tstat, tau,
+                       grad_out, zb, g.dq, g.dk, g.dcb, g.dzv, part, d.N, d.NP, d.H, d.D, d.HM, d.B * d.H, d.causal,
+                       (float)sgn);
+  else
+    hipLaunchKernelGGL((soft_bwd_kernel<M, DV, false>), grid, dim3(256), 0, s, p.qa, p.ka, p.vt, p.vlo, p.tstat, tau,
+                       grad_out, zb, g.dq, g.dk, g.dcb, g.dzv, part, d.N, d.NP, d.H, d.D, d.HM, d.B * d.H, d.causal,
+                       (float)sgn);
+  return hipGetLastError();
+}
+
+hipError_t launch_soft_bwd(const Dims& d, const ProjBuffers& p, const f16* grad_out, const float* zb,
+                           const float* tau, int sgn, const BwdBuffers& g, float* part, hipStream_t s) {
+  MORPHO_MDV_DISPATCH(launch_soft_bwd_t, d, p, grad_out, zb, tau, sgn, g, part, s);
+}
+
+// ============================================================ dtau
+// dtau = (sum dO out - sum ds s - sum dV V) / tau with out = sgn tau ln2 zb,
+// s = ln2 acc and V = sgn tau ln2 w:
+//     dtau = ln2 (sgn sum dO zb - (sum ds acc) / tau - sgn sum dV w).
+// One workgroup; each thread sums a strided slice, then a fixed tree.
+__global__ __launch_bounds__(256) void soft_tau_reduce_kernel(const float* __restrict__ prep, int nprep,
+                                                              const float* __restrict__ bwd, int nbwd,
+                                                              const float* __restrict__ tau_p, float sgn,
+                                                              float* __restrict__ dtau) {
+  __shared__ float red[3][256];
+  float a = 0.f, s = 0.f, v = 0.f;
+  for (int i = threadIdx.x; i < nprep; i += 256) a += prep[i];
+  for (int i = threadIdx.x; i < nbwd; i += 256) {
+    s += bwd[2 * i];
+    v += bwd[2 * i + 1];
+  }
+  red[0][threadIdx.x] = a;
+  red[1][threadIdx.x] = s;
+  red[2][threadIdx.x] = v;
+  __syncthreads();
+  for (int w = 128; w >= 1; w >>= 1) {
+    if ((int)threadIdx.x < w) {
+      red[0][threadIdx.x] += red[0][threadIdx.x + w];
+      red[1][threadIdx.x] += red[1][threadIdx.x + w];
+      red[2][threadIdx.x] += red[2][threadIdx.x + w];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    const float tau = *tau_p;
+    dtau[0] = kLn2 * (sgn * red[0][0] - red[1][0] / tau - sgn * red[2][0]);
+  }
+}
+
+hipError_t launch_soft_tau_reduce(const float* prep, int nprep, const float* bwd, int nbwd, const float* tau, int sgn,
+                                  float* dtau, hipStream_t s) {
+  hipLaunchKernelGGL(soft_tau_reduce_kernel, dim3(1), dim3(256), 0, s, prep, nprep, bwd, nbwd, tau, (float)sgn, dtau);
+  return hipGetLastError();
+}
+
+}  // namespace morpho

@@ -152,6 +152,77 @@ std::vector<at::Tensor> op_backward_train(const at::Tensor& grad_out, const at::
                        variant);
 }
 
+// ---- soft tropical aggregation (no reference op: the reference defines the
+// accumulators of morfology/soft_morph.cuh but never wires them)
+void check_tau(const at::Tensor& tau, const at::Tensor& X) {
+  TORCH_CHECK(tau.is_cuda() && tau.device() == X.device(), "tau must be a CUDA tensor on the device of X");
+  TORCH_CHECK(tau.scalar_type() == at::kFloat && tau.numel() == 1 && tau.is_contiguous(),
+              "tau must be one contiguous float32 element");
+}
+
+int sgn_of(int64_t sgn) {
+  TORCH_CHECK(sgn == 1 || sgn == -1, "sgn must be +1 (dilation) or -1 (erosion), got ", sgn);
+  return (int)sgn;
+}
+
+std::vector<at::Tensor> op_soft_forward(const at::Tensor& X, const at::Tensor& W_phi, const at::Tensor& gate_q,
+                                        const at::Tensor& gate_k, const at::Tensor& W_V, const at::Tensor& tau,
+                                        int64_t H, int64_t cube_m, double scale, bool causal, int64_t sgn,
+                                        int64_t variant) {
+  const int mode = mode_of(causal, variant);
+  const int sg = sgn_of(sgn);
+  const Shape s = check_inputs(X, W_phi, gate_q, gate_k, W_V, H, cube_m);
+  check_tau(tau, X);
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(X.device());
+  auto out = at::empty_like(X);
+  auto zb = at::empty({s.B * H, s.N, s.D / H}, X.options().dtype(at::kFloat));
+  const size_t ws_bytes = morpho_forward_workspace_size(s.B, s.N, s.D, s.H, s.M);
+  TORCH_CHECK(ws_bytes > 0, "morphottention soft_forward: unsupported sizes (cube_m must be 16, 32 or 64; "
+              "D / H must be 32, 64 or 128)");
+  auto ws = at::empty({(int64_t)ws_bytes}, X.options().dtype(at::kByte));
+  raise_on(morpho_soft_forward(X.data_ptr(), W_phi.data_ptr(), gate_q.data_ptr(), gate_k.data_ptr(), W_V.data_ptr(),
+                               tau.data_ptr<float>(), out.data_ptr(), zb.data_ptr<float>(), s.B, s.N, s.D, s.H, s.M,
+                               (float)scale, mode, sg, ws.data_ptr(), ws_bytes, current_stream(X)),
+           "soft_forward");
+  return {out, zb, ws};
+}
+
+std::vector<at::Tensor> op_soft_backward(const at::Tensor& grad_out, const at::Tensor& X, const at::Tensor& W_phi,
+                                         const at::Tensor& gate_q, const at::Tensor& gate_k, const at::Tensor& W_V,
+                                         const at::Tensor& tau, const at::Tensor& zb, const at::Tensor& workspace,
+                                         int64_t H, int64_t cube_m, double scale, bool causal, int64_t sgn,
+                                         int64_t variant) {
+  const int mode = mode_of(causal, variant);
+  const int sg = sgn_of(sgn);
+  check(grad_out, "grad_out");
+  const Shape s = check_inputs(X, W_phi, gate_q, gate_k, W_V, H, cube_m);
+  check_tau(tau, X);
+  TORCH_CHECK(grad_out.sizes() == X.sizes(), "grad_out must match X shape [B, N, D]");
+  TORCH_CHECK(zb.is_cuda() && zb.scalar_type() == at::kFloat && zb.is_contiguous() && zb.dim() == 3 &&
+                  zb.size(0) == s.B * H && zb.size(1) == s.N && zb.size(2) == s.D / H,
+              "zb must be the float32 [B*H, N, D/H] tensor of soft_forward");
+  const size_t need = morpho_forward_workspace_size(s.B, s.N, s.D, s.H, s.M);
+  TORCH_CHECK(workspace.is_cuda() && workspace.scalar_type() == at::kByte && workspace.is_contiguous() &&
+                  (size_t)workspace.numel() >= need,
+              "workspace must be the uint8 CUDA tensor returned by soft_forward for these sizes");
+  const c10::hip::HIPGuardMasqueradingAsCUDA guard(X.device());
+  auto dX = at::empty_like(X);
+  auto dW_phi = at::empty_like(W_phi);
+  auto d_gate_q = at::empty_like(gate_q);
+  auto d_gate_k = at::empty_like(gate_k);
+  auto dW_V = at::empty_like(W_V);
+  auto dtau = at::empty_like(tau);
+  const size_t ws_bytes = morpho_soft_backward_workspace_size(s.B, s.N, s.D, s.H, s.M, 1);
+  auto ws = at::empty({(int64_t)ws_bytes}, X.options().dtype(at::kByte));
+  raise_on(morpho_soft_backward(grad_out.data_ptr(), X.data_ptr(), W_phi.data_ptr(), gate_q.data_ptr(),
+                                gate_k.data_ptr(), W_V.data_ptr(), tau.data_ptr<float>(), zb.data_ptr<float>(),
+                                dX.data_ptr(), dW_phi.data_ptr(), d_gate_q.data_ptr(), d_gate_k.data_ptr(),
+                                dW_V.data_ptr(), dtau.data_ptr<float>(), s.B, s.N, s.D, s.H, s.M, (float)scale, mode,
+                                sg, workspace.data_ptr(), ws.data_ptr(), ws_bytes, current_stream(X)),
+           "soft_backward");
+  return {dX, dW_phi, d_gate_q, d_gate_k, dW_V, dtau};
+}
+
 }  // namespace
 
 TORCH_LIBRARY(morphottention, m) {
@@ -164,6 +235,11 @@ TORCH_LIBRARY(morphottention, m) {
   m.def("backward_train(Tensor grad_out, Tensor X, Tensor W_phi, Tensor gate_q, Tensor gate_k, "
         "Tensor W_V, Tensor out, Tensor lse, Tensor workspace, int H, int cube_m, float scale, bool causal, "
         "int variant=0) -> Tensor[]");
+  m.def("soft_forward(Tensor X, Tensor W_phi, Tensor gate_q, Tensor gate_k, Tensor W_V, Tensor tau, "
+        "int H, int cube_m, float scale, bool causal, int sgn, int variant=0) -> Tensor[]");
+  m.def("soft_backward(Tensor grad_out, Tensor X, Tensor W_phi, Tensor gate_q, Tensor gate_k, Tensor W_V, "
+        "Tensor tau, Tensor zb, Tensor workspace, int H, int cube_m, float scale, bool causal, int sgn, "
+        "int variant=0) -> Tensor[]");
 }
 
 TORCH_LIBRARY_IMPL(morphottention, CUDA, m) {
@@ -171,4 +247,6 @@ TORCH_LIBRARY_IMPL(morphottention, CUDA, m) {
   m.impl("backward", &op_backward);
   m.impl("forward_train", &op_forward_train);
   m.impl("backward_train", &op_backward_train);
+  m.impl("soft_forward", &op_soft_forward);
+  m.impl("soft_backward", &op_soft_backward);
 }

@@ -31,6 +31,16 @@ mathematically complete gradient (the reference CUDA backward drops the
 query-side code gradient, ``attention.cu:446-451,472-482``; that defect is not
 reproduced).
 
+* soft tropical aggregation (``soft_morph_ref``, ``soft_morph_brute_force``)
+               ``packages/morphottention/csrc/cuda/morfology/soft_morph.cuh:10-77``
+  (``out = sgn tau ln sum_j exp(sgn (s_ij + V_jc) / tau)`` from the
+  ``lse_update`` / ``lse_merge`` / ``lse_finalize`` accumulators, which the
+  reference defines but never calls; pinned in ``tests/test_soft_morph_oracle.py``
+  against a scalar restatement of those accumulators, the hard max-plus /
+  min-plus limit, the large-tau (Hoeffding) bound, erosion-dilation duality,
+  the single-key case, the partition of unity of the weights, the
+  tau-gradient identity and fp64 gradcheck)
+
 Pinning (all in ``tests/test_oracle.py``): fp64 ``gradcheck``; equivalence with
 ``F.scaled_dot_product_attention`` on augmented operands; a brute-force
 pure-Python loop restatement; the binary-hypercube Hamming closed form; causal
@@ -276,3 +286,156 @@ def sdpa_equivalent(x, W_phi, gate_q, gate_k, W_V, num_heads: int, cube_m: int, 
     V = (x @ W_V.to(x.dtype)).view(B, N, H, dv).permute(0, 2, 1, 3)
     O = F.scaled_dot_product_attention(Qt, Kt, V, is_causal=causal, scale=1.0)
     return O.permute(0, 2, 1, 3).reshape(B, N, D)
+
+
+# ---------------------------------------------------------------------------
+# Soft tropical aggregation (packages/morphottention/csrc/cuda/morfology/
+# soft_morph.cuh:10-77). The reference defines the accumulators but never
+# calls them; here they aggregate the values with the morpho scores in place
+# of the softmax-weighted sum:
+#     out_ic = sgn * tau * ln sum_j exp(sgn * (s_ij + V_jc) / tau)
+# sgn = +1 is the soft max-plus product (dilation), sgn = -1 the soft
+# min-plus product (erosion); s_ij are the natural-log scores above.
+
+
+def values(x, W_V, num_heads: int):
+    """Per-head values ``V = X W_V,h`` shaped ``[B, H, N, dv]``."""
+    B, N, _ = x.shape
+    dv = W_V.shape[1] // num_heads
+    return (x @ W_V.to(x.dtype)).view(B, N, num_heads, dv).permute(0, 2, 1, 3)
+
+
+def soft_morph_ref(x, W_phi, gate_q, gate_k, W_V, tau, num_heads: int, cube_m: int, *,
+                   scale: float = 1.0, causal: bool = False, sgn: float = 1.0,
+                   projection: str = "sigmoid", mask_diag: bool = False, return_zb: bool = False):
+    """Soft tropical aggregation in the dtype of ``x`` (fp32 or fp64).
+
+    ``morph_accumulate`` folds ``sgn * (s + v) / tau`` (``soft_morph.cuh:35-38``)
+    into a log-sum-exp (``:21-32,41-52``) and ``lse_finalize`` returns
+    ``sgn * tau * (m + log l)`` (``:66-69``). ``tau`` is a float or a 0-d
+    tensor (differentiable). Returns ``out [B, N, D]`` and, with ``return_zb``,
+    the base-2 normaliser ``zb = log2 sum_j 2^(log2e sgn (s_ij + V_jc) / tau)``
+    shaped ``[B*H, N, dv]`` (so ``out = sgn tau ln2 zb``). A row without keys
+    gives ``out = 0`` and ``zb = -FLT_MAX``.
+    """
+    B, N, D = x.shape
+    H, m = num_heads, cube_m
+    W_phi = W_phi.to(x.dtype)
+    _, q, k, qb, cb = project(x, W_phi, gate_q, gate_k, H, m, projection)
+    s = scores(q, k, qb, cb, scale)                             # [B, H, N, N]
+    V = values(x, W_V, H)                                       # [B, H, N, dv]
+    dv = V.shape[-1]
+    y = sgn * (s[..., :, :, None] + V[..., None, :, :]) / tau   # [B, H, Nq, Nk, dv]
+    mask = drop_mask(N, x.device, causal, mask_diag)
+    empty = None
+    if mask is not None:
+        y = y.masked_fill(mask[:, :, None], float("-inf"))
+        empty = mask.all(dim=-1)
+        if bool(empty.any()):
+            y = y.masked_fill(empty[:, None, None], 0.0)
+        else:
+            empty = None
+    lse = torch.logsumexp(y, dim=-2)                            # [B, H, N, dv]
+    O = sgn * tau * lse
+    if empty is not None:
+        O = O.masked_fill(empty[:, None], 0.0)
+    out = O.permute(0, 2, 1, 3).reshape(B, N, H * dv)
+    if not return_zb:
+        return out
+    zb = lse * LOG2E
+    if empty is not None:
+        zb = zb.masked_fill(empty[:, None], -FLT_MAX)
+    return out, zb.reshape(B * H, N, dv)
+
+
+def soft_morph_ref_grads(x, W_phi, gate_q, gate_k, W_V, tau: float, num_heads: int, cube_m: int, *,
+                         scale: float = 1.0, causal: bool = False, sgn: float = 1.0, dout=None,
+                         dtype=torch.float32, batch_chunk: int | None = None, head_chunk: int | None = None,
+                         projection: str = "sigmoid", mask_diag: bool = False):
+    """Forward + autograd backward of ``soft_morph_ref``, chunked over batch
+    and heads (exact, as in ``morpho_attention_ref_grads``). Returns ``out, zb,
+    (dX, dW_phi, d_gate_q, d_gate_k, dW_V, dtau)``."""
+    B, N, D = x.shape
+    H, m = num_heads, cube_m
+    dv = D // H
+    bc = batch_chunk or B
+    hc = head_chunk or H
+    params = [p.detach().to(dtype).clone().requires_grad_(True) for p in (W_phi, gate_q, gate_k, W_V)]
+    t = torch.tensor(float(tau), dtype=dtype, device=x.device, requires_grad=True)
+    out = torch.empty(B, N, D, dtype=dtype, device=x.device)
+    zb = torch.empty(B, H, N, dv, dtype=dtype, device=x.device)
+    dX = torch.zeros(B, N, D, dtype=dtype, device=x.device)
+    for b0 in range(0, B, bc):
+        b1 = min(B, b0 + bc)
+        xb = x[b0:b1].detach().to(dtype).clone().requires_grad_(True)
+        g_full = torch.ones(b1 - b0, N, D, dtype=dtype, device=x.device) if dout is None \
+            else dout[b0:b1].to(dtype)
+        for h0 in range(0, H, hc):
+            h1 = min(H, h0 + hc)
+            o, z = soft_morph_ref(xb, params[0][:, h0 * m:h1 * m], params[1][h0:h1], params[2][h0:h1],
+                                  params[3][:, h0 * dv:h1 * dv], t, h1 - h0, m, scale=scale, causal=causal,
+                                  sgn=sgn, projection=projection, mask_diag=mask_diag, return_zb=True)
+            o.backward(g_full[:, :, h0 * dv:h1 * dv])
+            out[b0:b1, :, h0 * dv:h1 * dv] = o.detach()
+            zb[b0:b1, h0:h1] = z.detach().view(b1 - b0, h1 - h0, N, dv)
+        dX[b0:b1] = xb.grad.detach()
+    grads = (dX, *(p.grad.detach() for p in params), t.grad.detach())
+    return out, zb.reshape(B * H, N, dv), grads
+
+
+def soft_morph_brute_force(x, W_phi, gate_q, gate_k, W_V, tau: float, num_heads: int, cube_m: int, *,
+                           scale: float = 1.0, causal: bool = False, sgn: float = 1.0, split: int = 2):
+    """Pure-Python scalar restatement of the reference accumulators (tiny inputs).
+
+    Per (query, value column): the keys are dealt round-robin into ``split``
+    accumulators, each folded key by key with ``lse_update``
+    (``soft_morph.cuh:27-31``) of ``sgn (s + v) / tau``; the partial
+    accumulators are combined with ``lse_merge`` (``:41-52``), as the
+    reference's warp reduction does (``:54-63``), and finished with
+    ``lse_finalize`` (``:66-69``). Returns nested lists ``out[b][i][d]``.
+    """
+    B, N, D = x.shape
+    H, m = num_heads, cube_m
+    dv = D // H
+    X = x.tolist()
+    Wp = W_phi.tolist()
+    Wv = W_V.tolist()
+    gq = gate_q.tolist()
+    gk = gate_k.tolist()
+    inv_tau = 1.0 / tau
+
+    def update(acc, a):
+        mm, ll = acc
+        m_new = max(mm, a)
+        return (m_new, ll * math.exp(mm - m_new) + math.exp(a - m_new))
+
+    def merge(a, b):
+        if a[0] == -math.inf:
+            return b
+        if b[0] == -math.inf:
+            return a
+        m_new = max(a[0], b[0])
+        return (m_new, a[1] * math.exp(a[0] - m_new) + b[1] * math.exp(b[0] - m_new))
+
+    out = [[[0.0] * D for _ in range(N)] for _ in range(B)]
+    for b in range(B):
+        for h in range(H):
+            phi = [[1.0 / (1.0 + math.exp(-sum(X[b][t][d] * Wp[d][h * m + c] for d in range(D))))
+                    for c in range(m)] for t in range(N)]
+            qc = [[gq[h][c] * phi[t][c] for c in range(m)] for t in range(N)]
+            kc = [[gk[h][c] * phi[t][c] for c in range(m)] for t in range(N)]
+            qb = [sum(gk[h][c] * qc[t][c] for c in range(m)) for t in range(N)]
+            cb = [sum(gq[h][c] * kc[t][c] for c in range(m)) for t in range(N)]
+            V = [[sum(X[b][t][d] * Wv[d][h * dv + e] for d in range(D)) for e in range(dv)] for t in range(N)]
+            for i in range(N):
+                keys = [j for j in range(N) if not (causal and j > i)]
+                s = {j: scale * (2.0 * sum(qc[i][c] * kc[j][c] for c in range(m)) - qb[i] - cb[j]) for j in keys}
+                for e in range(dv):
+                    parts = [(-math.inf, 0.0) for _ in range(split)]
+                    for n, j in enumerate(keys):
+                        parts[n % split] = update(parts[n % split], sgn * (s[j] + V[j][e]) * inv_tau)
+                    acc = parts[0]
+                    for p in parts[1:]:
+                        acc = merge(acc, p)
+                    out[b][i][h * dv + e] = sgn * tau * (acc[0] + math.log(acc[1]))
+    return out

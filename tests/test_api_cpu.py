@@ -199,3 +199,50 @@ def test_multihead_self_attention_wrapper_contract():
     x = torch.randn(1, 8, 128)
     with pytest.raises(ValueError, match="CUDA tensor"):
         layer2(x, x, x)
+
+
+def test_soft_entry_points_validate_without_the_device():
+    from morphottention_amd import capi
+    L = capi.lib()
+    vp = ctypes.c_void_p(4096)
+    ws = 1 << 20
+    # sgn must be +-1; tau must be given
+    st = L.morpho_soft_forward(vp, vp, vp, vp, vp, vp, vp, vp, 2, 8, 64, 2, 16, 1.0, 0, 2, vp, ws, None)
+    assert st == 1 and b"sgn" in L.morpho_last_error()
+    st = L.morpho_soft_forward(vp, vp, vp, vp, vp, None, vp, vp, 2, 8, 64, 2, 16, 1.0, 0, 1, vp, ws, None)
+    assert st == 1 and b"tau" in L.morpho_last_error()
+    st = L.morpho_soft_forward(vp, vp, vp, vp, vp, vp, vp, vp, 2, 8, 64, 2, 16, 1.0, 16, 1, vp, ws, None)
+    assert st == 1 and b"invalid mode bits" in L.morpho_last_error()
+    st = L.morpho_soft_backward(*([vp] * 14), 2, 8, 64, 2, 16, 1.0, 0, -3, None, vp, ws, None)
+    assert st == 1 and b"sgn" in L.morpho_last_error()
+    need_fwd = capi.soft_backward_workspace_size(2, 8, 64, 2, 16, True)
+    assert need_fwd > capi.backward_workspace_size(2, 8, 64, 2, 16, True)
+    assert capi.soft_backward_workspace_size(2, 8, 64, 2, 16, False) == need_fwd + capi.forward_workspace_size(
+        2, 8, 64, 2, 16)
+    assert capi.soft_backward_workspace_size(2, 8, 64, 2, 24, True) == 0
+
+
+def test_soft_fake_kernels_and_module():
+    import morphottention_amd  # noqa: F401
+    from morphottention_amd import SoftMorphAttention
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    ops = torch.ops.morphottention
+    with FakeTensorMode():
+        X = torch.empty(2, 8, 64, dtype=torch.float16, device="cuda")
+        W = torch.empty(64, 32, dtype=torch.float16, device="cuda")
+        g = torch.empty(2, 16, dtype=torch.float16, device="cuda")
+        V = torch.empty(64, 64, dtype=torch.float16, device="cuda")
+        t = torch.empty(1, dtype=torch.float32, device="cuda")
+        out, zb, ws = ops.soft_forward(X, W, g, g, V, t, 2, 16, 1.0, True, 1)
+        assert out.shape == X.shape and zb.shape == (4, 8, 32) and zb.dtype == torch.float32
+        grads = ops.soft_backward(out, X, W, g, g, V, t, zb, ws, 2, 16, 1.0, True, -1)
+        assert [x.shape for x in grads] == [X.shape, W.shape, g.shape, g.shape, V.shape, t.shape]
+    mod = SoftMorphAttention(64, 2, 16, tau=0.3, erosion=True, dtype=torch.float32, device="cpu")
+    assert set(dict(mod.named_parameters())) == {"W_phi", "gate_q", "gate_k", "W_V", "tau"}
+    assert mod.sgn == -1 and mod.tau.dtype == torch.float32 and float(mod.tau) == pytest.approx(0.3)
+    fixed = SoftMorphAttention(64, 2, 16, learn_tau=False, device="cpu")
+    assert "tau" not in dict(fixed.named_parameters()) and "tau" in dict(fixed.named_buffers())
+    with pytest.raises(ValueError, match="tau"):
+        SoftMorphAttention(64, 2, 16, tau=0.0)
+    with pytest.raises(ValueError, match="CUDA tensor"):
+        mod(torch.randn(1, 4, 64))

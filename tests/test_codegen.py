@@ -68,5 +68,5 @@ def test_no_kernel_has_an_empty_divergent_block(tmp_path):
     with concurrent.futures.ThreadPoolExecutor(max_workers=len(sources)) as ex:
         results = list(ex.map(asm_of, sources))
     for src, asm in results:
-        assert "attn_bwd_kernel" in asm or "proj_fwd_kernel" in asm
+        assert re.search(r"^_ZN6morpho\w*_kernel", asm, re.M), src  # the file's kernels were compiled
         assert empty_divergent_blocks(asm) == {}, src

@@ -1,0 +1,180 @@
+"""GPU parity of the soft tropical aggregation against the oracle.
+
+``mo.soft_morph_ref`` (pinned in ``tests/test_soft_morph_oracle.py``) in fp32
+on the same fp16 inputs is the reference. Bars:
+
+* the output beyond half an fp16 ulp of itself <= 2e-3;
+* the fp32 normaliser zb, in output units (tau ln2 |zb - zb_ref|, the error
+  of the output before its fp16 rounding), <= 2^-13 max|V| + 1e-4: the
+  values carry V_hi + an e4m3 remainder, exact to < 2^-14 |V|, and zb scales
+  as 1/tau, so a bar on zb itself would tighten as tau shrinks;
+* per gradient tensor max|g - g_ref| / max|g_ref| <= 1e-2; for dtau, which is
+  a difference of sums (exactly 0 with one key), the bar is 1e-2 |dtau_ref|
+  + 2e-6 sum|dO out| / tau (fp32 cancellation noise of its terms).
+"""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from oracle import morpho_oracle as mo
+
+pytestmark = pytest.mark.gpu
+
+FWD_TOL = 2e-3
+GRAD_TOL = 1e-2
+NAMES = ("dX", "dW_phi", "d_gate_q", "d_gate_k", "dW_V", "dtau")
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no ROCm GPU")
+    import morphottention_amd  # noqa: F401
+    torch.backends.cuda.matmul.allow_tf32 = False
+    yield
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def _half_ulp(x):
+    a = x.abs().clamp_min(2.0 ** -14)
+    return torch.exp2(torch.floor(torch.log2(a)) - 11)
+
+
+def _inputs(B, N, H, m, dv, seed, x_mult=1.0):
+    from morphottention_amd import MorphoAttention
+    torch.manual_seed(seed)
+    mod = MorphoAttention(H * dv, H, m, dtype=torch.float16, device="cpu")
+    params = [mod.W_phi.detach(), mod.gate_q.detach(), mod.gate_k.detach(), mod.W_V.detach()]
+    g = torch.Generator().manual_seed(seed + 1)
+    params[1] = (1.0 + 0.3 * torch.randn(H, m, generator=g)).half()
+    params[2] = (1.0 + 0.3 * torch.randn(H, m, generator=g)).half()
+    x = (x_mult * torch.randn(B, N, H * dv, generator=g)).half()
+    dout = torch.randn(B, N, H * dv, generator=g)
+    return x.cuda(), [p.cuda() for p in params], dout.cuda().half()
+
+
+def _run(x, params, tau, H, m, scale, causal, sgn, dout, projection="sigmoid", mask_diag=False):
+    from morphottention_amd import soft_morph_attention
+    leaves = [t.detach().clone().requires_grad_(True) for t in (x, *params)]
+    t = torch.tensor([tau], dtype=torch.float32, device="cuda", requires_grad=True)
+    out = soft_morph_attention(leaves[0], *leaves[1:], t, H, m, scale=scale, causal=causal, erosion=sgn < 0,
+                               projection=projection, mask_diag=mask_diag)
+    out.backward(dout)
+    from morphottention_amd.autograd import variant_bits
+    _, zb, _ = torch.ops.morphottention.soft_forward(x, *params, t.detach(), H, m, scale, causal, sgn,
+                                                     variant_bits(projection, mask_diag))
+    torch.cuda.synchronize()
+    return out.detach(), zb, [l.grad for l in leaves] + [t.grad]
+
+
+def _check(name, out, zb, grads, x, params, tau, H, m, scale, causal, sgn, dout, projection="sigmoid",
+           mask_diag=False):
+    ref_out, ref_zb, ref_grads = mo.soft_morph_ref_grads(x, *params, tau, H, m, scale=scale, causal=causal, sgn=sgn,
+                                                         dout=dout, dtype=torch.float32, projection=projection,
+                                                         mask_diag=mask_diag)
+    err = (out.float() - ref_out).abs()
+    excess = (err - _half_ulp(ref_out)).clamp_min(0).max().item()
+    live = ref_zb > -1e38
+    zerr = (tau * math.log(2.0) * (zb - ref_zb).abs()).masked_fill(~live, 0.0).max().item()
+    vmax = mo.values(x.float(), params[3].float(), H).abs().max().item()
+    zbar = 2.0 ** -13 * vmax + 1e-4
+    rels = []
+    for g, gr in zip(grads, ref_grads):
+        gr = gr.float().reshape(g.shape)
+        rels.append((g.float() - gr).abs().max().item() / max(gr.abs().max().item(), 1e-30))
+    dtau_err = (grads[5].float() - ref_grads[5].float().reshape(grads[5].shape)).abs().item()
+    dtau_bar = 1e-2 * ref_grads[5].abs().item() + 2e-6 * (dout.float() * ref_out).abs().sum().item() / tau
+    _say(f"[soft] {name}: fwd max-abs {err.max().item():.3e} beyond rounding {excess:.3e} zb (output units) "
+         f"{zerr:.2e} (bar {zbar:.2e}) max|out| {ref_out.abs().max().item():.2f} grads "
+         + " ".join(f"{n}={r:.2e}" for n, r in zip(NAMES[:5], rels)) + f" dtau {dtau_err:.2e} of {ref_grads[5].abs().item():.2e} (bar {dtau_bar:.2e})")
+    assert torch.isfinite(out).all() and all(torch.isfinite(g).all() for g in grads)
+    assert excess <= FWD_TOL, f"{name}: forward error beyond fp16 rounding {excess}"
+    assert zerr <= zbar, f"{name}: zb error {zerr} in output units"
+    for n, r in zip(NAMES[:5], rels):
+        assert r <= GRAD_TOL, f"{name}: {n} relative error {r}"
+    assert dtau_err <= dtau_bar, f"{name}: dtau error {dtau_err}"
+
+
+@pytest.mark.parametrize("sgn", [1, -1], ids=["dilation", "erosion"])
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+@pytest.mark.parametrize("m,dv", [(16, 64), (32, 32), (64, 128)])
+def test_soft_matches_oracle(m, dv, causal, sgn):
+    B, N, H, tau, scale = 2, 100, 2, 0.5, 0.8
+    _say(f"[case] soft m={m} dv={dv} causal={causal} sgn={sgn} N={N} tau={tau}")
+    x, params, dout = _inputs(B, N, H, m, dv, seed=500 + m + dv)
+    out, zb, grads = _run(x, params, tau, H, m, scale, causal, sgn, dout)
+    _check(f"m{m} dv{dv} {'causal' if causal else 'full'} sgn{sgn:+d}", out, zb, grads, x, params, tau, H, m, scale,
+           causal, sgn, dout)
+
+
+@pytest.mark.parametrize("tau", [0.05, 4.0])
+def test_soft_temperatures(tau):
+    B, N, H, m, dv = 2, 129, 2, 16, 64
+    _say(f"[case] soft tau={tau} N={N}")
+    x, params, dout = _inputs(B, N, H, m, dv, seed=600)
+    out, zb, grads = _run(x, params, tau, H, m, 1.0, True, 1, dout)
+    _check(f"tau {tau}", out, zb, grads, x, params, tau, H, m, 1.0, True, 1, dout)
+
+
+@pytest.mark.parametrize("N", [1, 33, 300])
+def test_soft_ragged_lengths(N):
+    B, H, m, dv = 1, 2, 32, 64
+    _say(f"[case] soft N={N}")
+    x, params, dout = _inputs(B, N, H, m, dv, seed=700 + N)
+    out, zb, grads = _run(x, params, 0.7, H, m, 0.9, False, -1, dout)
+    _check(f"N {N}", out, zb, grads, x, params, 0.7, H, m, 0.9, False, -1, dout)
+
+
+def test_soft_variants_masked_diagonal_and_projection():
+    """Causal with the diagonal masked leaves query 0 without keys: out 0,
+    zb -FLT_MAX, and no NaN in any gradient; HardTanh01 projection."""
+    B, N, H, m, dv = 2, 70, 2, 16, 32
+    _say(f"[case] soft mask_diag hardtanh01 N={N}")
+    x, params, dout = _inputs(B, N, H, m, dv, seed=800, x_mult=2.0)
+    out, zb, grads = _run(x, params, 0.4, H, m, 0.8, True, 1, dout, projection="hardtanh01", mask_diag=True)
+    assert bool((out[:, 0] == 0).all()) and bool((zb.view(B, H, N, dv)[:, :, 0] == -mo.FLT_MAX).all())
+    _check("mask_diag hardtanh01", out, zb, grads, x, params, 0.4, H, m, 0.8, True, 1, dout,
+           projection="hardtanh01", mask_diag=True)
+
+
+def test_small_tau_tends_to_the_hard_tropical_product():
+    """tau = 1e-3: max_j (s + V) <= out <= max_j (s + V) + tau ln n, up to the
+    fp16 rounding of out and the fp16 inputs' projection in fp32."""
+    from morphottention_amd import soft_morph_attention
+    B, N, H, m, dv, tau = 1, 64, 2, 16, 32, 1e-3
+    x, params, _ = _inputs(B, N, H, m, dv, seed=900)
+    t = torch.tensor([tau], dtype=torch.float32, device="cuda")
+    for sgn in (1, -1):
+        out = soft_morph_attention(x, *params, t, H, m, scale=1.0, causal=True, erosion=sgn < 0).float()
+        xf = x.float()
+        _, q, k, qb, cb = mo.project(xf, params[0].float(), params[1].float(), params[2].float(), H, m)
+        s = mo.scores(q, k, qb, cb, 1.0)
+        V = mo.values(xf, params[3].float(), H)
+        xs = s[..., :, :, None] + V[..., None, :, :]
+        keep = ~mo.causal_mask(N, "cuda")[:, :, None]
+        hard = (xs.masked_fill(~keep, -math.inf).amax(-2) if sgn > 0 else xs.masked_fill(~keep, math.inf).amin(-2))
+        o = out.view(B, N, H, dv).permute(0, 2, 1, 3)
+        slack = tau * math.log(N) + _half_ulp(hard).max().item() + 1e-3
+        dev = (o - hard).abs().max().item()
+        _say(f"[soft] hard limit sgn {sgn:+d}: max |out - hard| {dev:.3e} (slack {slack:.3e})")
+        assert dev <= slack
+
+
+def test_soft_module_trains_tau():
+    """SoftMorphAttention: tau is a parameter and receives a finite gradient;
+    the output is deterministic across calls."""
+    from morphottention_amd import SoftMorphAttention
+    torch.manual_seed(3)
+    mod = SoftMorphAttention(128, 2, 16, scale=0.7, causal=True, tau=0.6, device="cuda")
+    x = torch.randn(2, 50, 128, device="cuda").half()
+    out = mod(x)
+    out.float().square().mean().backward()
+    assert mod.tau.grad is not None and torch.isfinite(mod.tau.grad).all()
+    assert torch.equal(out.detach(), mod(x).detach())
