@@ -193,6 +193,70 @@ def bench_layer(args):
     }), flush=True)
 
 
+def bench_soft(args):
+    """fwd+bwd of the soft tropical aggregation (SoftMorphAttentionFunction,
+    learnable tau) at a config's shape. Its kernels do one exp2 per (query,
+    key, value column): the bound is the exponential unit, reported as
+    achieved exponentials per second against the rate measured on the box.
+    One JSON line."""
+    from morphottention_amd import SoftMorphAttentionFunction, capi
+    B, N, D, H, m, scale, causal, seed, xm = CONFIGS[args.config]
+    dv = D // H
+    dev = torch.device("cuda:0")
+    x, params, dout = make_inputs(CONFIGS[args.config], dev)
+    tau = torch.full((1,), args.tau, dtype=torch.float32, device=dev, requires_grad=True)
+    sgn = -1 if args.erosion else 1
+    leaves = [x, *params, tau]
+
+    def step():
+        out = SoftMorphAttentionFunction.apply(x, *params, tau, H, m, scale, causal, sgn)
+        return torch.autograd.grad(out, leaves, dout)
+
+    for _ in range(args.warmup):
+        step()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    capi.timing_enable(True)
+    capi.timing_read()
+    for _ in range(args.timing_steps):
+        step()
+    torch.cuda.synchronize()
+    recs = capi.timing_read()
+    capi.timing_enable(False)
+    per = {}
+    for name, t in recs:
+        per.setdefault(name, []).append(t)
+    elems = pairs(B, N, H, causal) * dv  # one exp2 per (query, key, column) in each of soft_fwd and soft_bwd
+    kernels = {}
+    for name, v in sorted(per.items(), key=lambda kv: -sum(kv[1])):
+        avg = sum(v) / len(v)
+        rate = elems / (avg * 1e-3) if name in ("soft_fwd", "soft_bwd") else None
+        kernels[name] = {"avg_ms": round(avg, 5), "exp_per_s": rate and round(rate / 1e12, 3)}
+        log(f"  {name:18s} {avg:8.4f} ms" + (f"  {rate / 1e12:.2f}e12 exp/s ({rate / PEAK_EXP_PER_S:.1%} of "
+                                             f"{PEAK_EXP_PER_S / 1e12:.1f}e12)" if rate else ""))
+    log(f"soft step {ms:.4f} ms")
+    dom = "soft_bwd" if sum(per.get("soft_bwd", [0])) >= sum(per.get("soft_fwd", [0])) else "soft_fwd"
+    dom_avg = sum(per[dom]) / len(per[dom])
+    print(json.dumps({
+        "metric": "soft tropical aggregation fwd+bwd tokens/s",
+        "value": round(B * N / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp16 in/out, fp32 exponent arithmetic", "data": "synthetic",
+        "config": {"workload": f"{args.config} shape, soft {'erosion' if sgn < 0 else 'dilation'} tau={args.tau}",
+                   "global_batch": B, "seq_len": N},
+        "roofline": {"bound": "exp", "kernel": dom, "achieved": round(elems / (dom_avg * 1e-3) / 1e12, 3),
+                     "peak": PEAK_EXP_PER_S / 1e12, "unit": "1e12 exp2/s",
+                     "frac": round(elems / (dom_avg * 1e-3) / PEAK_EXP_PER_S, 4)},
+        "kernels": kernels,
+    }), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -202,8 +266,11 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--timing-steps", type=int, default=5, help="steps re-run with per-kernel HIP events")
     ap.add_argument("--calib-copy", action="store_true", help="run one 256 MiB copy first (PMC calibration)")
-    ap.add_argument("--layer", choices=["mhsa"], default=None,
-                    help="time the attn-bench MultiHeadSelfAttention layer (fp32 in/out) instead of the bare op")
+    ap.add_argument("--layer", choices=["mhsa", "soft"], default=None,
+                    help="time the attn-bench MultiHeadSelfAttention layer (fp32 in/out), or the soft tropical "
+                         "aggregation, instead of the bare op")
+    ap.add_argument("--tau", type=float, default=0.5, help="--layer soft: temperature")
+    ap.add_argument("--erosion", action="store_true", help="--layer soft: soft min-plus instead of max-plus")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; the path is sharded over "
@@ -215,6 +282,8 @@ def main():
 
     from morphottention_amd import MorphoAttentionFunction, capi
 
+    if args.layer == "soft":
+        return bench_soft(args)
     if args.layer:
         return bench_layer(args)
     cfg = CONFIGS[args.config]
