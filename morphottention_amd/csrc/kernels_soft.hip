@@ -313,7 +313,7 @@ hipError_t launch_soft_bwd_prep(const Dims& d, const f16* grad_out, const float*
 // dk, dcb += ds^T phi_q (key side, registers) and dq = ds phi_k (query side,
 // fp32 atomics) from the summed partials.
 template <int M, int DV, bool MD>
-__global__ __launch_bounds__(256) void soft_bwd_kernel(const f16* __restrict__ qa, const f16* __restrict__ ka,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void soft_bwd_kernel(const f16* __restrict__ qa, const f16* __restrict__ ka,
                                                        const f16* __restrict__ vt, const uint8_t* __restrict__ vlo,
                                                        const float4* __restrict__ tstat, const float* __restrict__ tau_p,
                                                        const f16* __restrict__ grad_out, const float* __restrict__ zb,
@@ -330,6 +330,7 @@ __global__ __launch_bounds__(256) void soft_bwd_kernel(const f16* __restrict__ q
   __shared__ __align__(16) float sphq[C::QT * C::PS];    // phi of the step's queries
   __shared__ __align__(16) float sphk[C::KW * C::PS];    // phi of the workgroup's keys
   __shared__ __align__(16) float sds[C::CG][C::QT * C::DS];  // partial ds per column group: [query][key]
+  __shared__ __align__(16) float swv[C::KW * C::WS];         // scaled values of the workgroup's keys
   __shared__ float red[2][4];
 
   const int tid = threadIdx.x, lane = tid & 63, h32 = lane >> 5, l32 = lane & 31;
@@ -357,17 +358,17 @@ __global__ __launch_bounds__(256) void soft_bwd_kernel(const f16* __restrict__ q
   f16x4 kaug = {};
 #pragma unroll
   for (int c = 0; c < C::NCH; ++c) kf[c] = f16x8{};
-  float wv[32], dv[32];
+  float dv[32];
 #pragma unroll
-  for (int c = 0; c < 32; ++c) {
-    wv[c] = 0.f;
-    dv[c] = 0.f;
+  for (int c = 0; c < 32; ++c) dv[c] = 0.f;
+  if (kvalid) load_key_operand<M>(ka + (rowbase + key) * C::CW, h32, kf, kaug);
+  // scaled values of the workgroup's keys, [key][column] (zero past N); each
+  // lane reads its own key's row, four columns at a time
+  for (int e = tid; e < C::KW * DV; e += 256) {
+    const int r = e / DV, c = e % DV, kk = k0 + r;
+    swv[r * C::WS + c] = kk < N ? kw * load_value(vt, vlo, bh, DV, NP, c, kk) : 0.f;
   }
-  if (kvalid) {
-    load_key_operand<M>(ka + (rowbase + key) * C::CW, h32, kf, kaug);
-#pragma unroll
-    for (int c = 0; c < 32; ++c) wv[c] = kw * load_value(vt, vlo, bh, DV, NP, c0 + c, key);
-  }
+  const float* wrow = swv + (32 * kb + l32) * C::WS + c0;
   // phi of the workgroup's keys (zero past N)
   for (int e = tid; e < C::KW * M; e += 256) {
     const int r = e / M, c = e % M, kk = k0 + r;
@@ -427,15 +428,16 @@ __global__ __launch_bounds__(256) void soft_bwd_kernel(const f16* __restrict__ q
     // ---- P = 2^(y - zb); ds_ij += dO P over this wave's columns; dV_jc += dO P
 #pragma unroll
     for (int c4 = 0; c4 < 8; ++c4) {
+      const float4 w4 = *reinterpret_cast<const float4*>(wrow + 4 * c4);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int qr = acc_row(r, lane);
         const float4 n4 = *reinterpret_cast<const float4*>(snz + qr * C::WS + c0 + 4 * c4);
         const float4 g4 = *reinterpret_cast<const float4*>(sdo + qr * C::WS + c0 + 4 * c4);
-        const float p0 = fast_exp2(u[r] + wv[4 * c4 + 0] + n4.x);
-        const float p1 = fast_exp2(u[r] + wv[4 * c4 + 1] + n4.y);
-        const float p2 = fast_exp2(u[r] + wv[4 * c4 + 2] + n4.z);
-        const float p3 = fast_exp2(u[r] + wv[4 * c4 + 3] + n4.w);
+        const float p0 = fast_exp2(u[r] + w4.x + n4.x);
+        const float p1 = fast_exp2(u[r] + w4.y + n4.y);
+        const float p2 = fast_exp2(u[r] + w4.z + n4.z);
+        const float p3 = fast_exp2(u[r] + w4.w + n4.w);
         ds[r] = fmaf(p0, g4.x, ds[r]);
         ds[r] = fmaf(p1, g4.y, ds[r]);
         ds[r] = fmaf(p2, g4.z, ds[r]);
@@ -502,7 +504,7 @@ __global__ __launch_bounds__(256) void soft_bwd_kernel(const f16* __restrict__ q
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float v = h32 ? dv[16 + 8 * g + e] : dv[8 * g + e];
-        const float wc = h32 ? wv[16 + 8 * g + e] : wv[8 * g + e];
+        const float wc = wrow[16 * h32 + 8 * g + e];
         o[e] = (f16)v;
         sv = fmaf(v, wc, sv);
       }
