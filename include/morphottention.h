@@ -52,7 +52,12 @@ enum morpho_mode {
   MORPHO_MODE_CAUSAL = 1,
   MORPHO_MODE_MASK_DIAG = 2,
   MORPHO_MODE_PROJ_HARDTANH01 = 4,
-  MORPHO_MODE_PROJ_IDENTITY = 8
+  MORPHO_MODE_PROJ_IDENTITY = 8,
+  /* Soft aggregation only: always use the element-wise kernels instead of the
+   * product form on MFMA (which falls back to them by itself when it cannot
+   * guarantee its precision). No reference counterpart; for tests and
+   * measurement. */
+  MORPHO_MODE_SOFT_EXACT = 16
 };
 
 enum morpho_status {
@@ -115,8 +120,8 @@ int morpho_backward(const void* grad_out, const void* X, const void* W_phi, cons
  * lse_finalize), which the reference defines but never calls; it has no
  * launcher or op for them, so these entry points have no counterpart to
  * replace. Shapes, dtypes, `mode` bits and workspace rules are those of
- * morpho_forward / morpho_backward (the forward workspace size is
- * morpho_forward_workspace_size). `tau` points to one float32 in device
+ * morpho_forward / morpho_backward; the forward workspace size is
+ * morpho_soft_forward_workspace_size. `tau` points to one float32 in device
  * memory (> 0; read by the kernels, so it may be a learnable parameter).
  * zb [B*H, N, D/H] float32 receives log2 sum_j 2^(log2e sgn (s_ij + V_jc) /
  * tau), so out = sgn tau ln2 zb (-FLT_MAX, with out = 0, for a row without
@@ -125,6 +130,10 @@ int morpho_soft_forward(const void* X, const void* W_phi, const void* gate_q, co
                         const float* tau, void* out, float* zb, int64_t B, int64_t N, int64_t D, int64_t H,
                         int64_t cube_m, float scale, int mode, int sgn, void* workspace, size_t workspace_bytes,
                         morpho_stream_t stream);
+
+/* Bytes of device workspace morpho_soft_forward needs: the projection of
+ * morpho_forward_workspace_size plus the state of the product form. */
+size_t morpho_soft_forward_workspace_size(int64_t B, int64_t N, int64_t D, int64_t H, int64_t cube_m);
 
 /* Bytes of device workspace morpho_soft_backward needs (as
  * morpho_backward_workspace_size, plus the dtau partial sums). */

@@ -40,6 +40,8 @@ def lib() -> ctypes.CDLL:
         L.morpho_soft_forward.restype = ctypes.c_int
         L.morpho_soft_forward.argtypes = ([vp] * 5 + [vp, vp, vp] + [i64] * 5
                                           + [ctypes.c_float, ctypes.c_int, ctypes.c_int, vp, sz, vp])
+        L.morpho_soft_forward_workspace_size.restype = sz
+        L.morpho_soft_forward_workspace_size.argtypes = [i64] * 5
         L.morpho_soft_backward_workspace_size.restype = sz
         L.morpho_soft_backward_workspace_size.argtypes = [i64] * 5 + [ctypes.c_int]
         L.morpho_soft_backward.restype = ctypes.c_int
@@ -60,6 +62,10 @@ def forward_workspace_size(B: int, N: int, D: int, H: int, cube_m: int) -> int:
 
 def backward_workspace_size(B: int, N: int, D: int, H: int, cube_m: int, have_forward_workspace: bool) -> int:
     return int(lib().morpho_backward_workspace_size(B, N, D, H, cube_m, int(have_forward_workspace)))
+
+
+def soft_forward_workspace_size(B: int, N: int, D: int, H: int, cube_m: int) -> int:
+    return int(lib().morpho_soft_forward_workspace_size(B, N, D, H, cube_m))
 
 
 def soft_backward_workspace_size(B: int, N: int, D: int, H: int, cube_m: int, have_forward_workspace: bool) -> int:

@@ -314,6 +314,25 @@ namespace {
 size_t soft_part_bytes(const Dims& d) {
   return align_up((size_t)(soft_prep_blocks(d) + 2 * soft_bwd_slots(d)) * sizeof(float));
 }
+size_t soft_state_bytes(const Dims& d) {
+  const size_t bh = (size_t)d.B * d.H;
+  return 2 * align_up(bh * d.DV * 4) + align_up(bh * d.N * 4) + align_up(4);
+}
+SoftState carve_soft_state(void* base, const Dims& d) {
+  const size_t bh = (size_t)d.B * d.H;
+  char* p = static_cast<char*>(base);
+  SoftState st;
+  st.vmax = reinterpret_cast<float*>(p); p += align_up(bh * d.DV * 4);
+  st.vmin = reinterpret_cast<float*>(p); p += align_up(bh * d.DV * 4);
+  st.arow = reinterpret_cast<float*>(p); p += align_up(bh * d.N * 4);
+  st.flag = reinterpret_cast<int*>(p);
+  return st;
+}
+// The soft entry points accept MORPHO_MODE_SOFT_EXACT beside the common bits.
+int soft_mode(int mode, bool& exact) {
+  exact = (mode & MORPHO_MODE_SOFT_EXACT) != 0;
+  return mode & ~MORPHO_MODE_SOFT_EXACT;
+}
 int check_soft_args(const float* tau, int sgn) {
   if (!tau) return fail(MORPHO_ERR_INVALID_ARGUMENT, "Null tau pointer");
   if ((reinterpret_cast<uintptr_t>(tau) & 3) != 0)
@@ -322,6 +341,14 @@ int check_soft_args(const float* tau, int sgn) {
   return MORPHO_OK;
 }
 }  // namespace
+
+MORPHO_EXPORT size_t morpho_soft_forward_workspace_size(int64_t B, int64_t N, int64_t D, int64_t H, int64_t cube_m) {
+  Dims d;
+  std::string keep = g_last_error;
+  const int st = make_dims(B, N, D, H, cube_m, 1.0f, 0, d);
+  g_last_error = keep;
+  return st == MORPHO_OK ? proj_bytes(d) + soft_state_bytes(d) : 0;
+}
 
 MORPHO_EXPORT size_t morpho_soft_backward_workspace_size(int64_t B, int64_t N, int64_t D, int64_t H, int64_t cube_m,
                                                          int have_forward_workspace) {
@@ -339,22 +366,34 @@ MORPHO_EXPORT int morpho_soft_forward(const void* X, const void* W_phi, const vo
                                       void* workspace, size_t workspace_bytes, morpho_stream_t stream) {
   g_last_error.clear();
   Dims d;
-  int st = make_dims(B, N, D, H, cube_m, scale, mode, d);
+  bool exact = false;
+  int st = make_dims(B, N, D, H, cube_m, scale, soft_mode(mode, exact), d);
   if (st != MORPHO_OK) return st;
   if (!X || !W_phi || !gate_q || !gate_k || !W_V || !out || !zb) return fail(MORPHO_ERR_INVALID_ARGUMENT, "Null pointer");
   if ((st = check_soft_args(tau, sgn)) != MORPHO_OK) return st;
   if (misaligned(X) || misaligned(W_phi) || misaligned(W_V) || misaligned(out) || misaligned(zb))
     return fail(MORPHO_ERR_INVALID_ARGUMENT, "tensor pointers must be 16-byte aligned");
-  const size_t need = proj_bytes(d);
+  const size_t need = proj_bytes(d) + soft_state_bytes(d);
   if (!workspace || workspace_bytes < need)
-    return fail(MORPHO_ERR_WORKSPACE, "forward workspace needs %zu bytes (got %zu)", need, workspace_bytes);
+    return fail(MORPHO_ERR_WORKSPACE, "soft forward workspace needs %zu bytes (got %zu)", need, workspace_bytes);
   if ((reinterpret_cast<uintptr_t>(workspace) & 255) != 0)
     return fail(MORPHO_ERR_WORKSPACE, "workspace must be 256-byte aligned");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const ProjBuffers p = carve_proj(workspace, d);
+  const SoftState ss = carve_soft_state(static_cast<char*>(workspace) + proj_bytes(d), d);
   st = run_projection(d, X, W_phi, gate_q, gate_k, W_V, p, s);
   if (st != MORPHO_OK) return st;
-  MORPHO_LAUNCH("soft_fwd", launch_soft_fwd(d, p, tau, sgn, static_cast<_Float16*>(out), zb, s));
+  auto* o = static_cast<_Float16*>(out);
+  if (exact) {
+    MORPHO_LAUNCH("soft_fwd", launch_soft_fwd(d, p, tau, sgn, o, zb, nullptr, s));
+    MORPHO_LAUNCH("soft_flag", launch_set_flag(ss.flag, 1, s));  // a backward handed this workspace stays exact
+    return MORPHO_OK;
+  }
+  // product form on MFMA; the element-wise kernel runs only if some output
+  // failed its check (the flag, cleared by soft_colext)
+  MORPHO_LAUNCH("soft_colext", launch_soft_colext(d, p, ss, s));
+  MORPHO_LAUNCH("soft_fwd_fast", launch_soft_fwd_fast(d, p, tau, sgn, ss, o, zb, s));
+  MORPHO_LAUNCH("soft_fwd", launch_soft_fwd(d, p, tau, sgn, o, zb, ss.flag, s));
   return MORPHO_OK;
 }
 
@@ -366,7 +405,8 @@ MORPHO_EXPORT int morpho_soft_backward(const void* grad_out, const void* X, cons
                                        size_t workspace_bytes, morpho_stream_t stream) {
   g_last_error.clear();
   Dims d;
-  int st = make_dims(B, N, D, H, cube_m, scale, mode, d);
+  bool exact = false;
+  int st = make_dims(B, N, D, H, cube_m, scale, soft_mode(mode, exact), d);
   if (st != MORPHO_OK) return st;
   if (!grad_out || !X || !W_phi || !gate_q || !gate_k || !W_V || !zb)
     return fail(MORPHO_ERR_INVALID_ARGUMENT, "Null input pointer");
@@ -397,9 +437,19 @@ MORPHO_EXPORT int morpho_soft_backward(const void* grad_out, const void* X, cons
   const BwdBuffers g = carve_bwd(ws, d);
   float* prep_part = reinterpret_cast<float*>(ws + bwd_bytes(d));
   float* bwd_part = prep_part + soft_prep_blocks(d);
+  float* fast_part = bwd_part + 2 * soft_bwd_exact_slots(d);
   const auto* go = static_cast<const _Float16*>(grad_out);
   MORPHO_LAUNCH("soft_bwd_prep", launch_soft_bwd_prep(d, go, zb, g, prep_part, s));
-  MORPHO_LAUNCH("soft_bwd", launch_soft_bwd(d, p, go, zb, tau, sgn, g, bwd_part, s));
+  if (have_fwd && !exact) {
+    // the forward's state: the product form when its flag stayed 0, else the
+    // element-wise kernel (each writes zero partials when it does not run)
+    const SoftState ss = carve_soft_state(static_cast<char*>(const_cast<void*>(forward_workspace)) + proj_bytes(d), d);
+    MORPHO_LAUNCH("soft_bwd_fast", launch_soft_bwd_fast(d, p, go, zb, tau, sgn, ss, g, fast_part, s));
+    MORPHO_LAUNCH("soft_bwd", launch_soft_bwd(d, p, go, zb, tau, sgn, g, bwd_part, ss.flag, s));
+  } else {
+    MORPHO_LAUNCH("soft_bwd", launch_soft_bwd(d, p, go, zb, tau, sgn, g, bwd_part, nullptr, s));
+    MORPHO_LAUNCH("soft_part_clear", launch_fill_zero(fast_part, 2 * (soft_bwd_slots(d) - soft_bwd_exact_slots(d)), s));
+  }
   MORPHO_LAUNCH("proj_bwd_elem", launch_proj_bwd_elem(d, static_cast<const _Float16*>(gate_q),
                                                       static_cast<const _Float16*>(gate_k), p, g, s));
   MORPHO_LAUNCH("bwd_gemm", launch_bwd_gemm(d, p, g, static_cast<const _Float16*>(X), static_cast<_Float16*>(dX), s));

@@ -113,16 +113,35 @@ hipError_t launch_attn_bwd(const Dims& d, const ProjBuffers& p, const _Float16* 
 // kernels_soft.hip: soft tropical aggregation (out = sgn tau ln sum_j
 // exp(sgn (s + v) / tau)). `tau` is a device pointer to one float; sgn is +1
 // (dilation) or -1 (erosion); zb is the fp32 base-2 normaliser [B*H, N, DV].
+// State of the product-form fast path, kept in the soft forward workspace
+// after the projection buffers.
+struct SoftState {
+  float* vmax;  // [B*H, DV] max over keys of V
+  float* vmin;  // [B*H, DV] min over keys of V
+  float* arow;  // [B*H, N] row reference A_i (maximum of sgn log2e s_ij / tau over the row's keys)
+  int* flag;    // nonzero: some output failed the product form's check; the element-wise path ran
+};
+// Element-wise kernels; with run_flag they do nothing unless *run_flag != 0.
 hipError_t launch_soft_fwd(const Dims& d, const ProjBuffers& p, const float* tau, int sgn, _Float16* out, float* zb,
-                           hipStream_t s);
+                           const int* run_flag, hipStream_t s);
+hipError_t launch_soft_colext(const Dims& d, const ProjBuffers& p, const SoftState& st, hipStream_t s);
+hipError_t launch_soft_fwd_fast(const Dims& d, const ProjBuffers& p, const float* tau, int sgn, const SoftState& st,
+                                _Float16* out, float* zb, hipStream_t s);
 hipError_t launch_soft_bwd_prep(const Dims& d, const _Float16* grad_out, const float* zb, const BwdBuffers& g,
                                 float* part, hipStream_t s);
 hipError_t launch_soft_bwd(const Dims& d, const ProjBuffers& p, const _Float16* grad_out, const float* zb,
-                           const float* tau, int sgn, const BwdBuffers& g, float* part, hipStream_t s);
+                           const float* tau, int sgn, const BwdBuffers& g, float* part, const int* run_flag,
+                           hipStream_t s);
+hipError_t launch_soft_bwd_fast(const Dims& d, const ProjBuffers& p, const _Float16* grad_out, const float* zb,
+                                const float* tau, int sgn, const SoftState& st, const BwdBuffers& g, float* part,
+                                hipStream_t s);
+int soft_bwd_exact_slots(const Dims& d);  // the element-wise backward's share of soft_bwd_slots
+hipError_t launch_fill_zero(float* p, int n, hipStream_t s);
+hipError_t launch_set_flag(int* p, int v, hipStream_t s);
 hipError_t launch_soft_tau_reduce(const float* prep, int nprep, const float* bwd, int nbwd, const float* tau, int sgn,
                                   float* dtau, hipStream_t s);
 int soft_prep_blocks(const Dims& d);  // partial sums written by the prep (one float each)
-int soft_bwd_slots(const Dims& d);    // workgroup slots of the backward (two floats each)
+int soft_bwd_slots(const Dims& d);    // workgroup slots of both backward kernels (two floats each)
 
 // Timing hooks (capi.hip): bracket one launch with events when enabled.
 void timing_begin(const char* name, hipStream_t s);

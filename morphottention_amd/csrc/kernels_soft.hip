@@ -99,9 +99,11 @@ __global__ __launch_bounds__(256) void soft_fwd_kernel(const f16* __restrict__ q
                                                        const f16* __restrict__ vt, const uint8_t* __restrict__ vlo,
                                                        const float4* __restrict__ tstat, const float* __restrict__ tau_p,
                                                        f16* __restrict__ out, float* __restrict__ zb, int N, int NP,
-                                                       int H, int D, int BH, int causal, float sgn) {
+                                                       int H, int D, int BH, int causal, float sgn,
+                                                       const int* __restrict__ run_flag) {
   using C = SoftCfg<M, DV>;
   __shared__ __align__(16) float sw[2][32 * C::WS];
+  if (run_flag && *run_flag == 0) return;  // the product form was exact for every output
   const int tid = threadIdx.x, lane = tid & 63, h32 = lane >> 5, l32 = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nqb = (N + C::QW - 1) / C::QW;
@@ -227,21 +229,252 @@ __global__ __launch_bounds__(256) void soft_fwd_kernel(const f16* __restrict__ q
 
 template <int M, int DV>
 static hipError_t launch_soft_fwd_t(const Dims& d, const ProjBuffers& p, const float* tau, int sgn, f16* out,
-                                    float* zb, hipStream_t s) {
+                                    float* zb, const int* run_flag, hipStream_t s) {
   using C = SoftCfg<M, DV>;
   const dim3 grid(xcd_grid((d.N + C::QW - 1) / C::QW, d.B * d.H));
   if (d.mask_diag)
     hipLaunchKernelGGL((soft_fwd_kernel<M, DV, true>), grid, dim3(256), 0, s, p.qa, p.ka, p.vt, p.vlo, p.tstat, tau,
-                       out, zb, d.N, d.NP, d.H, d.D, d.B * d.H, d.causal, (float)sgn);
+                       out, zb, d.N, d.NP, d.H, d.D, d.B * d.H, d.causal, (float)sgn, run_flag);
   else
     hipLaunchKernelGGL((soft_fwd_kernel<M, DV, false>), grid, dim3(256), 0, s, p.qa, p.ka, p.vt, p.vlo, p.tstat, tau,
-                       out, zb, d.N, d.NP, d.H, d.D, d.B * d.H, d.causal, (float)sgn);
+                       out, zb, d.N, d.NP, d.H, d.D, d.B * d.H, d.causal, (float)sgn, run_flag);
   return hipGetLastError();
 }
 
 hipError_t launch_soft_fwd(const Dims& d, const ProjBuffers& p, const float* tau, int sgn, f16* out, float* zb,
-                           hipStream_t s) {
-  MORPHO_MDV_DISPATCH(launch_soft_fwd_t, d, p, tau, sgn, out, zb, s);
+                           const int* run_flag, hipStream_t s) {
+  MORPHO_MDV_DISPATCH(launch_soft_fwd_t, d, p, tau, sgn, out, zb, run_flag, s);
+}
+
+// ============================================================ product form
+// sum_j 2^(u_ij + w_jc) = 2^(A_i + B_c) sum_j E_ij F_jc with E = 2^(u - A_i) and
+// F = 2^(w - B_c), A_i the running row maximum of u and B_c the maximum of w
+// over the head's keys. The sum is then a matrix product, which runs on the
+// bf16 MFMA with hi/lo pairs (bf16 keeps fp32's exponent range, the pairs
+// carry 2^-16 relative precision). It equals the exact sum to that precision
+// while the largest term is not far below 2^(A_i + B_c): every output with
+// S_ic >= 2^-80 is exact (terms lost below fp32's normal range are then below
+// 2^-30 S_ic). A launch where some output fails the check raises a flag, and
+// the element-wise kernels recompute the whole aggregation.
+typedef __bf16 bf16;
+typedef bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ f32x16 mfma_bf16(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+// x = hi + lo to ~2^-16 relative; x is made opaque so that both halves are
+// formed from the same fp32 value
+__device__ __forceinline__ void split_bf16(float x, bf16& hi, bf16& lo) {
+  asm("" : "+v"(x));
+  hi = (bf16)x;
+  lo = (bf16)(x - (float)hi);
+}
+constexpr float kProductFloor = 0x1p-80f;
+
+// Per (head, value column): max and min of V over the head's keys (the
+// column reference B_c is kw max V for kw > 0, kw min V for kw < 0). One wave
+// per column. Block 0 also clears the fallback flag of this call.
+__global__ __launch_bounds__(256) void soft_colext_kernel(const f16* __restrict__ vt, const uint8_t* __restrict__ vlo,
+                                                          float* __restrict__ vmax, float* __restrict__ vmin,
+                                                          int* __restrict__ flag, int N, int NP, int DV, int ncol) {
+  if (blockIdx.x == 0 && threadIdx.x == 0) *flag = 0;
+  const int col = blockIdx.x * 4 + (int)(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (col >= ncol) return;
+  const int bh = col / DV, c = col - bh * DV;
+  float hi = kNegInf, lo = -kNegInf;
+  for (int k = lane; k < N; k += 64) {
+    const float v = load_value(vt, vlo, bh, DV, NP, c, k);
+    hi = fmaxf(hi, v);
+    lo = fminf(lo, v);
+  }
+#pragma unroll
+  for (int sh = 32; sh >= 1; sh >>= 1) {
+    hi = fmaxf(hi, __shfl_xor(hi, sh));
+    lo = fminf(lo, __shfl_xor(lo, sh));
+  }
+  if (lane == 0) {
+    vmax[col] = hi;
+    vmin[col] = lo;
+  }
+}
+
+hipError_t launch_soft_colext(const Dims& d, const ProjBuffers& p, const SoftState& st, hipStream_t s) {
+  const int ncol = d.B * d.H * d.DV;
+  hipLaunchKernelGGL(soft_colext_kernel, dim3((unsigned)((ncol + 3) / 4)), dim3(256), 0, s, p.vt, p.vlo, st.vmax,
+                     st.vmin, st.flag, d.N, d.NP, d.DV, ncol);
+  return hipGetLastError();
+}
+
+template <int M, int DV>
+struct FastCfg {
+  static constexpr int CW = 2 * M + 8;
+  static constexpr int NCH = M / 8;
+  static constexpr int QW = 128;   // 4 waves x 32 queries
+  static constexpr int FS = 40;    // bf16 row stride of the F^T tiles (32 keys + 8: conflict-free b128 reads)
+  static constexpr int CB = DV / 32;
+};
+
+// Forward, product form. Wave = 32 queries x all DV columns (O^T accumulators:
+// rows = value column, lane = query). Per 32-key block: the S^T block from the
+// code rows, loaded in swap23 key order so that the accumulator holds each
+// lane's keys 8 h32 + 0..7 and 16 + 8 h32 + 0..7 in order (the B-operand
+// layout of the next product); E = 2^(u - A_i) with A_i the running maximum
+// (the accumulators are rescaled when it grows); O^T += F^T E in three bf16
+// MFMAs per 16 keys (hi.hi, hi.lo, lo.hi). F^T of the block is staged by the
+// whole workgroup into double-buffered LDS tiles.
+template <int M, int DV, bool MD>
+__global__ __launch_bounds__(256) void soft_fwd_fast_kernel(const f16* __restrict__ qa, const f16* __restrict__ ka,
+                                                            const f16* __restrict__ vt,
+                                                            const uint8_t* __restrict__ vlo,
+                                                            const float4* __restrict__ tstat,
+                                                            const float* __restrict__ tau_p, SoftState st,
+                                                            f16* __restrict__ out, float* __restrict__ zb, int N,
+                                                            int NP, int H, int D, int BH, int causal, float sgn) {
+  using C = FastCfg<M, DV>;
+  __shared__ __align__(16) bf16 sfh[2][DV * C::FS];
+  __shared__ __align__(16) bf16 sfl[2][DV * C::FS];
+  __shared__ float sbc[DV];
+  const int tid = threadIdx.x, lane = tid & 63, h32 = lane >> 5, l32 = lane & 31;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nqb = (N + C::QW - 1) / C::QW;
+  int bh, blk;
+  if (!(causal ? xcd_map_lpt(nqb, BH, bh, blk) : xcd_map(nqb, BH, bh, blk))) return;
+  const int qblk = causal ? nqb - 1 - blk : blk;
+  const int q0 = qblk * C::QW, qw0 = q0 + 32 * w;
+  const int b = bh / H, h = bh - b * H;
+  const int64_t rowbase = (int64_t)bh * N;
+  const float tau = *tau_p;
+  const float ks = sgn / tau, kw = sgn * kLog2e / tau;
+  for (int c = tid; c < DV; c += 256) sbc[c] = kw * (kw > 0.f ? st.vmax[bh * DV + c] : st.vmin[bh * DV + c]);
+
+  const int q = qw0 + l32;
+  f16x8 qf[C::NCH];
+  f16x4 qaug = {};
+#pragma unroll
+  for (int c = 0; c < C::NCH; ++c) qf[c] = f16x8{};
+  if (q < N) load_query_operand<M>(qa + (rowbase + q) * C::CW, tstat[rowbase + q].x, h32, qf, qaug);
+  f32x16 o[C::CB];
+#pragma unroll
+  for (int i = 0; i < C::CB; ++i) o[i] = f32x16{};
+  float mrow = kNegInf;  // running maximum of u over this query's keys so far
+
+  const int kend = causal ? min(N, q0 + C::QW) : N;
+  const int nkb = (kend + 31) / 32;
+  auto stage = [&](int kb, bf16* fh, bf16* fl) {
+    for (int e = tid; e < 32 * DV; e += 256) {
+      const int k = e & 31, c = e >> 5, key = 32 * kb + k;
+      float f = 0.f;
+      if (key < N) f = fast_exp2(kw * load_value(vt, vlo, bh, DV, NP, c, key) - sbc[c]);
+      bf16 hi, lo;
+      split_bf16(f, hi, lo);
+      fh[c * C::FS + k] = hi;
+      fl[c * C::FS + k] = lo;
+    }
+  };
+  __syncthreads();  // sbc
+  if (nkb > 0) stage(0, sfh[0], sfl[0]);
+  __syncthreads();
+  for (int kb = 0; kb < nkb; ++kb) {
+    const bf16* fh = sfh[kb & 1];
+    const bf16* fl = sfl[kb & 1];
+    if (kb + 1 < nkb) stage(kb + 1, sfh[(kb + 1) & 1], sfl[(kb + 1) & 1]);
+    const int key0 = 32 * kb, krow = key0 + swap23(l32);
+    f16x8 kf[C::NCH];
+    f16x4 kaug = {};
+#pragma unroll
+    for (int c = 0; c < C::NCH; ++c) kf[c] = f16x8{};
+    if (krow < N) load_key_operand<M>(ka + (rowbase + krow) * C::CW, h32, kf, kaug);
+    f32x16 acc = code_dot<M, true>(kf, qf, f32x16{});
+    acc = mfma8(kaug, qaug, acc);
+    float u[16], tm = kNegInf;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int key = key0 + (r < 8 ? 8 * h32 + r : 8 + 8 * h32 + r);
+      const bool drop = (key >= N) | (causal != 0 && key > q) | (MD && key == q);
+      u[r] = drop ? kNegInf : ks * acc[r];
+      tm = fmaxf(tm, u[r]);
+    }
+    tm = fmaxf(tm, __shfl_xor(tm, 32));
+    const float mn = fmaxf(mrow, tm);
+    const float ref = mn == kNegInf ? 0.f : mn;
+    if (__builtin_amdgcn_ballot_w64(mn > mrow) != 0) {  // some query's maximum grew: rescale its sums
+      const float sc = fast_exp2(mrow - ref);
+#pragma unroll
+      for (int i = 0; i < C::CB; ++i) o[i] *= sc;
+    }
+    mrow = mn;
+    bf16x8 eh[2], el[2];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      bf16 hi, lo;
+      split_bf16(fast_exp2(u[r] - ref), hi, lo);
+      eh[r >> 3][r & 7] = hi;
+      el[r >> 3][r & 7] = lo;
+    }
+#pragma unroll
+    for (int cb = 0; cb < C::CB; ++cb) {
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc) {
+        const int off = (32 * cb + l32) * C::FS + 16 * kc + 8 * h32;
+        const bf16x8 ah = *reinterpret_cast<const bf16x8*>(fh + off);
+        const bf16x8 al = *reinterpret_cast<const bf16x8*>(fl + off);
+        o[cb] = mfma_bf16(ah, eh[kc], o[cb]);
+        o[cb] = mfma_bf16(ah, el[kc], o[cb]);
+        o[cb] = mfma_bf16(al, eh[kc], o[cb]);
+      }
+    }
+    __syncthreads();
+  }
+
+  // zb = A_i + B_c + log2 S_ic; out = sgn tau ln2 zb
+  bool low = false;
+  if (q < N) {
+    const float ko = sgn * tau * kLn2;
+    f16* orow = out + ((int64_t)b * N + q) * D + h * DV;
+    float* zrow = zb + (rowbase + q) * DV;
+#pragma unroll
+    for (int cb = 0; cb < C::CB; ++cb)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        float4 z4;
+        f16x4 o4;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int c = 32 * cb + 8 * g + 4 * h32 + e;
+          const float sv = o[cb][4 * g + e];
+          float z = -kFltMax;
+          if (mrow > kNegInf) {
+            low = low || !(sv >= kProductFloor);
+            z = mrow + sbc[c] + fast_log2(sv);
+          }
+          (&z4.x)[e] = z;
+          o4[e] = (f16)(mrow > kNegInf ? ko * z : 0.f);
+        }
+        *reinterpret_cast<float4*>(zrow + 32 * cb + 8 * g + 4 * h32) = z4;
+        *reinterpret_cast<f16x4*>(orow + 32 * cb + 8 * g + 4 * h32) = o4;
+      }
+    if (h32 == 0) st.arow[rowbase + q] = mrow;
+  }
+  if (__builtin_amdgcn_ballot_w64(low) != 0 && lane == 0) atomicOr(st.flag, 1);
+}
+
+template <int M, int DV>
+static hipError_t launch_soft_fwd_fast_t(const Dims& d, const ProjBuffers& p, const float* tau, int sgn,
+                                         const SoftState& st, f16* out, float* zb, hipStream_t s) {
+  using C = FastCfg<M, DV>;
+  const dim3 grid(xcd_grid((d.N + C::QW - 1) / C::QW, d.B * d.H));
+  if (d.mask_diag)
+    hipLaunchKernelGGL((soft_fwd_fast_kernel<M, DV, true>), grid, dim3(256), 0, s, p.qa, p.ka, p.vt, p.vlo, p.tstat,
+                       tau, st, out, zb, d.N, d.NP, d.H, d.D, d.B * d.H, d.causal, (float)sgn);
+  else
+    hipLaunchKernelGGL((soft_fwd_fast_kernel<M, DV, false>), grid, dim3(256), 0, s, p.qa, p.ka, p.vt, p.vlo, p.tstat,
+                       tau, st, out, zb, d.N, d.NP, d.H, d.D, d.B * d.H, d.causal, (float)sgn);
+  return hipGetLastError();
+}
+
+hipError_t launch_soft_fwd_fast(const Dims& d, const ProjBuffers& p, const float* tau, int sgn, const SoftState& st,
+                                f16* out, float* zb, hipStream_t s) {
+  MORPHO_MDV_DISPATCH(launch_soft_fwd_fast_t, d, p, tau, sgn, st, out, zb, s);
 }
 
 // ============================================================ backward prep
@@ -320,7 +553,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                                                        float* __restrict__ dq, float* __restrict__ dk,
                                                        float* __restrict__ dcb, f16* __restrict__ dzv,
                                                        float* __restrict__ part, int N, int NP, int H, int D, int HM,
-                                                       int BH, int causal, float sgn) {
+                                                       int BH, int causal, float sgn, const int* __restrict__ run_flag) {
   using C = SoftCfg<M, DV>;
   constexpr int NG = 256 / C::KW;   // dk phase: thread groups per key
   constexpr int CPT = M / NG;       // dk phase: codes per thread
@@ -337,7 +570,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nkb = (N + C::KW - 1) / C::KW;
   int bh, kblk;
-  if (!(causal ? xcd_map_lpt(nkb, BH, bh, kblk) : xcd_map(nkb, BH, bh, kblk))) {
+  if ((run_flag && *run_flag == 0) || !(causal ? xcd_map_lpt(nkb, BH, bh, kblk) : xcd_map(nkb, BH, bh, kblk))) {
     if (tid == 0) {
       part[2 * blockIdx.x] = 0.f;
       part[2 * blockIdx.x + 1] = 0.f;
@@ -540,26 +773,324 @@ template <int M, int DV>
 static int soft_bwd_slots_t(const Dims& d) {
   return (int)xcd_grid((d.N + SoftCfg<M, DV>::KW - 1) / SoftCfg<M, DV>::KW, d.B * d.H);
 }
-int soft_bwd_slots(const Dims& d) { return (int)xcd_grid((d.N + 32 * (128 / d.DV) - 1) / (32 * (128 / d.DV)), d.B * d.H); }
+// slots of the element-wise backward, then of the product-form backward
+// (128 keys per workgroup)
+int soft_bwd_slots(const Dims& d) {
+  return (int)xcd_grid((d.N + 32 * (128 / d.DV) - 1) / (32 * (128 / d.DV)), d.B * d.H) +
+         (int)xcd_grid((d.N + 127) / 128, d.B * d.H);
+}
 
 template <int M, int DV>
 static hipError_t launch_soft_bwd_t(const Dims& d, const ProjBuffers& p, const f16* grad_out, const float* zb,
-                                    const float* tau, int sgn, const BwdBuffers& g, float* part, hipStream_t s) {
+                                    const float* tau, int sgn, const BwdBuffers& g, float* part, const int* run_flag,
+                                    hipStream_t s) {
   const dim3 grid((unsigned)soft_bwd_slots_t<M, DV>(d));
   if (d.mask_diag)
     hipLaunchKernelGGL((soft_bwd_kernel<M, DV, true>), grid, dim3(256), 0, s, p.qa, p.ka, p.vt, p.vlo, p.tstat, tau,
                        grad_out, zb, g.dq, g.dk, g.dcb, g.dzv, part, d.N, d.NP, d.H, d.D, d.HM, d.B * d.H, d.causal,
-                       (float)sgn);
+                       (float)sgn, run_flag);
   else
     hipLaunchKernelGGL((soft_bwd_kernel<M, DV, false>), grid, dim3(256), 0, s, p.qa, p.ka, p.vt, p.vlo, p.tstat, tau,
                        grad_out, zb, g.dq, g.dk, g.dcb, g.dzv, part, d.N, d.NP, d.H, d.D, d.HM, d.B * d.H, d.causal,
-                       (float)sgn);
+                       (float)sgn, run_flag);
   return hipGetLastError();
 }
 
 hipError_t launch_soft_bwd(const Dims& d, const ProjBuffers& p, const f16* grad_out, const float* zb,
-                           const float* tau, int sgn, const BwdBuffers& g, float* part, hipStream_t s) {
-  MORPHO_MDV_DISPATCH(launch_soft_bwd_t, d, p, grad_out, zb, tau, sgn, g, part, s);
+                           const float* tau, int sgn, const BwdBuffers& g, float* part, const int* run_flag,
+                           hipStream_t s) {
+  MORPHO_MDV_DISPATCH(launch_soft_bwd_t, d, p, grad_out, zb, tau, sgn, g, part, run_flag, s);
+}
+
+// Backward, product form. With G_ic = dO_ic 2^(A_i + B_c - zb_ic) = dO_ic / S_ic:
+//     ds_ij = E_ij sum_c G_ic F_jc          (X = G F^T, then times E)
+//     dV_jc = F_jc sum_i E_ij G_ic          (dV^T = G^T E, then times F)
+// Workgroup: 4 waves x 32 keys, lane = key; per 32-query step the workgroup
+// stages G (bf16 hi/lo, [query][column]), the row references A_i and phi of the
+// queries. The S block is loaded in swap23 query order so that E is already
+// the B operand of G^T E; G^T comes from the row-major tile by transposing
+// reads. dk, dcb and dq are formed from ds as in the element-wise kernel.
+// two waves per SIMD where the registers allow it without spilling
+template <int M, int DV>
+constexpr int soft_fast_bwd_waves() { return (DV >= 128 || M * DV >= 4096) ? 1 : 2; }
+
+template <int M, int DV, bool MD>
+__global__ __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(soft_fast_bwd_waves<M, DV>(), soft_fast_bwd_waves<M, DV>()))) void soft_bwd_fast_kernel(
+    const f16* __restrict__ qa, const f16* __restrict__ ka, const f16* __restrict__ vt,
+    const uint8_t* __restrict__ vlo, const float4* __restrict__ tstat, const float* __restrict__ tau_p, SoftState st,
+    const f16* __restrict__ grad_out, const float* __restrict__ zb, float* __restrict__ dq, float* __restrict__ dk,
+    float* __restrict__ dcb, f16* __restrict__ dzv, float* __restrict__ part, int N, int NP, int H, int D, int HM,
+    int BH, int causal, float sgn) {
+  constexpr int CW = 2 * M + 8, NCH = M / 8, CB = DV / 32, KW = 128, QT = 32;
+  constexpr int GS = DV + 8;            // bf16 row stride of the G tiles
+  constexpr int PS = M + 4, DS = KW + 1;
+  constexpr int NG = 256 / KW, CPT = M / NG, CPQ = M / 8;
+  __shared__ __align__(16) bf16 sgh[QT * GS];
+  __shared__ __align__(16) bf16 sgl[QT * GS];
+  __shared__ __align__(16) float sphq[QT * PS];
+  __shared__ __align__(16) float sphk[KW * PS];
+  __shared__ __align__(16) float sds[QT * DS];
+  __shared__ float sar[QT];
+  __shared__ float sbc[DV];
+  __shared__ float red[2][4];
+
+  const int tid = threadIdx.x, lane = tid & 63, h32 = lane >> 5, l32 = lane & 31;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nkb = (N + KW - 1) / KW;
+  int bh, kblk;
+  if (*st.flag != 0 || !(causal ? xcd_map_lpt(nkb, BH, bh, kblk) : xcd_map(nkb, BH, bh, kblk))) {
+    if (tid == 0) {
+      part[2 * blockIdx.x] = 0.f;
+      part[2 * blockIdx.x + 1] = 0.f;
+    }
+    return;
+  }
+  const int k0 = kblk * KW, key = k0 + 32 * w + l32;
+  const bool kvalid = key < N;
+  const int b = bh / H, h = bh - b * H;
+  const int64_t rowbase = (int64_t)bh * N, tokbase = (int64_t)b * N;
+  const float tau = *tau_p;
+  const float ks = sgn / tau, kw = sgn * kLog2e / tau;
+  for (int c = tid; c < DV; c += 256) sbc[c] = kw * (kw > 0.f ? st.vmax[bh * DV + c] : st.vmin[bh * DV + c]);
+  // phi of the workgroup's keys (zero past N)
+  for (int e = tid; e < KW * M; e += 256) {
+    const int r = e / M, c = e % M, kk = k0 + r;
+    float v = 0.f;
+    if (kk < N) {
+      const f16* row = qa + (rowbase + kk) * CW;
+      v = (float)row[c] + (float)row[M + 8 + c];
+    }
+    sphk[r * PS + c] = v;
+  }
+  __syncthreads();  // sbc
+
+  // key operand; F of this lane's key as the B operand of G F^T: chunk cc
+  // holds columns 16 cc + 8 h32 + 0..7
+  f16x8 kf[NCH];
+  f16x4 kaug = {};
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) kf[c] = f16x8{};
+  bf16x8 fh[DV / 16], fl[DV / 16];
+#pragma unroll
+  for (int cc = 0; cc < DV / 16; ++cc)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int c = 16 * cc + 8 * h32 + j;
+      const float f = kvalid ? fast_exp2(kw * load_value(vt, vlo, bh, DV, NP, c, key) - sbc[c]) : 0.f;
+      bf16 hi, lo;
+      split_bf16(f, hi, lo);
+      fh[cc][j] = hi;
+      fl[cc][j] = lo;
+    }
+  if (kvalid) load_key_operand<M>(ka + (rowbase + key) * CW, h32, kf, kaug);
+  f32x16 dva[CB];
+#pragma unroll
+  for (int i = 0; i < CB; ++i) dva[i] = f32x16{};
+  float dka[CPT], dcba = 0.f, sacc = 0.f;
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) dka[i] = 0.f;
+
+  const int qstart = causal ? k0 : 0;
+  for (int qs = qstart; qs < N; qs += QT) {
+    // ---- stage G (hi/lo), A and phi of queries qs .. qs + QT - 1 (zero past N and for rows without keys)
+    for (int e = tid; e < QT * DV; e += 256) {
+      const int r = e / DV, c = e % DV, qq = qs + r;
+      float g = 0.f;
+      if (qq < N) {
+        const float a = st.arow[rowbase + qq];
+        if (a > kNegInf)
+          g = (float)grad_out[(tokbase + qq) * D + h * DV + c] * fast_exp2(a + sbc[c] - zb[(rowbase + qq) * DV + c]);
+      }
+      bf16 hi, lo;
+      split_bf16(g, hi, lo);
+      sgh[r * GS + c] = hi;
+      sgl[r * GS + c] = lo;
+    }
+    for (int e = tid; e < QT * M; e += 256) {
+      const int r = e / M, c = e % M, qq = qs + r;
+      float v = 0.f;
+      if (qq < N) {
+        const f16* row = qa + (rowbase + qq) * CW;
+        v = (float)row[c] + (float)row[M + 8 + c];
+      }
+      sphq[r * PS + c] = v;
+    }
+    if (tid < QT) {
+      const float a = qs + tid < N ? st.arow[rowbase + qs + tid] : kNegInf;
+      sar[tid] = a > kNegInf ? a : 0.f;  // rows without keys: every score is masked
+    }
+    // ---- S block, query rows in swap23 order: register r holds query p(r)
+    const int qrow = qs + swap23(l32);
+    f16x8 qf[NCH];
+    f16x4 qaug = {};
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) qf[c] = f16x8{};
+    if (qrow < N) load_query_operand<M>(qa + (rowbase + qrow) * CW, tstat[rowbase + qrow].x, h32, qf, qaug);
+    f32x16 acc = code_dot<M, false>(kf, qf, f32x16{});
+    acc = mfma8(qaug, kaug, acc);
+    __syncthreads();  // staging complete
+    // ---- E = 2^(u - A_i) (bf16 hi/lo, the B operand of G^T E)
+    bf16x8 eh[2], el[2];
+    float e32[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int p = r < 8 ? 8 * h32 + r : 8 + 8 * h32 + r;
+      const int qq = qs + p;
+      const bool drop = (qq >= N) | !kvalid | (causal != 0 && key > qq) | (MD && key == qq);
+      const float e = drop ? 0.f : fast_exp2(ks * acc[r] - sar[p]);
+      e32[r] = e;
+      bf16 hi, lo;
+      split_bf16(e, hi, lo);
+      eh[r >> 3][r & 7] = hi;
+      el[r >> 3][r & 7] = lo;
+    }
+    // ---- X = G F^T (rows = queries in the S block's order, lane = key)
+    f32x16 x = {};
+    const int grow = swap23(l32) * GS;
+#pragma unroll
+    for (int cc = 0; cc < DV / 16; ++cc) {
+      const bf16x8 ah = *reinterpret_cast<const bf16x8*>(sgh + grow + 16 * cc + 8 * h32);
+      const bf16x8 al = *reinterpret_cast<const bf16x8*>(sgl + grow + 16 * cc + 8 * h32);
+      x = mfma_bf16(ah, fh[cc], x);
+      x = mfma_bf16(ah, fl[cc], x);
+      x = mfma_bf16(al, fh[cc], x);
+    }
+    // ---- dV^T += G^T E (rows = value columns, lane = key)
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc) {
+        const bf16x8 ah = __builtin_bit_cast(bf16x8, frag_kmajor(reinterpret_cast<const f16*>(sgh), GS, 16 * kc, 32 * cb, lane));
+        const bf16x8 al = __builtin_bit_cast(bf16x8, frag_kmajor(reinterpret_cast<const f16*>(sgl), GS, 16 * kc, 32 * cb, lane));
+        dva[cb] = mfma_bf16(ah, eh[kc], dva[cb]);
+        dva[cb] = mfma_bf16(ah, el[kc], dva[cb]);
+        dva[cb] = mfma_bf16(al, eh[kc], dva[cb]);
+      }
+    // ---- ds = E X; sum ds * acc for dtau; the ds tile
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int p = r < 8 ? 8 * h32 + r : 8 + 8 * h32 + r;
+      const float dsv = e32[r] * x[r];
+      sacc = fmaf(dsv, acc[r], sacc);
+      sds[p * DS + 32 * w + l32] = dsv;
+    }
+    __syncthreads();  // the ds tile is complete
+    {  // key side: dk_j += sum_i ds_ij phi_i, dcb_j += sum_i ds_ij
+      const int kk = tid % KW, grp = tid / KW;
+#pragma unroll 4
+      for (int i = 0; i < QT; ++i) {
+        const float dsv = sds[i * DS + kk];
+        const float* ph = sphq + i * PS + grp * CPT;
+#pragma unroll
+        for (int c = 0; c < CPT; ++c) dka[c] = fmaf(dsv, ph[c], dka[c]);
+        dcba += dsv;
+      }
+    }
+    {  // query side: dq_i += sum_j ds_ij phi_j (fp32 atomics)
+      const int i = tid % QT, grp = tid / QT;
+      float dqa[CPQ];
+#pragma unroll
+      for (int c = 0; c < CPQ; ++c) dqa[c] = 0.f;
+#pragma unroll 4
+      for (int kk = 0; kk < KW; ++kk) {
+        const float dsv = sds[i * DS + kk];
+        const float* ph = sphk + kk * PS + grp * CPQ;
+#pragma unroll
+        for (int c = 0; c < CPQ; ++c) dqa[c] = fmaf(dsv, ph[c], dqa[c]);
+      }
+      if (qs + i < N) {
+#pragma unroll
+        for (int c = 0; c < CPQ; ++c) unsafeAtomicAdd(dq + (rowbase + qs + i) * M + grp * CPQ + c, dqa[c]);
+      }
+    }
+    __syncthreads();  // LDS tiles are free for the next step
+  }
+
+  // ---- epilogue: dV_jc = F_jc (G^T E)_cj; sum dV * w for dtau
+  float sv = 0.f;
+  if (kvalid) {
+    f16* drow = dzv + (tokbase + key) * (int64_t)(HM + D) + HM + h * DV;
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        f16x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int c = 32 * cb + 8 * g + 4 * h32 + e;
+          const float wv = kw * load_value(vt, vlo, bh, DV, NP, c, key);
+          const float v = fast_exp2(wv - sbc[c]) * dva[cb][4 * g + e];
+          o[e] = (f16)v;
+          sv = fmaf(v, wv, sv);
+        }
+        *reinterpret_cast<f16x4*>(drow + 32 * cb + 8 * g + 4 * h32) = o;
+      }
+  }
+  {
+    const int kk = tid % KW, grp = tid / KW;
+    if (k0 + kk < N) {
+#pragma unroll
+      for (int c = 0; c < CPT; ++c) dk[(rowbase + k0 + kk) * M + grp * CPT + c] = dka[c];
+      if (grp == 0) dcb[rowbase + k0 + kk] += dcba;  // the prep wrote the row sum
+    }
+  }
+#pragma unroll
+  for (int sh = 32; sh >= 1; sh >>= 1) {
+    sacc += __shfl_xor(sacc, sh);
+    sv += __shfl_xor(sv, sh);
+  }
+  if (lane == 0) {
+    red[0][w] = sacc;
+    red[1][w] = sv;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    part[2 * blockIdx.x] = (red[0][0] + red[0][1]) + (red[0][2] + red[0][3]);
+    part[2 * blockIdx.x + 1] = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
+  }
+}
+
+template <int M, int DV>
+static hipError_t launch_soft_bwd_fast_t(const Dims& d, const ProjBuffers& p, const f16* grad_out, const float* zb,
+                                         const float* tau, int sgn, const SoftState& st, const BwdBuffers& g,
+                                         float* part, hipStream_t s) {
+  const dim3 grid(xcd_grid((d.N + 127) / 128, d.B * d.H));
+  if (d.mask_diag)
+    hipLaunchKernelGGL((soft_bwd_fast_kernel<M, DV, true>), grid, dim3(256), 0, s, p.qa, p.ka, p.vt, p.vlo, p.tstat,
+                       tau, st, grad_out, zb, g.dq, g.dk, g.dcb, g.dzv, part, d.N, d.NP, d.H, d.D, d.HM, d.B * d.H,
+                       d.causal, (float)sgn);
+  else
+    hipLaunchKernelGGL((soft_bwd_fast_kernel<M, DV, false>), grid, dim3(256), 0, s, p.qa, p.ka, p.vt, p.vlo, p.tstat,
+                       tau, st, grad_out, zb, g.dq, g.dk, g.dcb, g.dzv, part, d.N, d.NP, d.H, d.D, d.HM, d.B * d.H,
+                       d.causal, (float)sgn);
+  return hipGetLastError();
+}
+
+hipError_t launch_soft_bwd_fast(const Dims& d, const ProjBuffers& p, const f16* grad_out, const float* zb,
+                                const float* tau, int sgn, const SoftState& st, const BwdBuffers& g, float* part,
+                                hipStream_t s) {
+  MORPHO_MDV_DISPATCH(launch_soft_bwd_fast_t, d, p, grad_out, zb, tau, sgn, st, g, part, s);
+}
+int soft_bwd_exact_slots(const Dims& d) {
+  return (int)xcd_grid((d.N + 32 * (128 / d.DV) - 1) / (32 * (128 / d.DV)), d.B * d.H);
+}
+
+// Small fills (vector stores from a kernel, so that the sequence stays free of
+// memset nodes when a caller captures it in a graph).
+__global__ void fill_kernel(float* __restrict__ p, int n, float v) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+hipError_t launch_fill_zero(float* p, int n, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(fill_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p, n, 0.f);
+  return hipGetLastError();
+}
+__global__ void flag_kernel(int* __restrict__ p, int v) { *p = v; }
+hipError_t launch_set_flag(int* p, int v, hipStream_t s) {
+  hipLaunchKernelGGL(flag_kernel, dim3(1), dim3(1), 0, s, p, v);
+  return hipGetLastError();
 }
 
 // ============================================================ dtau

@@ -160,6 +160,11 @@ void check_tau(const at::Tensor& tau, const at::Tensor& X) {
               "tau must be one contiguous float32 element");
 }
 
+// The soft ops also accept MORPHO_MODE_SOFT_EXACT (16) in `variant`.
+int soft_mode_of(bool causal, int64_t variant) {
+  return mode_of(causal, variant & ~(int64_t)MORPHO_MODE_SOFT_EXACT) | (int)(variant & MORPHO_MODE_SOFT_EXACT);
+}
+
 int sgn_of(int64_t sgn) {
   TORCH_CHECK(sgn == 1 || sgn == -1, "sgn must be +1 (dilation) or -1 (erosion), got ", sgn);
   return (int)sgn;
@@ -169,14 +174,14 @@ std::vector<at::Tensor> op_soft_forward(const at::Tensor& X, const at::Tensor& W
                                         const at::Tensor& gate_k, const at::Tensor& W_V, const at::Tensor& tau,
                                         int64_t H, int64_t cube_m, double scale, bool causal, int64_t sgn,
                                         int64_t variant) {
-  const int mode = mode_of(causal, variant);
+  const int mode = soft_mode_of(causal, variant);
   const int sg = sgn_of(sgn);
   const Shape s = check_inputs(X, W_phi, gate_q, gate_k, W_V, H, cube_m);
   check_tau(tau, X);
   const c10::hip::HIPGuardMasqueradingAsCUDA guard(X.device());
   auto out = at::empty_like(X);
   auto zb = at::empty({s.B * H, s.N, s.D / H}, X.options().dtype(at::kFloat));
-  const size_t ws_bytes = morpho_forward_workspace_size(s.B, s.N, s.D, s.H, s.M);
+  const size_t ws_bytes = morpho_soft_forward_workspace_size(s.B, s.N, s.D, s.H, s.M);
   TORCH_CHECK(ws_bytes > 0, "morphottention soft_forward: unsupported sizes (cube_m must be 16, 32 or 64; "
               "D / H must be 32, 64 or 128)");
   auto ws = at::empty({(int64_t)ws_bytes}, X.options().dtype(at::kByte));
@@ -192,7 +197,7 @@ std::vector<at::Tensor> op_soft_backward(const at::Tensor& grad_out, const at::T
                                          const at::Tensor& tau, const at::Tensor& zb, const at::Tensor& workspace,
                                          int64_t H, int64_t cube_m, double scale, bool causal, int64_t sgn,
                                          int64_t variant) {
-  const int mode = mode_of(causal, variant);
+  const int mode = soft_mode_of(causal, variant);
   const int sg = sgn_of(sgn);
   check(grad_out, "grad_out");
   const Shape s = check_inputs(X, W_phi, gate_q, gate_k, W_V, H, cube_m);
@@ -201,7 +206,7 @@ std::vector<at::Tensor> op_soft_backward(const at::Tensor& grad_out, const at::T
   TORCH_CHECK(zb.is_cuda() && zb.scalar_type() == at::kFloat && zb.is_contiguous() && zb.dim() == 3 &&
                   zb.size(0) == s.B * H && zb.size(1) == s.N && zb.size(2) == s.D / H,
               "zb must be the float32 [B*H, N, D/H] tensor of soft_forward");
-  const size_t need = morpho_forward_workspace_size(s.B, s.N, s.D, s.H, s.M);
+  const size_t need = morpho_soft_forward_workspace_size(s.B, s.N, s.D, s.H, s.M);
   TORCH_CHECK(workspace.is_cuda() && workspace.scalar_type() == at::kByte && workspace.is_contiguous() &&
                   (size_t)workspace.numel() >= need,
               "workspace must be the uint8 CUDA tensor returned by soft_forward for these sizes");

@@ -29,7 +29,7 @@ from .autograd import variant_bits
 @torch.library.register_fake(add_op_namespace_prefix("soft_forward"))
 def _soft_forward_fake(X, W_phi, gate_q, gate_k, W_V, tau, H, cube_m, scale, causal, sgn, variant=0):
     B, N, D = X.shape
-    ws = X.new_empty((capi.forward_workspace_size(B, N, D, H, cube_m),), dtype=torch.uint8)
+    ws = X.new_empty((capi.soft_forward_workspace_size(B, N, D, H, cube_m),), dtype=torch.uint8)
     return [torch.empty_like(X), X.new_empty((B * H, N, D // H), dtype=torch.float32), ws]
 
 

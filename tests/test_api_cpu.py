@@ -211,8 +211,10 @@ def test_soft_entry_points_validate_without_the_device():
     assert st == 1 and b"sgn" in L.morpho_last_error()
     st = L.morpho_soft_forward(vp, vp, vp, vp, vp, None, vp, vp, 2, 8, 64, 2, 16, 1.0, 0, 1, vp, ws, None)
     assert st == 1 and b"tau" in L.morpho_last_error()
-    st = L.morpho_soft_forward(vp, vp, vp, vp, vp, vp, vp, vp, 2, 8, 64, 2, 16, 1.0, 16, 1, vp, ws, None)
-    assert st == 1 and b"invalid mode bits" in L.morpho_last_error()
+    st = L.morpho_soft_forward(vp, vp, vp, vp, vp, vp, vp, vp, 2, 8, 64, 2, 16, 1.0, 32, 1, vp, ws, None)
+    assert st == 1 and b"invalid mode bits" in L.morpho_last_error()  # 16 (SOFT_EXACT) is valid here, 32 is not
+    st = L.morpho_soft_forward(vp, vp, vp, vp, vp, vp, vp, vp, 2, 8, 64, 2, 16, 1.0, 16, 1, vp, 64, None)
+    assert st == 3 and b"soft forward workspace" in L.morpho_last_error()
     st = L.morpho_soft_backward(*([vp] * 14), 2, 8, 64, 2, 16, 1.0, 0, -3, None, vp, ws, None)
     assert st == 1 and b"sgn" in L.morpho_last_error()
     need_fwd = capi.soft_backward_workspace_size(2, 8, 64, 2, 16, True)

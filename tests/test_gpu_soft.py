@@ -178,3 +178,49 @@ def test_soft_module_trains_tau():
     out.float().square().mean().backward()
     assert mod.tau.grad is not None and torch.isfinite(mod.tau.grad).all()
     assert torch.equal(out.detach(), mod(x).detach())
+
+
+def _flag(ws, B, N, D, H, m):
+    """The product form's fallback flag in a soft forward workspace: after the
+    projection buffers come V's column max and min [B*H, dv] and the row
+    references [B*H, N] fp32, each region 256-byte aligned, then the flag."""
+    from morphottention_amd import capi
+    up = lambda n: (n + 255) // 256 * 256  # noqa: E731
+    off = capi.forward_workspace_size(B, N, D, H, m) + 2 * up(B * H * (D // H) * 4) + up(B * H * N * 4)
+    return int(ws[off:off + 4].cpu().view(torch.int32).item())
+
+
+@pytest.mark.parametrize("tau,sgn,causal", [(0.5, 1, True), (0.5, -1, False), (4.0, 1, False), (0.25, -1, True)])
+def test_product_form_matches_elementwise_kernels(tau, sgn, causal):
+    """Where the product form is exact (its flag stays 0) it gives the
+    element-wise kernels' output to within the fp16 rounding of out and the
+    normaliser to 2^-16 relative in output units."""
+    B, N, H, m, dv = 2, 200, 2, 16, 64
+    x, params, _ = _inputs(B, N, H, m, dv, seed=1000)
+    t = torch.tensor([tau], dtype=torch.float32, device="cuda")
+    fast = torch.ops.morphottention.soft_forward(x, *params, t, H, m, 0.8, causal, sgn, 0)
+    exact = torch.ops.morphottention.soft_forward(x, *params, t, H, m, 0.8, causal, sgn, 16)
+    torch.cuda.synchronize()
+    flag = _flag(fast[2], B, N, H * dv, H, m)
+    dz = (tau * math.log(2.0) * (fast[1] - exact[1]).abs()).max().item()
+    do = ((fast[0].float() - exact[0].float()).abs() - 2 * _half_ulp(exact[0].float())).max().item()
+    _say(f"[soft] product form tau={tau} sgn={sgn:+d} causal={causal}: flag {flag} zb diff (output units) {dz:.2e} "
+         f"out diff beyond one ulp {do:.2e}")
+    assert flag == 0
+    assert dz <= 2.0 ** -16 * (1.0 + exact[0].float().abs().max().item())
+    assert do <= 0.0
+
+
+def test_product_form_falls_back_for_small_tau():
+    """tau = 0.02 spreads the exponents beyond the product form's range: the
+    flag is raised and the element-wise kernels' result is returned as is."""
+    B, N, H, m, dv = 1, 300, 2, 16, 64
+    x, params, _ = _inputs(B, N, H, m, dv, seed=1001, x_mult=2.0)
+    t = torch.tensor([0.02], dtype=torch.float32, device="cuda")
+    fast = torch.ops.morphottention.soft_forward(x, *params, t, H, m, 1.0, True, 1, 0)
+    exact = torch.ops.morphottention.soft_forward(x, *params, t, H, m, 1.0, True, 1, 16)
+    torch.cuda.synchronize()
+    flag = _flag(fast[2], B, N, H * dv, H, m)
+    _say(f"[soft] small tau: flag {flag}")
+    assert flag == 1
+    assert torch.equal(fast[0], exact[0]) and torch.equal(fast[1], exact[1])
