@@ -802,18 +802,23 @@ hipError_t launch_soft_bwd(const Dims& d, const ProjBuffers& p, const f16* grad_
   MORPHO_MDV_DISPATCH(launch_soft_bwd_t, d, p, grad_out, zb, tau, sgn, g, part, run_flag, s);
 }
 
+// two waves per SIMD where the registers allow it without spilling
+template <int M, int DV>
+constexpr int soft_fast_bwd_waves() { return (M == 16 && DV <= 64) ? 2 : 1; }
+
 // Backward, product form. With G_ic = dO_ic 2^(A_i + B_c - zb_ic) = dO_ic / S_ic:
 //     ds_ij = E_ij sum_c G_ic F_jc          (X = G F^T, then times E)
 //     dV_jc = F_jc sum_i E_ij G_ic          (dV^T = G^T E, then times F)
 // Workgroup: 4 waves x 32 keys, lane = key; per 32-query step the workgroup
-// stages G (bf16 hi/lo, [query][column]), the row references A_i and phi of the
-// queries. The S block is loaded in swap23 query order so that E is already
-// the B operand of G^T E; G^T comes from the row-major tile by transposing
-// reads. dk, dcb and dq are formed from ds as in the element-wise kernel.
-// two waves per SIMD where the registers allow it without spilling
-template <int M, int DV>
-constexpr int soft_fast_bwd_waves() { return (DV >= 128 || M * DV >= 4096) ? 1 : 2; }
-
+// stages G (bf16 hi/lo, [query][column]), the row references A_i and phi of
+// the queries (fp16 hi/lo, [query][code], with a column of ones at code M).
+// The S block is loaded in swap23 query order so that E and ds are already
+// B operands of the products that contract over the queries: dV^T += G^T E,
+// and [dk | dcb]^T += [phi | 1]^T ds (three fp16 MFMAs of hi/lo pairs; the
+// ones column gives dcb). dq_i = sum_j ds_ij phi_j contracts over the keys:
+// each wave reads its ds block back from LDS as the A operand against phi of
+// its keys (registers), and the four waves' partials are summed in LDS before
+// one fp32 atomic per (query, code).
 template <int M, int DV, bool MD>
 __global__ __launch_bounds__(256)
 __attribute__((amdgpu_waves_per_eu(soft_fast_bwd_waves<M, DV>(), soft_fast_bwd_waves<M, DV>()))) void soft_bwd_fast_kernel(
@@ -824,13 +829,16 @@ __attribute__((amdgpu_waves_per_eu(soft_fast_bwd_waves<M, DV>(), soft_fast_bwd_w
     int BH, int causal, float sgn) {
   constexpr int CW = 2 * M + 8, NCH = M / 8, CB = DV / 32, KW = 128, QT = 32;
   constexpr int GS = DV + 8;            // bf16 row stride of the G tiles
-  constexpr int PS = M + 4, DS = KW + 1;
-  constexpr int NG = 256 / KW, CPT = M / NG, CPQ = M / 8;
+  constexpr int MB = (M + 32) / 32;     // 32-code blocks of [phi | 1]
+  constexpr int PT = 32 * MB + 8;       // fp16 row stride of the [phi | 1] tiles
+  constexpr int NB = (M + 31) / 32;     // 32-code blocks of dq
+  constexpr int DS = KW + 4;            // fp32 row stride of the ds tile
   __shared__ __align__(16) bf16 sgh[QT * GS];
   __shared__ __align__(16) bf16 sgl[QT * GS];
-  __shared__ __align__(16) float sphq[QT * PS];
-  __shared__ __align__(16) float sphk[KW * PS];
+  __shared__ __align__(16) f16 sph[QT * PT];
+  __shared__ __align__(16) f16 spl[QT * PT];
   __shared__ __align__(16) float sds[QT * DS];
+  __shared__ __align__(16) float sdq[4][QT * 32 * NB];
   __shared__ float sar[QT];
   __shared__ float sbc[DV];
   __shared__ float red[2][4];
@@ -846,27 +854,18 @@ __attribute__((amdgpu_waves_per_eu(soft_fast_bwd_waves<M, DV>(), soft_fast_bwd_w
     }
     return;
   }
-  const int k0 = kblk * KW, key = k0 + 32 * w + l32;
+  const int k0 = kblk * KW, kw0 = k0 + 32 * w, key = kw0 + l32;
   const bool kvalid = key < N;
   const int b = bh / H, h = bh - b * H;
   const int64_t rowbase = (int64_t)bh * N, tokbase = (int64_t)b * N;
   const float tau = *tau_p;
   const float ks = sgn / tau, kw = sgn * kLog2e / tau;
   for (int c = tid; c < DV; c += 256) sbc[c] = kw * (kw > 0.f ? st.vmax[bh * DV + c] : st.vmin[bh * DV + c]);
-  // phi of the workgroup's keys (zero past N)
-  for (int e = tid; e < KW * M; e += 256) {
-    const int r = e / M, c = e % M, kk = k0 + r;
-    float v = 0.f;
-    if (kk < N) {
-      const f16* row = qa + (rowbase + kk) * CW;
-      v = (float)row[c] + (float)row[M + 8 + c];
-    }
-    sphk[r * PS + c] = v;
-  }
   __syncthreads();  // sbc
 
-  // key operand; F of this lane's key as the B operand of G F^T: chunk cc
-  // holds columns 16 cc + 8 h32 + 0..7
+  // key operand; F of this lane's key as the B operand of G F^T (chunk cc:
+  // columns 16 cc + 8 h32 + 0..7); phi of the wave's keys as the B operand of
+  // ds phi (chunk kc: keys 16 kc + 8 h32 + 0..7, code 32 nb + l32)
   f16x8 kf[NCH];
   f16x4 kaug = {};
 #pragma unroll
@@ -883,17 +882,34 @@ __attribute__((amdgpu_waves_per_eu(soft_fast_bwd_waves<M, DV>(), soft_fast_bwd_w
       fh[cc][j] = hi;
       fl[cc][j] = lo;
     }
+  f16x8 pkh[NB][2], pkl[NB][2];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int kk = kw0 + 16 * kc + 8 * h32 + j, code = 32 * nb + l32;
+        f16 hi = (f16)0.f, lo = (f16)0.f;
+        if (kk < N && code < M) {
+          hi = qa[(rowbase + kk) * CW + code];
+          lo = qa[(rowbase + kk) * CW + M + 8 + code];
+        }
+        pkh[nb][kc][j] = hi;
+        pkl[nb][kc][j] = lo;
+      }
   if (kvalid) load_key_operand<M>(ka + (rowbase + key) * CW, h32, kf, kaug);
-  f32x16 dva[CB];
+  f32x16 dva[CB], dka[MB];
 #pragma unroll
   for (int i = 0; i < CB; ++i) dva[i] = f32x16{};
-  float dka[CPT], dcba = 0.f, sacc = 0.f;
 #pragma unroll
-  for (int i = 0; i < CPT; ++i) dka[i] = 0.f;
+  for (int i = 0; i < MB; ++i) dka[i] = f32x16{};
+  float sacc = 0.f;
 
   const int qstart = causal ? k0 : 0;
   for (int qs = qstart; qs < N; qs += QT) {
-    // ---- stage G (hi/lo), A and phi of queries qs .. qs + QT - 1 (zero past N and for rows without keys)
+    // ---- stage G (hi/lo), A and [phi | 1] of queries qs .. qs + QT - 1 (zero
+    // past N and for rows without keys)
     for (int e = tid; e < QT * DV; e += 256) {
       const int r = e / DV, c = e % DV, qq = qs + r;
       float g = 0.f;
@@ -907,14 +923,19 @@ __attribute__((amdgpu_waves_per_eu(soft_fast_bwd_waves<M, DV>(), soft_fast_bwd_w
       sgh[r * GS + c] = hi;
       sgl[r * GS + c] = lo;
     }
-    for (int e = tid; e < QT * M; e += 256) {
-      const int r = e / M, c = e % M, qq = qs + r;
-      float v = 0.f;
+    for (int e = tid; e < QT * 32 * MB; e += 256) {
+      const int r = e / (32 * MB), c = e % (32 * MB), qq = qs + r;
+      f16 hi = (f16)0.f, lo = (f16)0.f;
       if (qq < N) {
-        const f16* row = qa + (rowbase + qq) * CW;
-        v = (float)row[c] + (float)row[M + 8 + c];
+        if (c < M) {
+          hi = qa[(rowbase + qq) * CW + c];
+          lo = qa[(rowbase + qq) * CW + M + 8 + c];
+        } else if (c == M) {
+          hi = (f16)1.f;
+        }
       }
-      sphq[r * PS + c] = v;
+      sph[r * PT + c] = hi;
+      spl[r * PT + c] = lo;
     }
     if (tid < QT) {
       const float a = qs + tid < N ? st.arow[rowbase + qs + tid] : kNegInf;
@@ -967,47 +988,68 @@ __attribute__((amdgpu_waves_per_eu(soft_fast_bwd_waves<M, DV>(), soft_fast_bwd_w
         dva[cb] = mfma_bf16(ah, el[kc], dva[cb]);
         dva[cb] = mfma_bf16(al, eh[kc], dva[cb]);
       }
-    // ---- ds = E X; sum ds * acc for dtau; the ds tile
+    // ---- ds = E X (fp16 hi/lo, the B operand of [phi | 1]^T ds); the ds tile for dq
+    f16x8 dsh[2], dsl[2];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int p = r < 8 ? 8 * h32 + r : 8 + 8 * h32 + r;
       const float dsv = e32[r] * x[r];
       sacc = fmaf(dsv, acc[r], sacc);
       sds[p * DS + 32 * w + l32] = dsv;
+      f16 hi, lo;
+      split_hi_lo(dsv, hi, lo);
+      dsh[r >> 3][r & 7] = hi;
+      dsl[r >> 3][r & 7] = lo;
     }
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc) {
+        const f16x8 ah = frag_kmajor(sph, PT, 16 * kc, 32 * mb, lane);
+        const f16x8 al = frag_kmajor(spl, PT, 16 * kc, 32 * mb, lane);
+        dka[mb] = mfma16(ah, dsh[kc], dka[mb]);
+        dka[mb] = mfma16(ah, dsl[kc], dka[mb]);
+        dka[mb] = mfma16(al, dsh[kc], dka[mb]);
+      }
     __syncthreads();  // the ds tile is complete
-    {  // key side: dk_j += sum_i ds_ij phi_i, dcb_j += sum_i ds_ij
-      const int kk = tid % KW, grp = tid / KW;
-#pragma unroll 4
-      for (int i = 0; i < QT; ++i) {
-        const float dsv = sds[i * DS + kk];
-        const float* ph = sphq + i * PS + grp * CPT;
+    // ---- dq partial of this wave's keys: ds (rows = queries, k = keys) phi_k
 #pragma unroll
-        for (int c = 0; c < CPT; ++c) dka[c] = fmaf(dsv, ph[c], dka[c]);
-        dcba += dsv;
+    for (int nb = 0; nb < NB; ++nb) {
+      f32x16 dqa = {};
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc) {
+        const float* src = sds + l32 * DS + 32 * w + 16 * kc + 8 * h32;
+        const float4 v0 = *reinterpret_cast<const float4*>(src);
+        const float4 v1 = *reinterpret_cast<const float4*>(src + 4);
+        const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+        f16x8 ah, al;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          f16 hi, lo;
+          split_hi_lo(vv[j], hi, lo);
+          ah[j] = hi;
+          al[j] = lo;
+        }
+        dqa = mfma16(ah, pkh[nb][kc], dqa);
+        dqa = mfma16(ah, pkl[nb][kc], dqa);
+        dqa = mfma16(al, pkh[nb][kc], dqa);
       }
+      // rows = queries, lane = code 32 nb + l32
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sdq[w][acc_row(r, lane) * 32 * NB + 32 * nb + l32] = dqa[r];
     }
-    {  // query side: dq_i += sum_j ds_ij phi_j (fp32 atomics)
-      const int i = tid % QT, grp = tid / QT;
-      float dqa[CPQ];
-#pragma unroll
-      for (int c = 0; c < CPQ; ++c) dqa[c] = 0.f;
-#pragma unroll 4
-      for (int kk = 0; kk < KW; ++kk) {
-        const float dsv = sds[i * DS + kk];
-        const float* ph = sphk + kk * PS + grp * CPQ;
-#pragma unroll
-        for (int c = 0; c < CPQ; ++c) dqa[c] = fmaf(dsv, ph[c], dqa[c]);
-      }
-      if (qs + i < N) {
-#pragma unroll
-        for (int c = 0; c < CPQ; ++c) unsafeAtomicAdd(dq + (rowbase + qs + i) * M + grp * CPQ + c, dqa[c]);
+    __syncthreads();  // the four partial dq tiles are complete
+    for (int e = tid; e < QT * M; e += 256) {
+      const int r = e / M, c = e % M;
+      if (qs + r < N) {
+        const int o = r * 32 * NB + c;
+        unsafeAtomicAdd(dq + (rowbase + qs + r) * M + c, (sdq[0][o] + sdq[1][o]) + (sdq[2][o] + sdq[3][o]));
       }
     }
     __syncthreads();  // LDS tiles are free for the next step
   }
 
-  // ---- epilogue: dV_jc = F_jc (G^T E)_cj; sum dV * w for dtau
+  // ---- epilogue: dV_jc = F_jc (G^T E)_cj; dk, dcb; sum dV * w for dtau
   float sv = 0.f;
   if (kvalid) {
     f16* drow = dzv + (tokbase + key) * (int64_t)(HM + D) + HM + h * DV;
@@ -1026,14 +1068,14 @@ __attribute__((amdgpu_waves_per_eu(soft_fast_bwd_waves<M, DV>(), soft_fast_bwd_w
         }
         *reinterpret_cast<f16x4*>(drow + 32 * cb + 8 * g + 4 * h32) = o;
       }
-  }
-  {
-    const int kk = tid % KW, grp = tid / KW;
-    if (k0 + kk < N) {
 #pragma unroll
-      for (int c = 0; c < CPT; ++c) dk[(rowbase + k0 + kk) * M + grp * CPT + c] = dka[c];
-      if (grp == 0) dcb[rowbase + k0 + kk] += dcba;  // the prep wrote the row sum
-    }
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int code = 32 * mb + acc_row(r, lane);
+        if (code < M) dk[(rowbase + key) * M + code] = dka[mb][r];
+        if (code == M) dcb[rowbase + key] += dka[mb][r];  // the prep wrote the row sum
+      }
   }
 #pragma unroll
   for (int sh = 32; sh >= 1; sh >>= 1) {
