@@ -316,8 +316,10 @@ size_t soft_part_bytes(const Dims& d) {
 }
 size_t soft_state_bytes(const Dims& d) {
   const size_t bh = (size_t)d.B * d.H;
-  return 2 * align_up(bh * d.DV * 4) + align_up(bh * d.N * 4) + align_up(4);
+  return 2 * align_up(bh * d.DV * 4) + align_up(bh * d.N * 4) + align_up(4) + 2 * align_up(bh * d.DV * d.NP * 2);
 }
+// G hi / lo of the product-form backward, [B*H, N, DV] bf16 each
+size_t soft_g_bytes(const Dims& d) { return 2 * align_up((size_t)d.B * d.H * d.N * d.DV * 2); }
 SoftState carve_soft_state(void* base, const Dims& d) {
   const size_t bh = (size_t)d.B * d.H;
   char* p = static_cast<char*>(base);
@@ -325,7 +327,9 @@ SoftState carve_soft_state(void* base, const Dims& d) {
   st.vmax = reinterpret_cast<float*>(p); p += align_up(bh * d.DV * 4);
   st.vmin = reinterpret_cast<float*>(p); p += align_up(bh * d.DV * 4);
   st.arow = reinterpret_cast<float*>(p); p += align_up(bh * d.N * 4);
-  st.flag = reinterpret_cast<int*>(p);
+  st.flag = reinterpret_cast<int*>(p); p += align_up(4);
+  st.fth = reinterpret_cast<uint16_t*>(p); p += align_up(bh * d.DV * d.NP * 2);
+  st.ftl = reinterpret_cast<uint16_t*>(p);
   return st;
 }
 // The soft entry points accept MORPHO_MODE_SOFT_EXACT beside the common bits.
@@ -357,7 +361,7 @@ MORPHO_EXPORT size_t morpho_soft_backward_workspace_size(int64_t B, int64_t N, i
   const int st = make_dims(B, N, D, H, cube_m, 1.0f, 0, d);
   g_last_error = keep;
   if (st != MORPHO_OK) return 0;
-  return bwd_bytes(d) + soft_part_bytes(d) + (have_forward_workspace ? 0 : proj_bytes(d));
+  return bwd_bytes(d) + soft_part_bytes(d) + soft_g_bytes(d) + (have_forward_workspace ? 0 : proj_bytes(d));
 }
 
 MORPHO_EXPORT int morpho_soft_forward(const void* X, const void* W_phi, const void* gate_q, const void* gate_k,
@@ -392,6 +396,7 @@ MORPHO_EXPORT int morpho_soft_forward(const void* X, const void* W_phi, const vo
   // product form on MFMA; the element-wise kernel runs only if some output
   // failed its check (the flag, cleared by soft_colext)
   MORPHO_LAUNCH("soft_colext", launch_soft_colext(d, p, ss, s));
+  MORPHO_LAUNCH("soft_fvals", launch_soft_fvals(d, p, tau, sgn, ss, s));
   MORPHO_LAUNCH("soft_fwd_fast", launch_soft_fwd_fast(d, p, tau, sgn, ss, o, zb, s));
   MORPHO_LAUNCH("soft_fwd", launch_soft_fwd(d, p, tau, sgn, o, zb, ss.flag, s));
   return MORPHO_OK;
@@ -417,7 +422,7 @@ MORPHO_EXPORT int morpho_soft_backward(const void* grad_out, const void* X, cons
       misaligned(dX) || misaligned(dW_phi) || misaligned(dW_V))
     return fail(MORPHO_ERR_INVALID_ARGUMENT, "tensor pointers must be 16-byte aligned");
   const bool have_fwd = forward_workspace != nullptr;
-  const size_t need = bwd_bytes(d) + soft_part_bytes(d) + (have_fwd ? 0 : proj_bytes(d));
+  const size_t need = bwd_bytes(d) + soft_part_bytes(d) + soft_g_bytes(d) + (have_fwd ? 0 : proj_bytes(d));
   if (!workspace || workspace_bytes < need)
     return fail(MORPHO_ERR_WORKSPACE, "backward workspace needs %zu bytes (got %zu)", need, workspace_bytes);
   if ((reinterpret_cast<uintptr_t>(workspace) & 255) != 0 ||
@@ -438,15 +443,18 @@ MORPHO_EXPORT int morpho_soft_backward(const void* grad_out, const void* X, cons
   float* prep_part = reinterpret_cast<float*>(ws + bwd_bytes(d));
   float* bwd_part = prep_part + soft_prep_blocks(d);
   float* fast_part = bwd_part + 2 * soft_bwd_exact_slots(d);
+  auto* gh = reinterpret_cast<uint16_t*>(ws + bwd_bytes(d) + soft_part_bytes(d));
+  auto* gl = gh + align_up((size_t)d.B * d.H * d.N * d.DV * 2) / 2;
   const auto* go = static_cast<const _Float16*>(grad_out);
-  MORPHO_LAUNCH("soft_bwd_prep", launch_soft_bwd_prep(d, go, zb, g, prep_part, s));
   if (have_fwd && !exact) {
     // the forward's state: the product form when its flag stayed 0, else the
     // element-wise kernel (each writes zero partials when it does not run)
     const SoftState ss = carve_soft_state(static_cast<char*>(const_cast<void*>(forward_workspace)) + proj_bytes(d), d);
-    MORPHO_LAUNCH("soft_bwd_fast", launch_soft_bwd_fast(d, p, go, zb, tau, sgn, ss, g, fast_part, s));
+    MORPHO_LAUNCH("soft_bwd_prep", launch_soft_bwd_prep(d, go, zb, g, prep_part, tau, sgn, &ss, gh, gl, s));
+    MORPHO_LAUNCH("soft_bwd_fast", launch_soft_bwd_fast(d, p, go, zb, tau, sgn, ss, gh, gl, g, fast_part, s));
     MORPHO_LAUNCH("soft_bwd", launch_soft_bwd(d, p, go, zb, tau, sgn, g, bwd_part, ss.flag, s));
   } else {
+    MORPHO_LAUNCH("soft_bwd_prep", launch_soft_bwd_prep(d, go, zb, g, prep_part, tau, sgn, nullptr, nullptr, nullptr, s));
     MORPHO_LAUNCH("soft_bwd", launch_soft_bwd(d, p, go, zb, tau, sgn, g, bwd_part, nullptr, s));
     MORPHO_LAUNCH("soft_part_clear", launch_fill_zero(fast_part, 2 * (soft_bwd_slots(d) - soft_bwd_exact_slots(d)), s));
   }

@@ -120,21 +120,28 @@ struct SoftState {
   float* vmin;  // [B*H, DV] min over keys of V
   float* arow;  // [B*H, N] row reference A_i (maximum of sgn log2e s_ij / tau over the row's keys)
   int* flag;    // nonzero: some output failed the product form's check; the element-wise path ran
+  uint16_t* fth;  // [B*H, DV, NP] bf16 hi of F = 2^(w - B_c), keys contiguous (zero past N)
+  uint16_t* ftl;  // [B*H, DV, NP] bf16 lo of F
 };
 // Element-wise kernels; with run_flag they do nothing unless *run_flag != 0.
 hipError_t launch_soft_fwd(const Dims& d, const ProjBuffers& p, const float* tau, int sgn, _Float16* out, float* zb,
                            const int* run_flag, hipStream_t s);
 hipError_t launch_soft_colext(const Dims& d, const ProjBuffers& p, const SoftState& st, hipStream_t s);
+hipError_t launch_soft_fvals(const Dims& d, const ProjBuffers& p, const float* tau, int sgn, const SoftState& st,
+                             hipStream_t s);
 hipError_t launch_soft_fwd_fast(const Dims& d, const ProjBuffers& p, const float* tau, int sgn, const SoftState& st,
                                 _Float16* out, float* zb, hipStream_t s);
+// With st non-null (the product form will run) the prep also writes G =
+// dO 2^(A_i + B_c - zb) as bf16 hi / lo pairs, [B*H, N, DV] each, to gh / gl.
 hipError_t launch_soft_bwd_prep(const Dims& d, const _Float16* grad_out, const float* zb, const BwdBuffers& g,
-                                float* part, hipStream_t s);
+                                float* part, const float* tau, int sgn, const SoftState* st, uint16_t* gh,
+                                uint16_t* gl, hipStream_t s);
 hipError_t launch_soft_bwd(const Dims& d, const ProjBuffers& p, const _Float16* grad_out, const float* zb,
                            const float* tau, int sgn, const BwdBuffers& g, float* part, const int* run_flag,
                            hipStream_t s);
 hipError_t launch_soft_bwd_fast(const Dims& d, const ProjBuffers& p, const _Float16* grad_out, const float* zb,
-                                const float* tau, int sgn, const SoftState& st, const BwdBuffers& g, float* part,
-                                hipStream_t s);
+                                const float* tau, int sgn, const SoftState& st, const uint16_t* gh,
+                                const uint16_t* gl, const BwdBuffers& g, float* part, hipStream_t s);
 int soft_bwd_exact_slots(const Dims& d);  // the element-wise backward's share of soft_bwd_slots
 hipError_t launch_fill_zero(float* p, int n, hipStream_t s);
 hipError_t launch_set_flag(int* p, int v, hipStream_t s);

@@ -305,6 +305,41 @@ hipError_t launch_soft_colext(const Dims& d, const ProjBuffers& p, const SoftSta
   return hipGetLastError();
 }
 
+// F^T = 2^(w - B_c) of every (head, column, key) as bf16 hi / lo pairs,
+// [B*H, DV, NP] with keys contiguous: the tiles every query block of the
+// product-form forward reads. One thread per 8 keys of a column.
+__global__ __launch_bounds__(256) void soft_fvals_kernel(const f16* __restrict__ vt, const uint8_t* __restrict__ vlo,
+                                                         const float* __restrict__ tau_p, SoftState st, int N, int NP,
+                                                         int DV, int64_t nchunks, float sgn) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= nchunks) return;
+  const int64_t col = i / (NP / 8);  // bh * DV + c
+  const int k0 = 8 * (int)(i - col * (NP / 8));
+  const int bh = (int)(col / DV), c = (int)(col - (int64_t)bh * DV);
+  const float kw = sgn * kLog2e / *tau_p;
+  const float bc = kw * (kw > 0.f ? st.vmax[col] : st.vmin[col]);
+  bf16x8 hi, lo;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int key = k0 + j;
+    const float f = key < N ? fast_exp2(kw * load_value(vt, vlo, bh, DV, NP, c, key) - bc) : 0.f;
+    bf16 h, l;
+    split_bf16(f, h, l);
+    hi[j] = h;
+    lo[j] = l;
+  }
+  *reinterpret_cast<bf16x8*>(st.fth + col * NP + k0) = hi;
+  *reinterpret_cast<bf16x8*>(st.ftl + col * NP + k0) = lo;
+}
+
+hipError_t launch_soft_fvals(const Dims& d, const ProjBuffers& p, const float* tau, int sgn, const SoftState& st,
+                             hipStream_t s) {
+  const int64_t n = (int64_t)d.B * d.H * d.DV * (d.NP / 8);
+  hipLaunchKernelGGL(soft_fvals_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p.vt, p.vlo, tau, st, d.N,
+                     d.NP, d.DV, n, (float)sgn);
+  return hipGetLastError();
+}
+
 template <int M, int DV>
 struct FastCfg {
   static constexpr int CW = 2 * M + 8;
@@ -360,15 +395,15 @@ __global__ __launch_bounds__(256) void soft_fwd_fast_kernel(const f16* __restric
 
   const int kend = causal ? min(N, q0 + C::QW) : N;
   const int nkb = (kend + 31) / 32;
+  // F^T tile of keys 32 kb .. + 31: 16-byte pieces of the precomputed rows
+  const bf16* fth = reinterpret_cast<const bf16*>(st.fth) + (int64_t)bh * DV * NP;
+  const bf16* ftl = reinterpret_cast<const bf16*>(st.ftl) + (int64_t)bh * DV * NP;
   auto stage = [&](int kb, bf16* fh, bf16* fl) {
-    for (int e = tid; e < 32 * DV; e += 256) {
-      const int k = e & 31, c = e >> 5, key = 32 * kb + k;
-      float f = 0.f;
-      if (key < N) f = fast_exp2(kw * load_value(vt, vlo, bh, DV, NP, c, key) - sbc[c]);
-      bf16 hi, lo;
-      split_bf16(f, hi, lo);
-      fh[c * C::FS + k] = hi;
-      fl[c * C::FS + k] = lo;
+    for (int e = tid; e < 4 * DV; e += 256) {
+      const int c = e >> 2, q4 = e & 3;
+      const int64_t src = (int64_t)c * NP + 32 * kb + 8 * q4;
+      *reinterpret_cast<bf16x8*>(fh + c * C::FS + 8 * q4) = *reinterpret_cast<const bf16x8*>(fth + src);
+      *reinterpret_cast<bf16x8*>(fl + c * C::FS + 8 * q4) = *reinterpret_cast<const bf16x8*>(ftl + src);
     }
   };
   __syncthreads();  // sbc
@@ -485,7 +520,12 @@ template <int DV>
 __global__ __launch_bounds__(256) void soft_bwd_prep_kernel(const f16* __restrict__ grad_out,
                                                             const float* __restrict__ zb, float* __restrict__ dcb,
                                                             float* __restrict__ dq, float* __restrict__ part,
-                                                            int64_t T, int N, int H, int D, int M) {
+                                                            int64_t T, int N, int H, int D, int M,
+                                                            const float* __restrict__ tau_p, float sgn,
+                                                            const float* __restrict__ vmax,
+                                                            const float* __restrict__ vmin,
+                                                            const float* __restrict__ arow, bf16* __restrict__ gh,
+                                                            bf16* __restrict__ gl) {
   constexpr int G = DV / 8;
   __shared__ float red[4];
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -507,6 +547,23 @@ __global__ __launch_bounds__(256) void soft_bwd_prep_kernel(const f16* __restric
       dz += (float)g[e] * z[e];
     }
     if (!live) rs = dz = 0.f;
+    if (gh) {  // G = dO 2^(A_i + B_c - zb) for the product-form backward (0 for a row without keys)
+      const float kw = sgn * kLog2e / *tau_p;
+      const float a = arow[bhn];
+      bf16x8 hi, lo;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int64_t col = bh * DV + c + e;
+        const float bc = kw * (kw > 0.f ? vmax[col] : vmin[col]);
+        const float gv = (live && a > kNegInf) ? (float)g[e] * fast_exp2(a + bc - z[e]) : 0.f;
+        bf16 h, l;
+        split_bf16(gv, h, l);
+        hi[e] = h;
+        lo[e] = l;
+      }
+      *reinterpret_cast<bf16x8*>(gh + bhn * DV + c) = hi;
+      *reinterpret_cast<bf16x8*>(gl + bhn * DV + c) = lo;
+    }
   }
 #pragma unroll
   for (int sh = 1; sh < G; sh <<= 1) rs += __shfl_xor(rs, sh);
@@ -526,15 +583,19 @@ int soft_prep_blocks(const Dims& d) { return (int)((d.T * (d.D / 8) + 255) / 256
 
 template <int M, int DV>
 static hipError_t launch_soft_bwd_prep_t(const Dims& d, const f16* grad_out, const float* zb, const BwdBuffers& g,
-                                         float* part, hipStream_t s) {
+                                         float* part, const float* tau, int sgn, const SoftState* st, uint16_t* gh,
+                                         uint16_t* gl, hipStream_t s) {
   hipLaunchKernelGGL((soft_bwd_prep_kernel<DV>), dim3((unsigned)soft_prep_blocks(d)), dim3(256), 0, s, grad_out, zb,
-                     g.dcb, g.dq, part, d.T, d.N, d.H, d.D, d.M);
+                     g.dcb, g.dq, part, d.T, d.N, d.H, d.D, d.M, tau, (float)sgn, st ? st->vmax : nullptr,
+                     st ? st->vmin : nullptr, st ? st->arow : nullptr, st ? reinterpret_cast<bf16*>(gh) : nullptr,
+                     st ? reinterpret_cast<bf16*>(gl) : nullptr);
   return hipGetLastError();
 }
 
 hipError_t launch_soft_bwd_prep(const Dims& d, const f16* grad_out, const float* zb, const BwdBuffers& g, float* part,
+                                const float* tau, int sgn, const SoftState* st, uint16_t* gh, uint16_t* gl,
                                 hipStream_t s) {
-  MORPHO_MDV_DISPATCH(launch_soft_bwd_prep_t, d, grad_out, zb, g, part, s);
+  MORPHO_MDV_DISPATCH(launch_soft_bwd_prep_t, d, grad_out, zb, g, part, tau, sgn, st, gh, gl, s);
 }
 
 // ============================================================ backward
@@ -824,7 +885,7 @@ __global__ __launch_bounds__(256)
 __attribute__((amdgpu_waves_per_eu(soft_fast_bwd_waves<M, DV>(), soft_fast_bwd_waves<M, DV>()))) void soft_bwd_fast_kernel(
     const f16* __restrict__ qa, const f16* __restrict__ ka, const f16* __restrict__ vt,
     const uint8_t* __restrict__ vlo, const float4* __restrict__ tstat, const float* __restrict__ tau_p, SoftState st,
-    const f16* __restrict__ grad_out, const float* __restrict__ zb, float* __restrict__ dq, float* __restrict__ dk,
+    const bf16* __restrict__ gh, const bf16* __restrict__ gl, float* __restrict__ dq, float* __restrict__ dk,
     float* __restrict__ dcb, f16* __restrict__ dzv, float* __restrict__ part, int N, int NP, int H, int D, int HM,
     int BH, int causal, float sgn) {
   constexpr int CW = 2 * M + 8, NCH = M / 8, CB = DV / 32, KW = 128, QT = 32;
@@ -910,18 +971,15 @@ __attribute__((amdgpu_waves_per_eu(soft_fast_bwd_waves<M, DV>(), soft_fast_bwd_w
   for (int qs = qstart; qs < N; qs += QT) {
     // ---- stage G (hi/lo), A and [phi | 1] of queries qs .. qs + QT - 1 (zero
     // past N and for rows without keys)
-    for (int e = tid; e < QT * DV; e += 256) {
-      const int r = e / DV, c = e % DV, qq = qs + r;
-      float g = 0.f;
+    for (int e = tid; e < QT * DV / 8; e += 256) {  // 16-byte pieces of the prep's G rows
+      const int r = e / (DV / 8), c8 = 8 * (e % (DV / 8)), qq = qs + r;
+      bf16x8 hi = {}, lo = {};
       if (qq < N) {
-        const float a = st.arow[rowbase + qq];
-        if (a > kNegInf)
-          g = (float)grad_out[(tokbase + qq) * D + h * DV + c] * fast_exp2(a + sbc[c] - zb[(rowbase + qq) * DV + c]);
+        hi = *reinterpret_cast<const bf16x8*>(gh + (rowbase + qq) * DV + c8);
+        lo = *reinterpret_cast<const bf16x8*>(gl + (rowbase + qq) * DV + c8);
       }
-      bf16 hi, lo;
-      split_bf16(g, hi, lo);
-      sgh[r * GS + c] = hi;
-      sgl[r * GS + c] = lo;
+      *reinterpret_cast<bf16x8*>(sgh + r * GS + c8) = hi;
+      *reinterpret_cast<bf16x8*>(sgl + r * GS + c8) = lo;
     }
     for (int e = tid; e < QT * 32 * MB; e += 256) {
       const int r = e / (32 * MB), c = e % (32 * MB), qq = qs + r;
@@ -1095,24 +1153,28 @@ __attribute__((amdgpu_waves_per_eu(soft_fast_bwd_waves<M, DV>(), soft_fast_bwd_w
 
 template <int M, int DV>
 static hipError_t launch_soft_bwd_fast_t(const Dims& d, const ProjBuffers& p, const f16* grad_out, const float* zb,
-                                         const float* tau, int sgn, const SoftState& st, const BwdBuffers& g,
-                                         float* part, hipStream_t s) {
+                                         const float* tau, int sgn, const SoftState& st, const uint16_t* gh,
+                                         const uint16_t* gl, const BwdBuffers& g, float* part, hipStream_t s) {
+  (void)grad_out;
+  (void)zb;
   const dim3 grid(xcd_grid((d.N + 127) / 128, d.B * d.H));
+  const auto* h = reinterpret_cast<const bf16*>(gh);
+  const auto* l = reinterpret_cast<const bf16*>(gl);
   if (d.mask_diag)
     hipLaunchKernelGGL((soft_bwd_fast_kernel<M, DV, true>), grid, dim3(256), 0, s, p.qa, p.ka, p.vt, p.vlo, p.tstat,
-                       tau, st, grad_out, zb, g.dq, g.dk, g.dcb, g.dzv, part, d.N, d.NP, d.H, d.D, d.HM, d.B * d.H,
+                       tau, st, h, l, g.dq, g.dk, g.dcb, g.dzv, part, d.N, d.NP, d.H, d.D, d.HM, d.B * d.H,
                        d.causal, (float)sgn);
   else
     hipLaunchKernelGGL((soft_bwd_fast_kernel<M, DV, false>), grid, dim3(256), 0, s, p.qa, p.ka, p.vt, p.vlo, p.tstat,
-                       tau, st, grad_out, zb, g.dq, g.dk, g.dcb, g.dzv, part, d.N, d.NP, d.H, d.D, d.HM, d.B * d.H,
+                       tau, st, h, l, g.dq, g.dk, g.dcb, g.dzv, part, d.N, d.NP, d.H, d.D, d.HM, d.B * d.H,
                        d.causal, (float)sgn);
   return hipGetLastError();
 }
 
 hipError_t launch_soft_bwd_fast(const Dims& d, const ProjBuffers& p, const f16* grad_out, const float* zb,
-                                const float* tau, int sgn, const SoftState& st, const BwdBuffers& g, float* part,
-                                hipStream_t s) {
-  MORPHO_MDV_DISPATCH(launch_soft_bwd_fast_t, d, p, grad_out, zb, tau, sgn, st, g, part, s);
+                                const float* tau, int sgn, const SoftState& st, const uint16_t* gh,
+                                const uint16_t* gl, const BwdBuffers& g, float* part, hipStream_t s) {
+  MORPHO_MDV_DISPATCH(launch_soft_bwd_fast_t, d, p, grad_out, zb, tau, sgn, st, gh, gl, g, part, s);
 }
 int soft_bwd_exact_slots(const Dims& d) {
   return (int)xcd_grid((d.N + 32 * (128 / d.DV) - 1) / (32 * (128 / d.DV)), d.B * d.H);
