@@ -61,16 +61,25 @@ class SoftMorphAttentionFunction(torch.autograd.Function):
         return (*grads, None, None, None, None, None, None)
 
 
+# Mode bit of the soft ops: always run the element-wise kernels instead of the
+# product form on MFMA (which falls back to them by itself where its
+# precision guarantee does not hold).
+SOFT_EXACT = 16
+
+
 def soft_morph_attention(x, W_phi, gate_q, gate_k, W_V, tau, num_heads: int, cube_m: int, *, scale: float = 1.0,
                          causal: bool = False, erosion: bool = False, projection: str = "sigmoid",
-                         mask_diag: bool = False) -> torch.Tensor:
+                         mask_diag: bool = False, exact: bool = False) -> torch.Tensor:
     """Soft tropical aggregation with autograd support.
 
     :param tau: float32 CUDA tensor with one element, the temperature (> 0).
     :param erosion: soft min-plus (``sgn = -1``) instead of soft max-plus.
+    :param exact: always use the element-wise kernels (one exp2 per query,
+        key and value column) instead of the product form on MFMA.
     """
+    variant = variant_bits(projection, mask_diag) | (SOFT_EXACT if exact else 0)
     return SoftMorphAttentionFunction.apply(x, W_phi, gate_q, gate_k, W_V, tau, num_heads, cube_m, scale, causal,
-                                            -1 if erosion else 1, variant_bits(projection, mask_diag))
+                                            -1 if erosion else 1, variant)
 
 
 class SoftMorphAttention(nn.Module):

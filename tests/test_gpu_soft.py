@@ -224,3 +224,22 @@ def test_product_form_falls_back_for_small_tau():
     _say(f"[soft] small tau: flag {flag}")
     assert flag == 1
     assert torch.equal(fast[0], exact[0]) and torch.equal(fast[1], exact[1])
+
+
+def test_exact_switch_gradients_agree():
+    """soft_morph_attention(..., exact=True) (element-wise kernels, forward and
+    backward) and the default product form give the same gradients to well
+    inside the parity bar."""
+    from morphottention_amd import soft_morph_attention
+    B, N, H, m, dv = 1, 150, 2, 16, 64
+    x, params, dout = _inputs(B, N, H, m, dv, seed=1100)
+    res = []
+    for exact in (False, True):
+        leaves = [t.detach().clone().requires_grad_(True) for t in (x, *params)]
+        t = torch.tensor([0.6], dtype=torch.float32, device="cuda", requires_grad=True)
+        out = soft_morph_attention(leaves[0], *leaves[1:], t, H, m, scale=0.9, causal=True, exact=exact)
+        out.backward(dout)
+        res.append([g.grad.float() for g in (*leaves, t)])
+    rels = [((a - b).abs().max() / b.abs().max().clamp_min(1e-30)).item() for a, b in zip(*res)]
+    _say("[soft] product form vs element-wise gradients: " + " ".join(f"{n}={r:.2e}" for n, r in zip(NAMES, rels)))
+    assert max(rels) <= 2e-3
