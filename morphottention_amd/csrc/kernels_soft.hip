@@ -13,26 +13,26 @@
 // the aggregation built from them on top of this library's projection.
 //
 // MI355X design:
-//  * The work is N^2 dv exponentials (one per query, key and value column):
-//    it is bound by the VALU and the transcendental unit, not by MFMA or HBM.
-//    Scores come from the same code-row MFMA as the softmax path (one 32 x 32
-//    tile per wave and key block), with the query affine block set to the
-//    token bias so that the accumulator is exactly log2e s_ij.
-//  * Everything runs in base 2: y = sgn log2e (s + v) / tau, so each element
-//    costs an add, a max or subtract, one v_exp_f32 and an accumulate.
-//  * Forward: lane = query, 16 keys of each 32-key block per lane, 32 value
-//    columns per wave; an online (max, sum) per (query, column) kept in
-//    registers, merged across the two half-waves at the end (lse_merge).
-//    The values of a 32-key block are decoded once (V_hi + V_lo) into an fp32
-//    LDS tile already scaled by sgn log2e / tau and read as broadcasts.
-//  * Backward: lane = key, key-outer. P_ijc = 2^(y - zb_ic) from the forward's
-//    fp32 normaliser zb; dV accumulates in registers, ds_ij = sum_c dO_ic P_ijc
-//    in registers, and the code gradients dk, dcb (key side) and dq (query
-//    side, fp32 atomics) are formed from the ds tile in LDS. The query-side
-//    row sum of ds, sum_c dO_ic, which the softmax gradient does not have, is
-//    folded into dcb, so the projection backward is shared unchanged.
-//  * dtau = (sum dO out - sum ds s - sum dV V) / tau from per-workgroup
-//    partials, reduced in a fixed order.
+//  * Scores come from the same code-row MFMA as the softmax path, with the
+//    query affine block set to the token bias so that the accumulator is
+//    exactly log2e s_ij. Everything runs in base 2: y = u + w with
+//    u = sgn log2e s / tau and w = sgn log2e v / tau.
+//  * Product form (the default): sum_j 2^(u_ij + w_jc) = 2^(A_i + B_c) (E F)_ic
+//    with E = 2^(u - A_i), F = 2^(w - B_c) (A_i the running row maximum of u,
+//    B_c the maximum of w over the head's keys), so the aggregation and both
+//    of its gradient products run on the bf16 MFMA (hi/lo pairs): one exp2
+//    per (query, key) instead of per (query, key, column). Each output checks
+//    that its sum is at least 2^-80, below which the form could lose
+//    precision; if any fails, a device flag makes the element-wise kernels
+//    recompute the call.
+//  * Element-wise kernels (the fallback, or on request): forward lane = query
+//    with an online (max, sum) per (query, column) (lse_update, lse_merge,
+//    lse_finalize); backward lane = key with P_ijc = 2^(y - zb_ic). One exp2
+//    and four VALU operations per (query, key, column).
+//  * Both backward paths fold the query-side row sum of ds, sum_c dO_ic (which
+//    the softmax gradient does not have), into dcb, so the projection
+//    backward is shared unchanged, and form dtau = (sum dO out - sum ds s -
+//    sum dV V) / tau from per-workgroup partials reduced in a fixed order.
 #include "common.h"
 #include "internal.h"
 
