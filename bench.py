@@ -295,7 +295,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; the path is sharded over "
-                                   "(batch x head) without collectives, see DESIGN.md"}))
+                                   "(batch x head) without collectives"}))
         sys.exit(2)
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no ROCm GPU visible"}))
