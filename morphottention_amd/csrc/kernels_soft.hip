@@ -422,12 +422,24 @@ __global__ __launch_bounds__(256) void soft_fwd_fast_kernel(const f16* __restric
     f32x16 acc = code_dot<M, true>(kf, qf, f32x16{});
     acc = mfma8(kaug, qaug, acc);
     float u[16], tm = kNegInf;
+    // wave-uniform: only blocks with ragged keys, keys after some query or the
+    // diagonal need the per-score mask
+    const bool need_mask = (key0 + 32 > N) || (causal != 0 && key0 + 31 > qw0) ||
+                           (MD && key0 <= qw0 + 31 && key0 + 31 >= qw0);
+    if (need_mask) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int key = key0 + (r < 8 ? 8 * h32 + r : 8 + 8 * h32 + r);
-      const bool drop = (key >= N) | (causal != 0 && key > q) | (MD && key == q);
-      u[r] = drop ? kNegInf : ks * acc[r];
-      tm = fmaxf(tm, u[r]);
+      for (int r = 0; r < 16; ++r) {
+        const int key = key0 + (r < 8 ? 8 * h32 + r : 8 + 8 * h32 + r);
+        const bool drop = (key >= N) | (causal != 0 && key > q) | (MD && key == q);
+        u[r] = drop ? kNegInf : ks * acc[r];
+        tm = fmaxf(tm, u[r]);
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        u[r] = ks * acc[r];
+        tm = fmaxf(tm, u[r]);
+      }
     }
     tm = fmaxf(tm, __shfl_xor(tm, 32));
     const float mn = fmaxf(mrow, tm);
@@ -1009,18 +1021,29 @@ __attribute__((amdgpu_waves_per_eu(soft_fast_bwd_waves<M, DV>(), soft_fast_bwd_w
     f32x16 acc = code_dot<M, false>(kf, qf, f32x16{});
     acc = mfma8(qaug, kaug, acc);
     __syncthreads();  // staging complete
-    // ---- E = 2^(u - A_i) (bf16 hi/lo, the B operand of G^T E)
+    // ---- E = 2^(u - A_i) (bf16 hi/lo, the B operand of G^T E); the per-score
+    // mask only for blocks with ragged queries or keys, keys after some query
+    // or the diagonal (wave-uniform)
     bf16x8 eh[2], el[2];
     float e32[16];
+    const bool need_mask = (qs + 32 > N) || (kw0 + 32 > N) || (causal != 0 && kw0 + 31 > qs) ||
+                           (MD && kw0 <= qs + 31 && kw0 + 31 >= qs);
+    if (need_mask) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int p = r < 8 ? 8 * h32 + r : 8 + 8 * h32 + r;
+        const int qq = qs + p;
+        const bool drop = (qq >= N) | !kvalid | (causal != 0 && key > qq) | (MD && key == qq);
+        e32[r] = drop ? 0.f : fast_exp2(ks * acc[r] - sar[p]);
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) e32[r] = fast_exp2(ks * acc[r] - sar[r < 8 ? 8 * h32 + r : 8 + 8 * h32 + r]);
+    }
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int p = r < 8 ? 8 * h32 + r : 8 + 8 * h32 + r;
-      const int qq = qs + p;
-      const bool drop = (qq >= N) | !kvalid | (causal != 0 && key > qq) | (MD && key == qq);
-      const float e = drop ? 0.f : fast_exp2(ks * acc[r] - sar[p]);
-      e32[r] = e;
       bf16 hi, lo;
-      split_bf16(e, hi, lo);
+      split_bf16(e32[r], hi, lo);
       eh[r >> 3][r & 7] = hi;
       el[r >> 3][r & 7] = lo;
     }
