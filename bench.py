@@ -241,9 +241,11 @@ def bench_soft(args):
             "soft_fwd_fast": ("mfma", 2.0 * P * (m + dv)), "soft_bwd_fast": ("mfma", 2.0 * P * (3 * m + 2 * dv))}
     kernels = {}
     avgs = {k: sum(v) / len(v) for k, v in per.items()}
-    for exact, fast in (("soft_fwd", "soft_fwd_fast"), ("soft_bwd", "soft_bwd_fast")):
-        if exact in avgs and fast in avgs and avgs[exact] < 0.05 * avgs[fast]:
-            work.pop(exact)  # the product form was exact: the element-wise kernel only read its flag
+    for exact in ("soft_fwd", "soft_bwd"):
+        # faster than the exponential unit allows: the product form was exact
+        # and the element-wise kernel only read its flag
+        if exact in avgs and work[exact][1] / (avgs[exact] * 1e-3) > PEAK_EXP_PER_S:
+            work.pop(exact)
     for name, v in sorted(per.items(), key=lambda kv: -sum(kv[1])):
         avg = sum(v) / len(v)
         kind, amount = work.get(name, (None, None))

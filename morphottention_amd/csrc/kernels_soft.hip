@@ -1034,7 +1034,11 @@ __attribute__((amdgpu_waves_per_eu(soft_fast_bwd_waves<M, DV>(), soft_fast_bwd_w
         const int p = r < 8 ? 8 * h32 + r : 8 + 8 * h32 + r;
         const int qq = qs + p;
         const bool drop = (qq >= N) | !kvalid | (causal != 0 && key > qq) | (MD && key == qq);
-        e32[r] = drop ? 0.f : fast_exp2(ks * acc[r] - sar[p]);
+        // sar[p] (p < 32) is read for every score and the result selected:
+        // a read under the condition compiles to one divergent block, with
+        // its own LDS wait, per score
+        const float ev = fast_exp2(ks * acc[r] - sar[p]);
+        e32[r] = drop ? 0.f : ev;
       }
     } else {
 #pragma unroll
