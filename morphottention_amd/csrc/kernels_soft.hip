@@ -982,35 +982,56 @@ __attribute__((amdgpu_waves_per_eu(soft_fast_bwd_waves<M, DV>(), soft_fast_bwd_w
   const int qstart = causal ? k0 : 0;
   for (int qs = qstart; qs < N; qs += QT) {
     // ---- stage G (hi/lo), A and [phi | 1] of queries qs .. qs + QT - 1 (zero
-    // past N and for rows without keys)
-    for (int e = tid; e < QT * DV / 8; e += 256) {  // 16-byte pieces of the prep's G rows
-      const int r = e / (DV / 8), c8 = 8 * (e % (DV / 8)), qq = qs + r;
-      bf16x8 hi = {}, lo = {};
-      if (qq < N) {
-        hi = *reinterpret_cast<const bf16x8*>(gh + (rowbase + qq) * DV + c8);
-        lo = *reinterpret_cast<const bf16x8*>(gl + (rowbase + qq) * DV + c8);
+    // past N and for rows without keys). Every global load of the tile is
+    // issued before the first LDS store, so the tile costs one memory
+    // latency; pieces are 16 bytes (G rows, and the hi / lo halves of the
+    // code rows: 8 codes, or the ones column and zero padding).
+    constexpr int GP = QT * DV / 8, GPT = (GP + 255) / 256;  // G pieces, per thread
+    constexpr int PP = QT * 4 * MB, PPT = (PP + 255) / 256;  // [phi | 1] pieces, per thread
+    bf16x8 gvh[GPT], gvl[GPT];
+    f16x8 pvh[PPT], pvl[PPT];
+#pragma unroll
+    for (int i = 0; i < GPT; ++i) {
+      const int e = tid + 256 * i, r = e / (DV / 8), c8 = 8 * (e % (DV / 8)), qq = qs + r;
+      gvh[i] = bf16x8{};
+      gvl[i] = bf16x8{};
+      if (e < GP && qq < N) {
+        gvh[i] = *reinterpret_cast<const bf16x8*>(gh + (rowbase + qq) * DV + c8);
+        gvl[i] = *reinterpret_cast<const bf16x8*>(gl + (rowbase + qq) * DV + c8);
       }
-      *reinterpret_cast<bf16x8*>(sgh + r * GS + c8) = hi;
-      *reinterpret_cast<bf16x8*>(sgl + r * GS + c8) = lo;
     }
-    for (int e = tid; e < QT * 32 * MB; e += 256) {
-      const int r = e / (32 * MB), c = e % (32 * MB), qq = qs + r;
-      f16 hi = (f16)0.f, lo = (f16)0.f;
-      if (qq < N) {
-        if (c < M) {
-          hi = qa[(rowbase + qq) * CW + c];
-          lo = qa[(rowbase + qq) * CW + M + 8 + c];
-        } else if (c == M) {
-          hi = (f16)1.f;
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) {
+      const int e = tid + 256 * i, r = e / (4 * MB), c8 = 8 * (e % (4 * MB)), qq = qs + r;
+      pvh[i] = f16x8{};
+      pvl[i] = f16x8{};
+      if (e < PP && qq < N) {
+        if (c8 < M) {
+          pvh[i] = *reinterpret_cast<const f16x8*>(qa + (rowbase + qq) * CW + c8);
+          pvl[i] = *reinterpret_cast<const f16x8*>(qa + (rowbase + qq) * CW + M + 8 + c8);
+        } else if (c8 == M) {
+          pvh[i][0] = (f16)1.f;
         }
       }
-      sph[r * PT + c] = hi;
-      spl[r * PT + c] = lo;
     }
-    if (tid < QT) {
-      const float a = qs + tid < N ? st.arow[rowbase + qs + tid] : kNegInf;
-      sar[tid] = a > kNegInf ? a : 0.f;  // rows without keys: every score is masked
+    const float arow = tid < QT && qs + tid < N ? st.arow[rowbase + qs + tid] : kNegInf;
+#pragma unroll
+    for (int i = 0; i < GPT; ++i) {
+      const int e = tid + 256 * i, r = e / (DV / 8), c8 = 8 * (e % (DV / 8));
+      if (e < GP) {
+        *reinterpret_cast<bf16x8*>(sgh + r * GS + c8) = gvh[i];
+        *reinterpret_cast<bf16x8*>(sgl + r * GS + c8) = gvl[i];
+      }
     }
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) {
+      const int e = tid + 256 * i, r = e / (4 * MB), c8 = 8 * (e % (4 * MB));
+      if (e < PP) {
+        *reinterpret_cast<f16x8*>(sph + r * PT + c8) = pvh[i];
+        *reinterpret_cast<f16x8*>(spl + r * PT + c8) = pvl[i];
+      }
+    }
+    if (tid < QT) sar[tid] = arow > kNegInf ? arow : 0.f;  // rows without keys: every score is masked
     // ---- S block, query rows in swap23 order: register r holds query p(r)
     const int qrow = qs + swap23(l32);
     f16x8 qf[NCH];
