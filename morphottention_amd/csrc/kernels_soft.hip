@@ -64,6 +64,25 @@ __device__ __forceinline__ float load_value(const f16* __restrict__ vt, const ui
   return hi + __builtin_amdgcn_cvt_f32_fp8((int)b, 0) * (1.0f / (float)(1 << kVloExp));
 }
 
+// V of keys k0 .. k0 + 7 of column c (k0 % 8 == 0, k0 + 8 <= NP), as
+// load_value computes it: one 16-byte V_hi load and one 8-byte remainder
+// load (vlo_pos maps 8 aligned keys to 8 consecutive bytes of their block).
+__device__ __forceinline__ void load_values8(const f16* __restrict__ vt, const uint8_t* __restrict__ vlo, int bh,
+                                             int DV, int NP, int c, int k0, float (&v)[8]) {
+  const f16x8 hi = *reinterpret_cast<const f16x8*>(vt + ((int64_t)bh * DV + c) * NP + k0);
+  const uint2 lo =
+      *reinterpret_cast<const uint2*>(vlo + (((int64_t)bh * (NP / 64) + k0 / 64) * DV + c) * 64 + vlo_pos(k0 & 63));
+  constexpr float s = 1.0f / (float)(1 << kVloExp);
+  v[0] = (float)hi[0] + __builtin_amdgcn_cvt_f32_fp8((int)lo.x, 0) * s;
+  v[1] = (float)hi[1] + __builtin_amdgcn_cvt_f32_fp8((int)lo.x, 1) * s;
+  v[2] = (float)hi[2] + __builtin_amdgcn_cvt_f32_fp8((int)lo.x, 2) * s;
+  v[3] = (float)hi[3] + __builtin_amdgcn_cvt_f32_fp8((int)lo.x, 3) * s;
+  v[4] = (float)hi[4] + __builtin_amdgcn_cvt_f32_fp8((int)lo.y, 0) * s;
+  v[5] = (float)hi[5] + __builtin_amdgcn_cvt_f32_fp8((int)lo.y, 1) * s;
+  v[6] = (float)hi[6] + __builtin_amdgcn_cvt_f32_fp8((int)lo.y, 2) * s;
+  v[7] = (float)hi[7] + __builtin_amdgcn_cvt_f32_fp8((int)lo.y, 3) * s;
+}
+
 // The query operand of a code row with its affine block set to {1, 1, b_hi,
 // b_lo}: the score accumulator is then log2e s_ij (the projection's row
 // reference R is replaced by the token bias b).
@@ -282,10 +301,15 @@ __global__ __launch_bounds__(256) void soft_colext_kernel(const f16* __restrict_
   if (col >= ncol) return;
   const int bh = col / DV, c = col - bh * DV;
   float hi = kNegInf, lo = -kNegInf;
-  for (int k = lane; k < N; k += 64) {
-    const float v = load_value(vt, vlo, bh, DV, NP, c, k);
-    hi = fmaxf(hi, v);
-    lo = fminf(lo, v);
+  for (int k0 = 8 * lane; k0 < N; k0 += 512) {  // 8 keys per lane and pass
+    float v[8];
+    load_values8(vt, vlo, bh, DV, NP, c, k0, v);
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (k0 + j < N) {
+        hi = fmaxf(hi, v[j]);
+        lo = fminf(lo, v[j]);
+      }
   }
 #pragma unroll
   for (int sh = 32; sh >= 1; sh >>= 1) {
@@ -319,10 +343,12 @@ __global__ __launch_bounds__(256) void soft_fvals_kernel(const f16* __restrict__
   const float kw = sgn * kLog2e / *tau_p;
   const float bc = kw * (kw > 0.f ? st.vmax[col] : st.vmin[col]);
   bf16x8 hi, lo;
+  float v[8];
+  load_values8(vt, vlo, bh, DV, NP, c, k0, v);
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const int key = k0 + j;
-    const float f = key < N ? fast_exp2(kw * load_value(vt, vlo, bh, DV, NP, c, key) - bc) : 0.f;
+    const float ev = fast_exp2(kw * v[j] - bc);
+    const float f = k0 + j < N ? ev : 0.f;
     bf16 h, l;
     split_bf16(f, h, l);
     hi[j] = h;
