@@ -1282,7 +1282,11 @@ __global__ __launch_bounds__(256) void soft_tau_reduce_kernel(const float* __res
                                                               float* __restrict__ dtau) {
   __shared__ float red[3][256];
   float a = 0.f, s = 0.f, v = 0.f;
+  // unrolled so that 8 loads are in flight; each thread still adds its
+  // partials in index order, so the result does not depend on the unrolling
+#pragma unroll 8
   for (int i = threadIdx.x; i < nprep; i += 256) a += prep[i];
+#pragma unroll 8
   for (int i = threadIdx.x; i < nbwd; i += 256) {
     s += bwd[2 * i];
     v += bwd[2 * i + 1];
