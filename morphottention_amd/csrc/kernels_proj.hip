@@ -498,7 +498,8 @@ __global__ __launch_bounds__(256) void dw_reduce_kernel(const float* __restrict_
     float s0 = 0.f, s1 = 0.f;
     if (col < HM) {
       int i = grp;
-      for (; i + 16 < nblk; i += 32) {
+#pragma unroll 4
+      for (; i + 16 < nblk; i += 32) {  // unrolled: several loads in flight, same order
         s0 += gpart[(int64_t)i * HM + col];
         s1 += gpart[(int64_t)(i + 16) * HM + col];
       }
@@ -521,7 +522,8 @@ __global__ __launch_bounds__(256) void dw_reduce_kernel(const float* __restrict_
   const int64_t idx = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
   if (idx >= total) return;
   float4 s = *reinterpret_cast<const float4*>(wpart + idx);
-  for (int z = 1; z < splits; ++z) {
+#pragma unroll 4
+  for (int z = 1; z < splits; ++z) {  // unrolled: several loads in flight, same order
     const float4 v = *reinterpret_cast<const float4*>(wpart + (int64_t)z * total + idx);
     s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
   }
