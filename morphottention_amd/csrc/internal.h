@@ -64,7 +64,9 @@ struct ProjBuffers {
   uint8_t* vlo;    // [B*H, NP/64, DV, 64] the rounding remainders V - V_hi, times 2^kVloExp, as
                    // e4m3 bytes rounded toward zero; one [DV][64] block per 64-key tile, whose row holds key
                    // 16 q + 8 h + r at byte 32 h + 8 q + r (h < 2, q < 4, r < 8); zero past N
-  float4* tstat;   // [B*H, N] {b, R, gap, 0}: token bias, softmax reference, bound gap (base 2)
+  float4* tstat;   // [B*H, N] {b, R, gap, t}: token bias, softmax reference, bound gap and the
+                   // self score t = s_ii - b (all base 2; 2^(t + b - lse) is the diagonal weight
+                   // the backward's correction needs)
   _Float16* wt;    // [H*M + D, D] transposed [W_phi | W_V]
   _Float16* wcat;  // [D, H*M + D] [W_phi | W_V] as one row-major matrix
 };
@@ -81,6 +83,8 @@ struct BwdBuffers {
   float* dq;       // [B*H, N, M] sum_j dS_ij phi_j (query side), fp32 atomics
   float* dk;       // [B*H, N, M] sum_i dS_ij phi_i (key side)
   float* dcb;      // [B*H, N]    sum_i dS_ij
+  float* dr;       // [B*H, N]    sum_j dS_ij, the row sums of the rounded dS (0 in exact
+                   //             arithmetic), fp32 atomics
   _Float16* dzv;   // [T, H*M + D] dZ | dV
   float* gpart;    // [n_gate_blocks, H*M] partial sums of phi (2 dk - dcb), the gate factor dG
   float* wpart;    // [splits, D, H*M + D] split-K partials of [dW_phi | dW_V]
@@ -94,8 +98,11 @@ hipError_t launch_transpose_weights(const Dims& d, const _Float16* W_phi, const 
                                     _Float16* wcat, hipStream_t s);
 hipError_t launch_proj_fwd(const Dims& d, const _Float16* X, const _Float16* gate_q, const _Float16* gate_k,
                            const ProjBuffers& p, hipStream_t s);
+// With lse non-null (softmax attention) the row sums g.dr are used to cancel
+// the noise of the rows' delta at the diagonal; null (soft aggregation) uses
+// dq, dk and dcb as they are.
 hipError_t launch_proj_bwd_elem(const Dims& d, const _Float16* gate_q, const _Float16* gate_k, const ProjBuffers& p,
-                                const BwdBuffers& g, hipStream_t s);
+                                const BwdBuffers& g, const float* lse, hipStream_t s);
 hipError_t launch_bwd_gemm(const Dims& d, const ProjBuffers& p, const BwdBuffers& g, const _Float16* X, _Float16* dX,
                            hipStream_t s);
 hipError_t launch_dw_reduce(const Dims& d, const BwdBuffers& g, const _Float16* gate_q, const _Float16* gate_k,

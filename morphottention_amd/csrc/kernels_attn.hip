@@ -517,13 +517,13 @@ hipError_t launch_attn_fwd(const Dims& d, const ProjBuffers& p, f16* out, float*
 // dO and of O; consecutive lane groups take consecutive tokens of one head, so
 // the per-row lse / tstat reads and aug writes are contiguous too, and a wave
 // reads whole 128-byte row pieces of dO and O. The partial dot products meet
-// in xor shuffles. The same grid zeroes the dq accumulator.
+// in xor shuffles. The same grid zeroes the dq and row-sum accumulators.
 template <int M, int DV>
 __global__ __launch_bounds__(256) void bwd_prep_kernel(const f16* __restrict__ grad_out, const f16* __restrict__ out,
                                                        const float* __restrict__ lse,
                                                        const float4* __restrict__ tstat, f16* __restrict__ aug,
                                                        f16* __restrict__ qa, int write_q, float* __restrict__ dq,
-                                                       int64_t T, int N, int H, int D) {
+                                                       float* __restrict__ dr, int64_t T, int N, int H, int D) {
   constexpr int G = DV / 8;  // lanes per (head, token): 4, 8 or 16, aligned within the wave
   constexpr int CW = 2 * M + 8;
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -553,10 +553,11 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(const f16* __restrict__ g
       *reinterpret_cast<f16x2*>(qa + bhn * CW + M + 2) = f16x2{lh, ll};
     }
   }
-  // zero dq: T * H * M floats, M / 4 float4 per (token, head)
+  // zero dq: T * H * M floats, M / 4 float4 per (token, head); and dr: T * H floats
   float4* z = reinterpret_cast<float4*>(dq);
   const int64_t nz = T * H * (M / 4);
   for (int64_t i = idx; i < nz; i += (int64_t)gridDim.x * 256) z[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int64_t i = idx; i < T * H; i += (int64_t)gridDim.x * 256) dr[i] = 0.f;
 }
 
 template <int M, int DV>
@@ -564,7 +565,7 @@ static hipError_t launch_bwd_prep_t(const Dims& d, const ProjBuffers& p, const f
                                     const float* lse, const BwdBuffers& g, int write_q, hipStream_t s) {
   const int64_t n = d.T * (d.D / 8);
   hipLaunchKernelGGL((bwd_prep_kernel<M, DV>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, grad_out, out, lse,
-                     p.tstat, g.aug, p.qa, write_q, g.dq, d.T, d.N, d.H, d.D);
+                     p.tstat, g.aug, p.qa, write_q, g.dq, g.dr, d.T, d.N, d.H, d.D);
   return hipGetLastError();
 }
 
@@ -657,9 +658,10 @@ struct BwdCfg {
 //   tiles of step s + 1, read the dq fragments of step s - 1, compute step s
 //   (S, dP, P, dS, dV += dO^T P, dk^T += phi^T dS, dS^T -> LDS), then finish
 //   dq of step s - 1 (MFMA over the workgroup's keys, fp32 atomics).
-// Every wave issues exactly 4 DQT atomics per step (masked lanes add 0.0 to a
-// valid address), so the tile wait can leave the latest step's atomics in
-// flight: vector-memory operations complete in issue order.
+// Every wave issues exactly 4 DQT + 1 atomics per step (masked lanes add 0.0 to
+// a valid address), so the tile wait can leave the latest step's atomics in
+// flight: vector-memory operations complete in issue order. The extra one
+// adds the step's row sums of dS (over the workgroup's keys) to dr.
 // The query rows come from the projection's code rows, whose affine block
 // holds {1, 1, -(lse - b)} by now (written by the forward, or by bwd_prep when
 // the backward computed the projection itself); the dO rows come from
@@ -669,8 +671,8 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ q
                                                        const f16* __restrict__ vt, const f16* __restrict__ aug,
                                                        const f16* __restrict__ grad_out, float* __restrict__ dq,
                                                        float* __restrict__ dk, float* __restrict__ dcb,
-                                                       f16* __restrict__ dzv, int N, int NP, int H, int D, int HM, int BH,
-                                                       int causal) {
+                                                       float* __restrict__ dr, f16* __restrict__ dzv, int N, int NP,
+                                                       int H, int D, int HM, int BH, int causal) {
   using C = BwdCfg<M, DV>;
   __shared__ __align__(16) char stg[2 * C::STAGE];
   __shared__ __align__(16) char sdS[2][C::KW * C::SRB];  // dS^T of the whole workgroup: row = key
@@ -868,10 +870,34 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ q
     const int qt = tile % (C::QT / 16), ct = tile / (C::QT / 16);
     a_off[t] = (16 * qt + 4 * (lane >> 4)) * M + 16 * ct + (lane & 15);
   }
+  // Row sums sum_j dS[q][j] over the workgroup's keys come from the A
+  // fragments of the tile (qt, ct = 0), tile w of the wave that owns it (all
+  // waves when M <= 32; waves 0 and 1 when M = 64, QT = 32): each lane sums its
+  // 8 values per key chunk (fp32 dot with ones), the four lane groups meet in
+  // xor shuffles, and lanes 0..15 add their query row's sum to dr. The other
+  // waves add 0 there, so every wave issues one such atomic per step.
+  const bool rs_wave = w / (C::QT / 16) == 0;  // uniform
+  const int rs_row = 16 * (w % (C::QT / 16)) + (lane & 15);
   auto dq_finish = [&](int st) {
     const int qs = qstart + st * C::QT;
     float* base = dq + (rowbase + qs) * M;
     const bool full = qs + C::QT <= N;  // uniform
+    {
+      float rsum = 0.f;
+      if (rs_wave) {
+        const f16x2 one2 = {(f16)1.f, (f16)1.f};
+#pragma unroll
+        for (int kc = 0; kc < C::KW / 32; ++kc)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            rsum = __builtin_amdgcn_fdot2(f16x2{dqa[0][kc][2 * i], dqa[0][kc][2 * i + 1]}, one2, rsum, false);
+        rsum += __shfl_xor(rsum, 16);
+        rsum += __shfl_xor(rsum, 32);
+      }
+      const int qq = qs + rs_row;
+      const bool ok = rs_wave && qq < N;
+      if (lane < 16) unsafeAtomicAdd(dr + rowbase + (qq < N ? qq : N - 1), ok ? rsum : 0.f);
+    }
 #pragma unroll
     for (int t = 0; t < C::DQT; ++t) {
       const int tile = w + 4 * t;
@@ -902,7 +928,7 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ q
     // this step's tiles have landed (the atomics of step - 2, issued after
     // them, may still be in flight) and this wave's dS^T writes are done
     if (step >= 2)
-      wait_vmcnt_lgkm0<4 * C::DQT>();
+      wait_vmcnt_lgkm0<4 * C::DQT + 1>();
     else
       wait_vmcnt_lgkm0<0>();
     __builtin_amdgcn_s_barrier();
@@ -983,7 +1009,7 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ q
   }
   if (step < nsteps) do_step(std::integral_constant<int, 0>{}, step);
   if (nsteps > 0) {
-    wait_vmcnt_lgkm0<4 * C::DQT>();
+    wait_vmcnt_lgkm0<4 * C::DQT + 1>();
     __builtin_amdgcn_s_barrier();  // dS^T of the last step from every wave
     dq_load(sdS[(nsteps - 1) & 1]);
     dq_finish(nsteps - 1);
@@ -1020,10 +1046,10 @@ static hipError_t launch_attn_bwd_t(const Dims& d, const ProjBuffers& p, const f
   const dim3 grid(xcd_grid((d.N + C::KW - 1) / C::KW, d.B * d.H));
   if (d.mask_diag)
     hipLaunchKernelGGL((attn_bwd_kernel<M, DV, true>), grid, dim3(256), 0, s, p.qa, p.ka, p.vt, g.aug, grad_out, g.dq,
-                       g.dk, g.dcb, g.dzv, d.N, d.NP, d.H, d.D, d.HM, d.B * d.H, d.causal);
+                       g.dk, g.dcb, g.dr, g.dzv, d.N, d.NP, d.H, d.D, d.HM, d.B * d.H, d.causal);
   else
     hipLaunchKernelGGL((attn_bwd_kernel<M, DV, false>), grid, dim3(256), 0, s, p.qa, p.ka, p.vt, g.aug, grad_out, g.dq,
-                       g.dk, g.dcb, g.dzv, d.N, d.NP, d.H, d.D, d.HM, d.B * d.H, d.causal);
+                       g.dk, g.dcb, g.dr, g.dzv, d.N, d.NP, d.H, d.D, d.HM, d.B * d.H, d.causal);
   return hipGetLastError();
 }
 

@@ -203,7 +203,7 @@ __global__ __launch_bounds__(kGemmThreads) void proj_fwd_kernel(const f16* __res
       const f16 one = (f16)1.f, zero = (f16)0.f;
       *reinterpret_cast<f16x8*>(qrow + M) = f16x8{one, one, rh, rl, zero, zero, zero, zero};
       *reinterpret_cast<f16x8*>(krow + M) = f16x8{bh_, bl_, one, one, zero, zero, zero, zero};
-      p.tstat[bhn] = make_float4(bias, R, gap, 0.f);
+      p.tstat[bhn] = make_float4(bias, R, gap, t_ii);
     }
     // values, transposed: vt[bh][dd][n] = V_hi, and the remainder V - V_hi as
     // e4m3 in vlo's tile-major, key-permuted rows. One item = one column x 8
@@ -296,13 +296,25 @@ hipError_t launch_proj_fwd(const Dims& d, const f16* X, const f16* gq, const f16
 
 // ---------------------------------------------------------------- backward elementwise
 // The output depends on the gates only through G = gate_q * gate_k, and with
-// dq = sum_j dS_ij phi_j, dk = sum_i dS_ij phi_i, dcb = sum_i dS_ij (natural-log
-// score gradients, ungated codes):
-//   dL/dphi_tc = scale G_c (2 (dq_tc + dk_tc) - dcb_t)
+// dq = sum_j dS_ij phi_j, dk = sum_i dS_ij phi_i, dcb = sum_i dS_ij, r =
+// sum_j dS_ij (natural-log score gradients, ungated codes):
+//   dL/dphi_tc = scale G_c (2 (dq_tc + dk_tc) - dcb_t - r_t)
 //   dL/dG_c    = scale sum_t phi_tc (2 dk_tc - dcb_t)
-// (both use sum_j dS_ij = 0). dL/dG is taken from the key-side sums only, whose
-// terms share the same rounded dS, so its cancellation stays exact; then
-// d gate_q = dL/dG gate_k and d gate_k = dL/dG gate_q.
+// (the gate sum uses sum_j dS_ij = 0). dL/dG is taken from the key-side sums
+// only, whose terms share the same rounded dS, so its cancellation stays
+// exact; then d gate_q = dL/dG gate_k and d gate_k = dL/dG gate_q.
+//
+// Diagonal correction (softmax attention, diagonal key present). The row sum
+// r_t of the rounded dS is 0 in exact arithmetic; what the kernels measure is
+// the error of the row's delta: an offset nu in delta makes dS_tj wrong by
+// -nu P_tj, so r_t = -nu sum_j P_tj. Where the row is concentrated on its
+// diagonal (saturated codes: the other weights are tiny and so is the true
+// gradient) that offset, however small (fp32 rounding of dO . O suffices),
+// dominates the code gradients. Replacing dS_tt by dS_tt - r_t P_tt cancels
+// it: dq, dk and dcb of token t lose c = r_t P_tt times the diagonal's
+// operands (phi_hi of t, the codes both products used, and 1), and the row
+// sum becomes r_t - c. P_tt = 2^(s_tt - lse_t) with s_tt = t_tt + b_t from
+// the projection's statistics.
 // A block covers kGateTokensPerBlock tokens and 256 projection columns. Each
 // thread owns 8 consecutive columns (one head) and every 8th token of the
 // block, so all loads and stores are 16-byte vectors: a wave covers 32
@@ -311,7 +323,7 @@ hipError_t launch_proj_fwd(const Dims& d, const f16* X, const f16* gq, const f16
 // fixed order.
 __global__ __launch_bounds__(256) void proj_bwd_elem_kernel(const f16* __restrict__ gate_q,
                                                             const f16* __restrict__ gate_k, Dims d, ProjBuffers p,
-                                                            BwdBuffers g) {
+                                                            BwdBuffers g, const float* __restrict__ lse) {
   __shared__ float red[8][257];
   const int c8 = threadIdx.x & 31, sub = threadIdx.x >> 5;
   const int col = blockIdx.y * 256 + 8 * c8;  // first of this thread's 8 columns
@@ -338,14 +350,26 @@ __global__ __launch_bounds__(256) void proj_bwd_elem_kernel(const f16* __restric
       const float4 q0 = dqp[0], q1 = dqp[1], k0 = dkp[0], k1 = dkp[1];
       const float dq[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
       const float dk[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
-      const float dcb = g.dcb[bhn];
+      float dcb = g.dcb[bhn], rs = 0.f, c = 0.f;
+      if (lse) {  // uniform
+        rs = g.dr[bhn];
+        const float l = lse[bhn];
+        if (!d.mask_diag && l > -kFltMax) {
+          const float4 ts = p.tstat[bhn];
+          c = rs * fast_exp2(ts.w + ts.x - l);
+        }
+        dcb -= c;
+        rs -= c;
+      }
       f16x8 dz;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float phi = (float)ph[e] + (float)pl[e];
-        const float dphi = sG[e] * (2.f * (dq[e] + dk[e]) - dcb);
+        const float cp = c * (float)ph[e];
+        const float dqe = dq[e] - cp, dke = dk[e] - cp;
+        const float dphi = sG[e] * (2.f * (dqe + dke) - dcb - rs);
         dz[e] = (f16)(dphi * cube_project_grad(phi, d.proj));
-        sg[e] += phi * (2.f * dk[e] - dcb);
+        sg[e] += phi * (2.f * dke - dcb);
       }
       *reinterpret_cast<f16x8*>(g.dzv + t * NC + col) = dz;
     }
@@ -363,9 +387,9 @@ __global__ __launch_bounds__(256) void proj_bwd_elem_kernel(const f16* __restric
 }
 
 hipError_t launch_proj_bwd_elem(const Dims& d, const f16* gq, const f16* gk, const ProjBuffers& p,
-                                const BwdBuffers& g, hipStream_t s) {
+                                const BwdBuffers& g, const float* lse, hipStream_t s) {
   dim3 grid((unsigned)((d.T + kGateTokensPerBlock - 1) / kGateTokensPerBlock), (d.HM + 255) / 256);
-  hipLaunchKernelGGL(proj_bwd_elem_kernel, grid, dim3(256), 0, s, gq, gk, d, p, g);
+  hipLaunchKernelGGL(proj_bwd_elem_kernel, grid, dim3(256), 0, s, gq, gk, d, p, g, lse);
   return hipGetLastError();
 }
 

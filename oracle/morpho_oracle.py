@@ -178,7 +178,7 @@ def morpho_attention_ref_grads(x, W_phi, gate_q, gate_k, W_V, num_heads: int, cu
                                scale: float = 1.0, causal: bool = False, dout=None,
                                dtype=torch.float32, batch_chunk: int | None = None,
                                head_chunk: int | None = None, projection: str = "sigmoid",
-                               mask_diag: bool = False):
+                               mask_diag: bool = False, heads: tuple[int, int] | None = None):
     """Forward + autograd backward of the restatement, chunked over batch and heads.
 
     Inputs are upcast to ``dtype``. ``dout`` defaults to ones (i.e. the
@@ -188,6 +188,10 @@ def morpho_attention_ref_grads(x, W_phi, gate_q, gate_k, W_V, num_heads: int, cu
     sum of their separate contributions to ``dX``, and the loss
     ``sum(out * dout)`` is a sum over (batch, head) blocks, so the gradients of
     the chunks add up to the full gradient.
+
+    ``heads = (h0, h1)`` evaluates only heads ``h0 .. h1-1``: their output
+    columns, ``lse`` rows and parameter-gradient slices are exact, everything
+    else is left zero (``dX`` then holds only these heads' share).
     """
     B, N, D = x.shape
     H, m = num_heads, cube_m
@@ -195,16 +199,17 @@ def morpho_attention_ref_grads(x, W_phi, gate_q, gate_k, W_V, num_heads: int, cu
     bc = batch_chunk or B
     hc = head_chunk or H
     params = [p.detach().to(dtype).clone().requires_grad_(True) for p in (W_phi, gate_q, gate_k, W_V)]
-    out = torch.empty(B, N, D, dtype=dtype, device=x.device)
-    lse = torch.empty(B, H, N, dtype=dtype, device=x.device)
+    out = torch.zeros(B, N, D, dtype=dtype, device=x.device)
+    lse = torch.zeros(B, H, N, dtype=dtype, device=x.device)
     dX = torch.zeros(B, N, D, dtype=dtype, device=x.device)
     for b0 in range(0, B, bc):
         b1 = min(B, b0 + bc)
         xb = x[b0:b1].detach().to(dtype).clone().requires_grad_(True)
         g_full = torch.ones(b1 - b0, N, D, dtype=dtype, device=x.device) if dout is None \
             else dout[b0:b1].to(dtype)
-        for h0 in range(0, H, hc):
-            h1 = min(H, h0 + hc)
+        hlo, hhi = heads if heads is not None else (0, H)
+        for h0 in range(hlo, hhi, hc):
+            h1 = min(hhi, h0 + hc)
             o, l = morpho_attention_ref(xb, params[0][:, h0 * m:h1 * m], params[1][h0:h1], params[2][h0:h1],
                                         params[3][:, h0 * dv:h1 * dv], h1 - h0, m,
                                         scale=scale, causal=causal, return_lse=True,

@@ -188,6 +188,27 @@ def test_batch_chunking_is_exact():
         assert torch.allclose(t.grad, gb, atol=1e-13)
 
 
+def test_head_range_gives_exact_slices():
+    """``heads=(h0, h1)`` evaluates only those heads: their output columns, lse
+    rows and parameter-gradient slices equal the full evaluation's, the rest is
+    zero (the GPU parity suite uses it for an fp64 reference of a head subset)."""
+    H, m, D = 4, 4, 16
+    dv = D // H
+    x, W_phi, gq, gk, W_V = _inputs(2, 7, D, H, m, seed=13)
+    full = mo.morpho_attention_ref_grads(x, W_phi, gq, gk, W_V, H, m, causal=True, dtype=torch.float64)
+    part = mo.morpho_attention_ref_grads(x, W_phi, gq, gk, W_V, H, m, causal=True, dtype=torch.float64,
+                                         head_chunk=1, heads=(1, 3))
+    sel_m, sel_v = slice(1 * m, 3 * m), slice(1 * dv, 3 * dv)
+    assert torch.allclose(part[0][..., sel_v], full[0][..., sel_v], atol=1e-14)
+    assert part[0][..., :dv].abs().max() == 0 and part[0][..., 3 * dv:].abs().max() == 0
+    assert torch.allclose(part[1].view(2, H, 7)[:, 1:3], full[1].view(2, H, 7)[:, 1:3], atol=1e-13)
+    assert torch.allclose(part[2][1][:, sel_m], full[2][1][:, sel_m], atol=1e-13)
+    assert torch.allclose(part[2][2][1:3], full[2][2][1:3], atol=1e-13)
+    assert torch.allclose(part[2][3][1:3], full[2][3][1:3], atol=1e-13)
+    assert torch.allclose(part[2][4][:, sel_v], full[2][4][:, sel_v], atol=1e-13)
+    assert part[2][1][:, :m].abs().max() == 0 and part[2][2][0].abs().max() == 0
+
+
 def test_default_init_matches_module_protocol():
     """RNG order W_phi then W_V, N(0, dim^-0.5) in fp32, gates ones."""
     torch.manual_seed(0)
