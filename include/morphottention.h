@@ -93,6 +93,29 @@ int morpho_forward(const void* X, const void* W_phi, const void* gate_q, const v
                    void* out, float* lse, int64_t B, int64_t N, int64_t D, int64_t H, int64_t cube_m, float scale,
                    int causal, void* workspace, size_t workspace_bytes, morpho_stream_t stream);
 
+/* Bytes of device memory inside the library used by morpho_forward_noalloc,
+ * per GPU. */
+#define MORPHO_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+
+/* Allocation-free forward. No counterpart in the reference: for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). Same arguments, kernels and
+ * results as morpho_forward, without the workspace: the library's own static
+ * device array of MORPHO_NOALLOC_SCRATCH_BYTES serves as the workspace (one
+ * per GPU, held from the library's first use on that GPU until the process
+ * ends). Problems whose forward workspace (morpho_forward_workspace_size)
+ * exceeds it are rejected with MORPHO_ERR_WORKSPACE before anything runs; at
+ * cube_m = 16 and D / H = 64 that is up to about 90,000 (token, head) pairs,
+ * fewer as the weights grow with D: B = 1, N = 4096, D = 1024, H = 16 needs
+ * 28 MiB. Every call on a GPU shares that GPU's
+ * array: calls that overlap in time on one GPU (unordered streams or
+ * threads) race, and the array is not a forward workspace that a later
+ * morpho_backward may be given (pass NULL there to recompute). Nothing is
+ * allocated or freed. */
+int morpho_forward_noalloc(const void* X, const void* W_phi, const void* gate_q, const void* gate_k,
+                           const void* W_V, void* out, float* lse, int64_t B, int64_t N, int64_t D, int64_t H,
+                           int64_t cube_m, float scale, int causal, morpho_stream_t stream);
+
 /* Bytes of device workspace morpho_backward needs. With `have_forward_workspace`
  * = 0 this includes room to recompute the projection. */
 size_t morpho_backward_workspace_size(int64_t B, int64_t N, int64_t D, int64_t H, int64_t cube_m,

@@ -34,6 +34,8 @@ def lib() -> ctypes.CDLL:
         L.morpho_backward_workspace_size.argtypes = [i64] * 5 + [ctypes.c_int]
         L.morpho_forward.restype = ctypes.c_int
         L.morpho_forward.argtypes = [vp] * 5 + [vp, vp] + [i64] * 5 + [ctypes.c_float, ctypes.c_int, vp, sz, vp]
+        L.morpho_forward_noalloc.restype = ctypes.c_int
+        L.morpho_forward_noalloc.argtypes = [vp] * 5 + [vp, vp] + [i64] * 5 + [ctypes.c_float, ctypes.c_int, vp]
         L.morpho_backward.restype = ctypes.c_int
         L.morpho_backward.argtypes = ([vp] * 8 + [vp] * 5 + [i64] * 5 + [ctypes.c_float, ctypes.c_int]
                                       + [vp, vp, sz, vp])

@@ -261,6 +261,60 @@ MORPHO_EXPORT int morpho_forward(const void* X, const void* W_phi, const void* g
   return MORPHO_OK;
 }
 
+// ---------------------------------------------------------------- allocation-free forward
+namespace {
+// The workspace of morpho_forward_noalloc: one array per GPU the library is
+// loaded on, held until the process ends. Its host-side name is not a device
+// address; host code uses only the per-device address that
+// hipGetSymbolAddress returns (scratch_for_current_device).
+__attribute__((used)) static __device__ __align__(256) unsigned char scratch[MORPHO_NOALLOC_SCRATCH_BYTES];
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices] = {};  // guarded by g_scratch_mu
+
+// This device's address of `scratch`, looked up on the first call with the
+// device current and kept per device.
+int scratch_for_current_device(void** ptr) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(MORPHO_ERR_HIP, "hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxScratchDevices)
+    return fail(MORPHO_ERR_UNSUPPORTED, "device index %d beyond the %d this build keeps scratch for", dev,
+                kMaxScratchDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(MORPHO_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return MORPHO_OK;
+}
+}  // namespace
+
+MORPHO_EXPORT int morpho_forward_noalloc(const void* X, const void* W_phi, const void* gate_q, const void* gate_k,
+                                         const void* W_V, void* out, float* lse, int64_t B, int64_t N, int64_t D,
+                                         int64_t H, int64_t cube_m, float scale, int causal, morpho_stream_t stream) {
+  g_last_error.clear();
+  Dims d;
+  int st = make_dims(B, N, D, H, cube_m, scale, causal, d);
+  if (st != MORPHO_OK) return st;
+  const size_t need = proj_bytes(d);
+  if (need > MORPHO_NOALLOC_SCRATCH_BYTES)
+    return fail(MORPHO_ERR_WORKSPACE,
+                "morpho_forward_noalloc: this problem needs %zu bytes of scratch, more than the library's %zu; "
+                "use morpho_forward with a workspace",
+                need, (size_t)MORPHO_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if ((st = scratch_for_current_device(&ws)) != MORPHO_OK) return st;
+  // the same kernels as morpho_forward; every byte of the workspace they read
+  // is written earlier in the same call, so nothing needs clearing
+  return morpho_forward(X, W_phi, gate_q, gate_k, W_V, out, lse, B, N, D, H, cube_m, scale, causal, ws,
+                        MORPHO_NOALLOC_SCRATCH_BYTES, stream);
+}
+
 MORPHO_EXPORT int morpho_backward(const void* grad_out, const void* X, const void* W_phi, const void* gate_q,
                                   const void* gate_k, const void* W_V, const void* out, const float* lse, void* dX,
                                   void* dW_phi, void* d_gate_q, void* d_gate_k, void* dW_V, int64_t B, int64_t N,
