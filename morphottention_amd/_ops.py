@@ -25,8 +25,8 @@ def _load_c_extension() -> str:
             torch.ops.load_library(matches[0])
             return matches[0]
     raise ImportError(
-        f"Could not find the compiled morphottention '_C' extension in {pkg_dir}. "
-        "Build it with `python morphottention_amd/build.py` (hipcc, gfx950)."
+        f"morphottention_amd: no built '_C' extension in {pkg_dir}; "
+        "build it with `python morphottention_amd/build.py` (hipcc, gfx950)"
     )
 
 

@@ -126,6 +126,25 @@ def test_fake_kernels():
         assert [t.shape for t in grads] == [X.shape, W.shape, g.shape, g.shape, V.shape]
 
 
+def test_reference_import_path():
+    """The reference's import line works unchanged
+    (torch-ext/morphottention/__init__.py:1-3; attn-bench's morpho_attention.py:7),
+    with the same public names and submodules, and resolves to this build."""
+    import morphottention
+    from morphottention import MorphoAttention, MorphoAttentionFunction, morpho_attention
+    from morphottention._ops import add_op_namespace_prefix, ops
+    import morphottention_amd
+    assert morphottention.__all__ == ["MorphoAttention", "MorphoAttentionFunction", "morpho_attention"]
+    assert MorphoAttention is morphottention_amd.MorphoAttention
+    assert MorphoAttentionFunction is morphottention_amd.MorphoAttentionFunction
+    assert morpho_attention is morphottention_amd.morpho_attention
+    assert morphottention.autograd.MorphoAttention is MorphoAttention
+    assert ops is torch.ops.morphottention and add_op_namespace_prefix("forward") == "morphottention::forward"
+    mod = MorphoAttention(64, 2, 16, dtype=torch.float16, device="cpu")
+    with pytest.raises(ValueError, match="CUDA tensor"):
+        mod(torch.randn(1, 4, 64, dtype=torch.float16))
+
+
 def test_module_construction_and_init_protocol():
     from morphottention_amd import MorphoAttention
     torch.manual_seed(0)

@@ -49,7 +49,7 @@ def half_ulp(x: torch.Tensor) -> torch.Tensor:
 
 
 def run_hip(x, params, H, m, scale, causal, dout):
-    from morphottention_amd import morpho_attention
+    from morphottention import morpho_attention  # the reference's import path
     leaves = [t.detach().clone().requires_grad_(True) for t in (x, *params)]
     out = morpho_attention(leaves[0], *leaves[1:], H, m, scale=scale, causal=causal)
     out.backward(dout)
