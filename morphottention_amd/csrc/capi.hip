@@ -138,7 +138,7 @@ size_t bwd_bytes(const Dims& d) {
   s += align_up(bhn * d.M * 4);                        // dq
   s += align_up(bhn * d.M * 4);                        // dk
   s += align_up(bhn * 4);                              // dcb
-  s += align_up(bhn * 4);                              // dr
+  s += align_up(bhn * 8);                              // dr
   s += align_up((size_t)d.T * (d.HM + d.D) * 2);       // dzv
   s += align_up(nblk * d.HM * 4);                      // gpart
   s += align_up((size_t)dw_splits(d) * d.D * (d.HM + d.D) * 4);  // wpart
@@ -154,7 +154,7 @@ BwdBuffers carve_bwd(void* base, const Dims& d) {
   g.dq = reinterpret_cast<float*>(p); p += align_up(bhn * d.M * 4);
   g.dk = reinterpret_cast<float*>(p); p += align_up(bhn * d.M * 4);
   g.dcb = reinterpret_cast<float*>(p); p += align_up(bhn * 4);
-  g.dr = reinterpret_cast<float*>(p); p += align_up(bhn * 4);
+  g.dr = reinterpret_cast<float*>(p); p += align_up(bhn * 8);
   g.dzv = reinterpret_cast<_Float16*>(p); p += align_up((size_t)d.T * (d.HM + d.D) * 2);
   g.gpart = reinterpret_cast<float*>(p); p += align_up(nblk * d.HM * 4);
   g.wpart = reinterpret_cast<float*>(p);
@@ -356,7 +356,7 @@ MORPHO_EXPORT int morpho_backward(const void* grad_out, const void* X, const voi
   MORPHO_LAUNCH("bwd_prep", launch_bwd_prep(d, p, go, static_cast<const _Float16*>(out), lse, g, have_fwd ? 0 : 1, s));
   MORPHO_LAUNCH("attn_bwd", launch_attn_bwd(d, p, go, g, s));
   MORPHO_LAUNCH("proj_bwd_elem", launch_proj_bwd_elem(d, static_cast<const _Float16*>(gate_q),
-                                                      static_cast<const _Float16*>(gate_k), p, g, lse, s));
+                                                      static_cast<const _Float16*>(gate_k), p, g, true, s));
   MORPHO_LAUNCH("bwd_gemm", launch_bwd_gemm(d, p, g, static_cast<const _Float16*>(X), static_cast<_Float16*>(dX), s));
   MORPHO_LAUNCH("dw_reduce", launch_dw_reduce(d, g, static_cast<const _Float16*>(gate_q),
                                               static_cast<const _Float16*>(gate_k), static_cast<_Float16*>(dW_phi),
@@ -515,7 +515,7 @@ MORPHO_EXPORT int morpho_soft_backward(const void* grad_out, const void* X, cons
     MORPHO_LAUNCH("soft_part_clear", launch_fill_zero(fast_part, 2 * (soft_bwd_slots(d) - soft_bwd_exact_slots(d)), s));
   }
   MORPHO_LAUNCH("proj_bwd_elem", launch_proj_bwd_elem(d, static_cast<const _Float16*>(gate_q),
-                                                      static_cast<const _Float16*>(gate_k), p, g, nullptr, s));
+                                                      static_cast<const _Float16*>(gate_k), p, g, false, s));
   MORPHO_LAUNCH("bwd_gemm", launch_bwd_gemm(d, p, g, static_cast<const _Float16*>(X), static_cast<_Float16*>(dX), s));
   MORPHO_LAUNCH("dw_reduce", launch_dw_reduce(d, g, static_cast<const _Float16*>(gate_q),
                                               static_cast<const _Float16*>(gate_k), static_cast<_Float16*>(dW_phi),

@@ -83,8 +83,9 @@ struct BwdBuffers {
   float* dq;       // [B*H, N, M] sum_j dS_ij phi_j (query side), fp32 atomics
   float* dk;       // [B*H, N, M] sum_i dS_ij phi_i (key side)
   float* dcb;      // [B*H, N]    sum_i dS_ij
-  float* dr;       // [B*H, N]    sum_j dS_ij, the row sums of the rounded dS (0 in exact
-                   //             arithmetic), fp32 atomics
+  float* dr;       // [B*H, N, 2] {r, P_ii}: r = sum_j dS_ij, the row sums of the rounded dS (0 in
+                   //             exact arithmetic, fp32 atomics), and the diagonal weight
+                   //             P_ii (0 when the diagonal is masked), written by bwd_prep
   _Float16* dzv;   // [T, H*M + D] dZ | dV
   float* gpart;    // [n_gate_blocks, H*M] partial sums of phi (2 dk - dcb), the gate factor dG
   float* wpart;    // [splits, D, H*M + D] split-K partials of [dW_phi | dW_V]
@@ -98,11 +99,11 @@ hipError_t launch_transpose_weights(const Dims& d, const _Float16* W_phi, const 
                                     _Float16* wcat, hipStream_t s);
 hipError_t launch_proj_fwd(const Dims& d, const _Float16* X, const _Float16* gate_q, const _Float16* gate_k,
                            const ProjBuffers& p, hipStream_t s);
-// With lse non-null (softmax attention) the row sums g.dr are used to cancel
-// the noise of the rows' delta at the diagonal; null (soft aggregation) uses
-// dq, dk and dcb as they are.
+// With row_corr (softmax attention) the row sums and diagonal weights in g.dr
+// cancel the noise of the rows' delta at the diagonal; without (soft
+// aggregation) dq, dk and dcb are used as they are.
 hipError_t launch_proj_bwd_elem(const Dims& d, const _Float16* gate_q, const _Float16* gate_k, const ProjBuffers& p,
-                                const BwdBuffers& g, const float* lse, hipStream_t s);
+                                const BwdBuffers& g, bool row_corr, hipStream_t s);
 hipError_t launch_bwd_gemm(const Dims& d, const ProjBuffers& p, const BwdBuffers& g, const _Float16* X, _Float16* dX,
                            hipStream_t s);
 hipError_t launch_dw_reduce(const Dims& d, const BwdBuffers& g, const _Float16* gate_q, const _Float16* gate_k,

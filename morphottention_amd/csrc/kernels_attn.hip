@@ -523,7 +523,8 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(const f16* __restrict__ g
                                                        const float* __restrict__ lse,
                                                        const float4* __restrict__ tstat, f16* __restrict__ aug,
                                                        f16* __restrict__ qa, int write_q, float* __restrict__ dq,
-                                                       float* __restrict__ dr, int64_t T, int N, int H, int D) {
+                                                       float2* __restrict__ dr, int diag, int64_t T, int N, int H,
+                                                       int D) {
   constexpr int G = DV / 8;  // lanes per (head, token): 4, 8 or 16, aligned within the wave
   constexpr int CW = 2 * M + 8;
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -546,18 +547,21 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(const f16* __restrict__ g
     split_hi_lo(-delta, dh, dl);
     const f16 zero = (f16)0.f;
     *reinterpret_cast<f16x8*>(aug + bhn * 8) = f16x8{dh, dl, zero, zero, zero, zero, zero, zero};
+    const float l = lse[bhn];
+    const float4 ts = tstat[bhn];
     if (write_q) {
       f16 lh, ll;
-      const float l = lse[bhn];
-      split_hi_lo(l > -kFltMax ? -(l - tstat[bhn].x) : 0.f, lh, ll);  // a row without keys: masked anyway
+      split_hi_lo(l > -kFltMax ? -(l - ts.x) : 0.f, lh, ll);  // a row without keys: masked anyway
       *reinterpret_cast<f16x2*>(qa + bhn * CW + M + 2) = f16x2{lh, ll};
     }
+    // the row-sum accumulator (zero) and the diagonal weight P_ii = 2^(s_ii - lse)
+    // with s_ii = t + b (0 when the diagonal is masked or the row has no keys)
+    dr[bhn] = make_float2(0.f, diag && l > -kFltMax ? fast_exp2(ts.w + ts.x - l) : 0.f);
   }
-  // zero dq: T * H * M floats, M / 4 float4 per (token, head); and dr: T * H floats
+  // zero dq: T * H * M floats, M / 4 float4 per (token, head)
   float4* z = reinterpret_cast<float4*>(dq);
   const int64_t nz = T * H * (M / 4);
   for (int64_t i = idx; i < nz; i += (int64_t)gridDim.x * 256) z[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int64_t i = idx; i < T * H; i += (int64_t)gridDim.x * 256) dr[i] = 0.f;
 }
 
 template <int M, int DV>
@@ -565,7 +569,8 @@ static hipError_t launch_bwd_prep_t(const Dims& d, const ProjBuffers& p, const f
                                     const float* lse, const BwdBuffers& g, int write_q, hipStream_t s) {
   const int64_t n = d.T * (d.D / 8);
   hipLaunchKernelGGL((bwd_prep_kernel<M, DV>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, grad_out, out, lse,
-                     p.tstat, g.aug, p.qa, write_q, g.dq, g.dr, d.T, d.N, d.H, d.D);
+                     p.tstat, g.aug, p.qa, write_q, g.dq, reinterpret_cast<float2*>(g.dr), d.mask_diag ? 0 : 1,
+                     d.T, d.N, d.H, d.D);
   return hipGetLastError();
 }
 
@@ -661,7 +666,7 @@ struct BwdCfg {
 // Every wave issues exactly 4 DQT + 1 atomics per step (masked lanes add 0.0 to
 // a valid address), so the tile wait can leave the latest step's atomics in
 // flight: vector-memory operations complete in issue order. The extra one
-// adds the step's row sums of dS (over the workgroup's keys) to dr.
+// adds the row sums of dS of step s - 1 (over the workgroup's keys) to dr.
 // The query rows come from the projection's code rows, whose affine block
 // holds {1, 1, -(lse - b)} by now (written by the forward, or by bwd_prep when
 // the backward computed the projection itself); the dO rows come from
@@ -870,34 +875,35 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ q
     const int qt = tile % (C::QT / 16), ct = tile / (C::QT / 16);
     a_off[t] = (16 * qt + 4 * (lane >> 4)) * M + 16 * ct + (lane & 15);
   }
-  // Row sums sum_j dS[q][j] over the workgroup's keys come from the A
-  // fragments of the tile (qt, ct = 0), tile w of the wave that owns it (all
-  // waves when M <= 32; waves 0 and 1 when M = 64, QT = 32): each lane sums its
-  // 8 values per key chunk (fp32 dot with ones), the four lane groups meet in
-  // xor shuffles, and lanes 0..15 add their query row's sum to dr. The other
+  // Row sums sum_j dS[q][j] over the workgroup's keys: the A fragments of the
+  // tile (qt, ct = 0) times a ones operand on the MFMA (tile w of the wave that
+  // owns it: all waves when M <= 32, waves 0 and 1 when M = 64, QT = 32). Every
+  // column of the 16 x 16 result holds the row sums; lanes with (lane & 15) < 4
+  // add rows 4 (lane / 16) + (lane & 3) to dr, one atomic per row. The other
   // waves add 0 there, so every wave issues one such atomic per step.
-  const bool rs_wave = w / (C::QT / 16) == 0;  // uniform
-  const int rs_row = 16 * (w % (C::QT / 16)) + (lane & 15);
+  const bool rs_wave = C::QT / 16 >= 4 || w < C::QT / 16;  // uniform
+  const int rs_row = 16 * (w % (C::QT / 16)) + 4 * (lane >> 4) + (lane & 3);
+  // issued right after the fragments of step st are read, so that it overlaps
+  // the next step's body
+  auto rowsum = [&](int st) {
+    const int qs = qstart + st * C::QT;
+    f32x4 racc = {};
+    if (rs_wave) {
+      const f16 one16 = (f16)1.f;
+      const f16x8 ones = {one16, one16, one16, one16, one16, one16, one16, one16};
+#pragma unroll
+      for (int kc = 0; kc < C::KW / 32; ++kc) racc = mfma16x16(dqa[0][kc], ones, racc);
+    }
+    const int j = lane & 3;
+    const float rsum = j == 0 ? racc[0] : j == 1 ? racc[1] : j == 2 ? racc[2] : racc[3];
+    const int qq = qs + rs_row;
+    if ((lane & 15) < 4)
+      unsafeAtomicAdd(&dr[2 * (rowbase + (qq < N ? qq : N - 1))], rs_wave && qq < N ? rsum : 0.f);
+  };
   auto dq_finish = [&](int st) {
     const int qs = qstart + st * C::QT;
     float* base = dq + (rowbase + qs) * M;
     const bool full = qs + C::QT <= N;  // uniform
-    {
-      float rsum = 0.f;
-      if (rs_wave) {
-        const f16x2 one2 = {(f16)1.f, (f16)1.f};
-#pragma unroll
-        for (int kc = 0; kc < C::KW / 32; ++kc)
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            rsum = __builtin_amdgcn_fdot2(f16x2{dqa[0][kc][2 * i], dqa[0][kc][2 * i + 1]}, one2, rsum, false);
-        rsum += __shfl_xor(rsum, 16);
-        rsum += __shfl_xor(rsum, 32);
-      }
-      const int qq = qs + rs_row;
-      const bool ok = rs_wave && qq < N;
-      if (lane < 16) unsafeAtomicAdd(dr + rowbase + (qq < N ? qq : N - 1), ok ? rsum : 0.f);
-    }
 #pragma unroll
     for (int t = 0; t < C::DQT; ++t) {
       const int tile = w + 4 * t;
@@ -933,7 +939,10 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ q
       wait_vmcnt_lgkm0<0>();
     __builtin_amdgcn_s_barrier();
     if (step + 1 < nsteps) issue(step + 1);  // its stage last served step - 1
-    if (step >= 1) dq_load(sdS[PAR ^ 1]);
+    if (step >= 1) {
+      dq_load(sdS[PAR ^ 1]);
+      rowsum(step - 1);
+    }
 
     const int qs = qstart + step * C::QT;
     const char* tQ = stg + PAR * C::STAGE;
@@ -1012,6 +1021,7 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ q
     wait_vmcnt_lgkm0<4 * C::DQT + 1>();
     __builtin_amdgcn_s_barrier();  // dS^T of the last step from every wave
     dq_load(sdS[(nsteps - 1) & 1]);
+    rowsum(nsteps - 1);
     dq_finish(nsteps - 1);
   }
 

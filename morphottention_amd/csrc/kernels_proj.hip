@@ -313,8 +313,8 @@ hipError_t launch_proj_fwd(const Dims& d, const f16* X, const f16* gq, const f16
 // dominates the code gradients. Replacing dS_tt by dS_tt - r_t P_tt cancels
 // it: dq, dk and dcb of token t lose c = r_t P_tt times the diagonal's
 // operands (phi_hi of t, the codes both products used, and 1), and the row
-// sum becomes r_t - c. P_tt = 2^(s_tt - lse_t) with s_tt = t_tt + b_t from
-// the projection's statistics.
+// sum becomes r_t - c. P_tt = 2^(s_tt - lse_t) (s_tt = t_tt + b_t from the
+// projection's statistics) comes from bwd_prep, next to r_t.
 // A block covers kGateTokensPerBlock tokens and 256 projection columns. Each
 // thread owns 8 consecutive columns (one head) and every 8th token of the
 // block, so all loads and stores are 16-byte vectors: a wave covers 32
@@ -323,7 +323,7 @@ hipError_t launch_proj_fwd(const Dims& d, const f16* X, const f16* gq, const f16
 // fixed order.
 __global__ __launch_bounds__(256) void proj_bwd_elem_kernel(const f16* __restrict__ gate_q,
                                                             const f16* __restrict__ gate_k, Dims d, ProjBuffers p,
-                                                            BwdBuffers g, const float* __restrict__ lse) {
+                                                            BwdBuffers g, int row_corr) {
   __shared__ float red[8][257];
   const int c8 = threadIdx.x & 31, sub = threadIdx.x >> 5;
   const int col = blockIdx.y * 256 + 8 * c8;  // first of this thread's 8 columns
@@ -350,22 +350,18 @@ __global__ __launch_bounds__(256) void proj_bwd_elem_kernel(const f16* __restric
       const float4 q0 = dqp[0], q1 = dqp[1], k0 = dkp[0], k1 = dkp[1];
       const float dq[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
       const float dk[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
-      float dcb = g.dcb[bhn], rs = 0.f, c = 0.f;
-      if (lse) {  // uniform
-        rs = g.dr[bhn];
-        const float l = lse[bhn];
-        if (!d.mask_diag && l > -kFltMax) {
-          const float4 ts = p.tstat[bhn];
-          c = rs * fast_exp2(ts.w + ts.x - l);
-        }
-        dcb -= c;
-        rs -= c;
+      float dcb = g.dcb[bhn], rs = 0.f, cr = 0.f;
+      if (row_corr) {  // uniform
+        const float2 rp = reinterpret_cast<const float2*>(g.dr)[bhn];  // {r, P_tt}
+        cr = rp.x * rp.y;
+        rs = rp.x - cr;
+        dcb -= cr;
       }
       f16x8 dz;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float phi = (float)ph[e] + (float)pl[e];
-        const float cp = c * (float)ph[e];
+        const float cp = cr * (float)ph[e];
         const float dqe = dq[e] - cp, dke = dk[e] - cp;
         const float dphi = sG[e] * (2.f * (dqe + dke) - dcb - rs);
         dz[e] = (f16)(dphi * cube_project_grad(phi, d.proj));
@@ -387,9 +383,9 @@ __global__ __launch_bounds__(256) void proj_bwd_elem_kernel(const f16* __restric
 }
 
 hipError_t launch_proj_bwd_elem(const Dims& d, const f16* gq, const f16* gk, const ProjBuffers& p,
-                                const BwdBuffers& g, const float* lse, hipStream_t s) {
+                                const BwdBuffers& g, bool row_corr, hipStream_t s) {
   dim3 grid((unsigned)((d.T + kGateTokensPerBlock - 1) / kGateTokensPerBlock), (d.HM + 255) / 256);
-  hipLaunchKernelGGL(proj_bwd_elem_kernel, grid, dim3(256), 0, s, gq, gk, d, p, g, lse);
+  hipLaunchKernelGGL(proj_bwd_elem_kernel, grid, dim3(256), 0, s, gq, gk, d, p, g, row_corr ? 1 : 0);
   return hipGetLastError();
 }
 
