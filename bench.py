@@ -32,9 +32,10 @@ CONFIGS = {
 }
 PEAK_FP16_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
 PEAK_HBM_GBS = 8000.0
-# v_exp_f32 throughput measured on the box: 128 exps x 64 lanes per 475 ns per
-# SIMD (two waves), x 1024 SIMDs
-PEAK_EXP_PER_S = 17.7e12
+# v_exp_f32 at quarter rate: 256 CUs x 16 lanes/clk x 2.4 GHz (BASELINE.md roofline constants)
+PEAK_EXP_PER_S = 9.8e12
+# the CPU reference configuration, timed in every run
+C1 = (2, 128, 256, 8, 16, 1.0, False, 0, 1.0)
 
 
 def log(*a):
@@ -85,17 +86,31 @@ def roofline_terms(flops, exps, nbytes):
     return bound, {k: round(v, 4) for k, v in t.items()}
 
 
-def make_inputs(cfg, device):
+def make_inputs(cfg, device, dtype=torch.float16):
+    """Synthetic inputs of a config (BASELINE protocol): default MorphoAttention
+    init on the CPU in fp32 then rounded to fp16, x ~ xm N(0,1) and dout ~
+    N(0,1) rounded to fp16. ``dtype`` float32 gives the same fp16 values upcast
+    (the CPU oracle's inputs), on the CPU."""
     from morphottention_amd import MorphoAttention
     B, N, D, H, m, scale, causal, seed, xm = cfg
     torch.manual_seed(seed)
     mod = MorphoAttention(D, H, m, scale=scale, causal=causal, dtype=torch.float16, device="cpu")
-    params = [p.detach().to(device).requires_grad_(True) for p in (mod.W_phi, mod.gate_q, mod.gate_k, mod.W_V)]
+    params = [p.detach().to(dtype).to(device).requires_grad_(True)
+              for p in (mod.W_phi, mod.gate_q, mod.gate_k, mod.W_V)]
     torch.manual_seed(seed)
-    x = (xm * torch.randn(B, N, D)).half().to(device).requires_grad_(True)
+    x = (xm * torch.randn(B, N, D)).half().to(dtype).to(device).requires_grad_(True)
     torch.manual_seed(seed + 1000)
-    dout = torch.randn(B, N, D).half().to(device)
+    dout = torch.randn(B, N, D).half().to(dtype).to(device)
     return x, params, dout
+
+
+def load_profile(kind, config):
+    """A committed rocprofv3 summary (profiles/<kind>_<config>.json), or None."""
+    try:
+        with open(os.path.join(ROOT, "profiles", f"{kind}_{config}.json")) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return None
 
 
 def load_traffic(kernel, config):
@@ -103,13 +118,22 @@ def load_traffic(kernel, config):
     (profiles/hbm_traffic_<config>.json: FETCH_SIZE and WRITE_SIZE per dispatch,
     each scaled by the same counter's reading for a plain copy of known size).
     Offline numbers: PMC passes cannot run inside this timed process."""
-    path = os.path.join(ROOT, "profiles", f"hbm_traffic_{config}.json")
+    data = load_profile("hbm_traffic", config)
     try:
-        with open(path) as f:
-            data = json.load(f)
         # the profiler names the device function, e.g. attn_bwd -> attn_bwd_kernel
         return data["kernels"][f"{kernel}_kernel"]["hbm_bytes_per_launch"]
-    except (OSError, KeyError, ValueError):
+    except (TypeError, KeyError):
+        return None
+
+
+def load_trace_avg(kernel, config):
+    """Mean duration (ms) of `kernel` over the timed steps of the committed
+    rocprofv3 kernel trace of this bench command
+    (profiles/kernel_trace_<config>.json), or None."""
+    data = load_profile("kernel_trace", config)
+    try:
+        return data["kernels"][f"{kernel}_kernel"]["timed_avg_us"] / 1e3
+    except (TypeError, KeyError):
         return None
 
 
@@ -124,31 +148,66 @@ def calib_copy(device, nbytes=256 << 20):
     del src, dst
 
 
-def cpu_baseline(cfg, budget_s=20.0):
-    """Time the eager fp32 oracle (oracle/morpho_oracle.py) on the host CPU on a
-    bounded sample of the workload: one batch row (all heads, full sequence)."""
-    from oracle import morpho_oracle as mo
-    B, N, D, H, m, scale, causal, seed, xm = cfg
-    torch.manual_seed(seed)
-    W_phi, gq, gk, W_V = mo.init_params(D, H, m)
-    torch.manual_seed(seed)
-    x = (xm * torch.randn(1, N, D)).half().float()
-    dout = torch.randn(1, N, D)
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def _time_cpu(fn, warmup=2, runs=5, budget_s=15.0):
+    """Median wall time (s) of fn() after `warmup` untimed calls; at least one
+    and at most `runs` timed calls, fewer when the budget is spent."""
+    for _ in range(warmup):
+        fn()
     times = []
     t_start = time.perf_counter()
-    while True:
+    while len(times) < runs:
         t0 = time.perf_counter()
-        mo.morpho_attention_ref_grads(x, W_phi, gq, gk, W_V, H, m, scale=scale, causal=causal, dout=dout,
-                                      dtype=torch.float32, head_chunk=4)
+        fn()
         times.append(time.perf_counter() - t0)
-        if time.perf_counter() - t_start > budget_s * 0.5 or len(times) >= 5:
+        if time.perf_counter() - t_start > budget_s:
             break
-    t = statistics.median(times)
+    return statistics.median(times), len(times)
+
+
+def cpu_baseline(cfg, name):
+    """The reference has no CPU path (its ops are CUDA-only), so the CPU
+    baseline is the eager fp32 oracle (oracle/morpho_oracle.py) on the host
+    cores, on the same fp16 input values upcast to fp32 (CPU
+    baseline plan): configs[0] (C1) in full, and a bounded sample of this
+    workload, one batch row with all heads and the full sequence. Each: 2
+    warm-up calls, then the median of up to 5 timed calls, forward and
+    forward + backward."""
+    from oracle import morpho_oracle as mo
+
+    def measure(c, rows):
+        B, N, D, H, m, scale, causal, seed, xm = c
+        x, params, dout = make_inputs(c, "cpu", dtype=torch.float32)
+        x, dout = x.detach()[:rows], dout[:rows]
+        params = [p.detach() for p in params]
+        with torch.no_grad():
+            fwd_s, nf = _time_cpu(lambda: mo.morpho_attention_ref(x, *params, H, m, scale=scale, causal=causal))
+        step_s, ns = _time_cpu(lambda: mo.morpho_attention_ref_grads(
+            x, *params, H, m, scale=scale, causal=causal, dout=dout, dtype=torch.float32, head_chunk=4))
+        return {"fwd_ms": round(fwd_s * 1e3, 2), "fwd_bwd_ms": round(step_s * 1e3, 2),
+                "tokens_per_s": round(rows * N / step_s, 1), "runs": [nf, ns]}
+
+    c1 = measure(C1, C1[0])
+    B, N = cfg[0], cfg[1]
+    w = measure(cfg, 1)
     return {
-        "value": N / t, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
-        "sample": f"oracle fp32 fwd+bwd of 1 of {B} batch rows (N={N}, all {H} heads), median of {len(times)} runs, "
-                  f"{t * 1e3:.0f} ms each; CPU: {platform.processor() or platform.machine()}, "
-                  f"os.cpu_count()={os.cpu_count()}",
+        "value": w["tokens_per_s"], "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+        "sample": f"oracle fp32 fwd+bwd of 1 of {B} batch rows of {name} (N={N}, all heads): "
+                  f"{w['fwd_bwd_ms']} ms (fwd {w['fwd_ms']} ms), median of {w['runs'][1]} runs after 2 warm-ups; "
+                  f"C1 (B2 N128 D256 H8 m16, full): fwd+bwd {c1['fwd_bwd_ms']} ms, fwd {c1['fwd_ms']} ms; "
+                  f"CPU: {cpu_model()}, os.cpu_count()={os.cpu_count()}, torch threads {torch.get_num_threads()}",
+        "workload_sample": w,
+        "c1": c1,
     }
 
 
@@ -380,6 +439,16 @@ def main():
     log(f"step {ms_step:.4f} ms  fwd {ms_fwd:.4f} ms  step-level {(f_fwd + f_bwd) / (ms_step * 1e-3) / 1e12:.1f} "
         f"TFLOP/s")
 
+    roofline = {"bound": "mfma", "kernel": dominant, "achieved": round(achieved, 2), "peak": PEAK_FP16_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
+                "traffic": load_traffic(dominant, args.config)}
+    trace_ms = load_trace_avg(dominant, args.config)
+    if trace_ms:
+        # the same kernel's mean over the timed steps of the committed
+        # rocprofv3 kernel trace of this command (the tracer's own timestamps)
+        roofline["rocprof"] = {"avg_ms": round(trace_ms, 5),
+                               "achieved": round(dom_flops / (trace_ms * 1e-3) / 1e12, 2),
+                               "frac": round(dom_flops / (trace_ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4)}
     result = {
         "metric": "fwd+bwd ms & tokens/s at B4 N4096 D1024 H16 causal fp16; % of roofline",
         "value": round(B * N / (ms_step * 1e-3), 1),
@@ -399,14 +468,12 @@ def main():
         "fwd_tokens_per_s": round(B * N / (ms_fwd * 1e-3), 1),
         "step_roofline_frac": round((f_fwd + f_bwd) / 2.5e15 / (ms_step * 1e-3), 4),
         "fwd_roofline": fwd_roof,
-        "roofline": {"bound": "mfma", "kernel": dominant, "achieved": round(achieved, 2),
-                     "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
-                     "traffic": load_traffic(dominant, args.config)},
+        "roofline": roofline,
         "kernels": kernels,
     }
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle on host cores)...")
-        result["cpu_baseline"] = cpu_baseline(cfg)
+        result["cpu_baseline"] = cpu_baseline(cfg, args.config)
     print(json.dumps(result), flush=True)
 
 

@@ -243,3 +243,42 @@ def test_exact_switch_gradients_agree():
     rels = [((a - b).abs().max() / b.abs().max().clamp_min(1e-30)).item() for a, b in zip(*res)]
     _say("[soft] product form vs element-wise gradients: " + " ".join(f"{n}={r:.2e}" for n, r in zip(NAMES, rels)))
     assert max(rels) <= 2e-3
+
+
+@pytest.mark.parametrize("sgn", [1, -1], ids=["dilation", "erosion"])
+def test_soft_product_form_at_the_benchmarked_head_shape(sgn):
+    """The C3 head shape the soft aggregation is benchmarked on (N = 4096,
+    cube_m = 16, dv = 64, causal, tau = 0.5; two heads, default init): the
+    product form must be the path taken (flag 0), and outputs, zb and every
+    gradient including dtau meet the bars against the fp32 oracle (evaluated
+    one head at a time: it materialises [N, N, dv] per head)."""
+    from morphottention_amd import MorphoAttention
+    B, N, H, m, dv, tau, scale = 1, 4096, 2, 16, 64, 0.5, 1.0
+    _say(f"[case] soft benchmarked head shape N={N} m={m} dv={dv} sgn={sgn:+d}")
+    torch.manual_seed(2)
+    mod = MorphoAttention(H * dv, H, m, dtype=torch.float16, device="cpu")
+    params = [t.detach().cuda() for t in (mod.W_phi, mod.gate_q, mod.gate_k, mod.W_V)]
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(B, N, H * dv, generator=g).half().cuda()
+    dout = torch.randn(B, N, H * dv, generator=g).half().cuda()
+    t = torch.tensor([tau], dtype=torch.float32, device="cuda")
+    _, _, ws = torch.ops.morphottention.soft_forward(x, *params, t, H, m, scale, True, sgn, 0)
+    torch.cuda.synchronize()
+    assert _flag(ws, B, N, H * dv, H, m) == 0, "the product form fell back"
+    out, zb, grads = _run(x, params, tau, H, m, scale, True, sgn, dout)
+    ref_out, ref_zb, ref_grads = mo.soft_morph_ref_grads(x, *params, tau, H, m, scale=scale, causal=True, sgn=sgn,
+                                                         dout=dout, dtype=torch.float32, head_chunk=1)
+    err = (out.float() - ref_out).abs()
+    excess = (err - _half_ulp(ref_out)).clamp_min(0).max().item()
+    zerr = (tau * math.log(2.0) * (zb - ref_zb).abs()).max().item()
+    vmax = mo.values(x.float(), params[3].float(), H).abs().max().item()
+    zbar = 2.0 ** -13 * vmax + 1e-4
+    rels = [(a.float() - b.float().reshape(a.shape)).abs().max().item() / max(b.abs().max().item(), 1e-30)
+            for a, b in zip(grads, ref_grads)]
+    dtau_bar = 1e-2 * ref_grads[5].abs().item() + 2e-6 * (dout.float() * ref_out).abs().sum().item() / tau
+    dtau_err = (grads[5].float() - ref_grads[5].float().reshape(grads[5].shape)).abs().item()
+    _say(f"[soft] head shape sgn {sgn:+d}: beyond rounding {excess:.3e} zb {zerr:.2e} (bar {zbar:.2e}) grads "
+         + " ".join(f"{n}={r:.2e}" for n, r in zip(NAMES[:5], rels))
+         + f" dtau {dtau_err:.2e} of {ref_grads[5].abs().item():.2e} (bar {dtau_bar:.2e})")
+    assert excess <= FWD_TOL and zerr <= zbar
+    assert all(r <= GRAD_TOL for r in rels[:5]) and dtau_err <= dtau_bar
