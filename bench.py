@@ -115,10 +115,10 @@ def load_profile(kind, config):
 
 def load_traffic(kernel, config):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary
-    (profiles/hbm_traffic_<config>.json: FETCH_SIZE and WRITE_SIZE per dispatch,
+    (profiles/counters_<config>.json: FETCH_SIZE and WRITE_SIZE per dispatch,
     each scaled by the same counter's reading for a plain copy of known size).
     Offline numbers: PMC passes cannot run inside this timed process."""
-    data = load_profile("hbm_traffic", config)
+    data = load_profile("counters", config)
     try:
         # the profiler names the device function, e.g. attn_bwd -> attn_bwd_kernel
         return data["kernels"][f"{kernel}_kernel"]["hbm_bytes_per_launch"]
@@ -135,6 +135,144 @@ def load_trace_avg(kernel, config):
         return data["kernels"][f"{kernel}_kernel"]["timed_avg_us"] / 1e3
     except (TypeError, KeyError):
         return None
+
+
+def _short_kernel_name(name):
+    """`morpho::attn_bwd_kernel<...>(...)` or its mangled form -> `attn_bwd_kernel`."""
+    if name.startswith("_ZN6morpho"):
+        rest = name[len("_ZN6morpho"):]
+        n = 0
+        while rest and rest[0].isdigit():
+            n = 10 * n + int(rest[0])
+            rest = rest[1:]
+        return rest[:n]
+    return name.split("(")[0].split("<")[0].split("::")[-1]
+
+
+# SQ counters of the PMC passes (rocprofv3 --pmc, one pass each) and how they
+# are normalised: per SIMD, per CU or per wave-cycle, with GRBM_GUI_ACTIVE summed
+# over the 8 XCDs (kernel cycles = GRBM_GUI_ACTIVE / 8).
+PMC_PASSES = [
+    "SQ_WAVES SQ_WAVE_CYCLES SQ_BUSY_CYCLES SQ_WAIT_INST_ANY SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_VALU "
+    "SQ_INSTS_MFMA SQ_INSTS_LDS GRBM_GUI_ACTIVE",
+    "SQ_ACTIVE_INST_VALU SQ_ACTIVE_INST_LDS SQ_LDS_BANK_CONFLICT SQ_LDS_IDX_ACTIVE SQ_WAIT_INST_LDS "
+    "SQ_VALU_MFMA_COEXEC_CYCLES SQ_INSTS_VALU_TRANS_F32 SQ_ACTIVE_INST_ANY GRBM_GUI_ACTIVE",
+    "FETCH_SIZE",
+    "WRITE_SIZE",
+]
+
+
+def rocprof_commands(config):
+    """The profiling commands whose output --summarize condenses (repo root,
+    TMPDIR=/tmp; each PMC pass in a process of its own)."""
+    base = f"python bench.py --config {config} --no-cpu-baseline"
+    kt = (f"rocprofv3 --kernel-trace --stats -f csv -d gpurun_out/prof/kt_{config} -o run -- "
+          f"{base} --steps 5 --warmup 2 --timing-steps 1")
+    pmc = [f"rocprofv3 --pmc {ctrs} -f csv -d gpurun_out/prof/pmc{i + 1}_{config} -o run -- "
+           f"{base} --steps 1 --warmup 1 --timing-steps 1 --calib-copy" for i, ctrs in enumerate(PMC_PASSES)]
+    return kt, pmc
+
+
+def summarize_rocprof(kind, config, src, steps, warmup):
+    """Condense rocprofv3 CSV output into the committed summary
+    profiles/<kind>_<config>.(json|md). kind "kernel_trace": `src` is the
+    --kernel-trace output directory; per kernel, the mean duration over the
+    dispatches of the timed steps (dispatches warmup .. warmup + steps - 1 of
+    each kernel, all of which launch once per step). kind "counters": `src` is
+    a comma-separated list of --pmc output directories (PMC_PASSES order, the
+    last two FETCH_SIZE and WRITE_SIZE with --calib-copy)."""
+    import csv
+    import glob as _glob
+    os.makedirs(os.path.join(ROOT, "profiles"), exist_ok=True)
+    if kind == "kernel_trace":
+        f = _glob.glob(os.path.join(src, "*kernel_trace.csv"))[0]
+        per = {}
+        for r in csv.DictReader(open(f)):
+            per.setdefault(_short_kernel_name(r["Kernel_Name"]), []).append(
+                (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+        out = {"config": config, "command": rocprof_commands(config)[0],
+               "summary_command": f"python bench.py --config {config} --steps {steps} --warmup {warmup} "
+                                  f"--summarize kernel_trace {src}",
+               "timed_window":
+               f"dispatches {warmup}..{warmup + steps - 1} of each kernel", "kernels": {}}
+        for k, v in per.items():
+            w = v[warmup:warmup + steps]
+            if not w:
+                continue
+            out["kernels"][k] = {"calls": len(v), "timed_avg_us": round(sum(w) / len(w), 2),
+                                 "all_avg_us": round(sum(v) / len(v), 2), "min_us": round(min(v), 2),
+                                 "max_us": round(max(v), 2)}
+    else:
+        dirs = src.split(",")
+        vals = {}
+        for d in dirs:
+            f = _glob.glob(os.path.join(d, "*counter_collection.csv"))[0]
+            for r in csv.DictReader(open(f)):
+                k = _short_kernel_name(r["Kernel_Name"])
+                vals.setdefault(k, {}).setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+        mean = {k: {c: sum(v) / len(v) for c, v in d.items()} for k, d in vals.items()}
+        # the calibration copy is the largest copyBuffer dispatch of the run
+        calib = {c: max(v) for c, v in vals.get("__amd_rocclr_copyBuffer", {}).items()}
+        copy_kib = 256 * 1024.0
+        ff = copy_kib / calib["FETCH_SIZE"] if calib.get("FETCH_SIZE") else None
+        wf = copy_kib / calib["WRITE_SIZE"] if calib.get("WRITE_SIZE") else None
+        out = {"config": config, "commands": rocprof_commands(config)[1],
+               "summary_command": f"python bench.py --config {config} --summarize counters {src}",
+               "calibration": {"copy_bytes": 256 << 20, "fetch_factor": ff, "write_factor": wf,
+                               "note": "plain 256 MiB device copy (--calib-copy); factor = known KiB / counter KiB"},
+               "kernels": {}}
+        for k, a in mean.items():
+            if not k.endswith("_kernel"):
+                continue
+            e = {"counters": {c: round(v, 1) for c, v in sorted(a.items())}}
+            cyc = a.get("GRBM_GUI_ACTIVE", 0) / 8.0  # per-XCD kernel cycles
+            if cyc and "SQ_VALU_MFMA_BUSY_CYCLES" in a:
+                e["mfma_busy"] = round(a["SQ_VALU_MFMA_BUSY_CYCLES"] / (1024 * cyc), 4)
+            if "SQ_WAVE_CYCLES" in a and "SQ_WAIT_INST_ANY" in a:
+                e["wait_inst_any_per_wave_cycle"] = round(a["SQ_WAIT_INST_ANY"] / a["SQ_WAVE_CYCLES"], 4)
+                e["wait_inst_lds_per_wave_cycle"] = round(a.get("SQ_WAIT_INST_LDS", 0) / a["SQ_WAVE_CYCLES"], 4)
+            if "SQ_INSTS_MFMA" in a and a["SQ_INSTS_MFMA"]:
+                e["valu_per_mfma"] = round((a["SQ_INSTS_VALU"] - a["SQ_INSTS_MFMA"]) / a["SQ_INSTS_MFMA"], 2)
+            if cyc and "SQ_LDS_IDX_ACTIVE" in a:
+                e["lds_active_per_cu_cycle"] = round(a["SQ_LDS_IDX_ACTIVE"] / (256 * cyc), 4)
+                e["lds_bank_conflict_per_active"] = round(a["SQ_LDS_BANK_CONFLICT"] / max(a["SQ_LDS_IDX_ACTIVE"], 1), 4)
+            if cyc and "SQ_ACTIVE_INST_VALU" in a:
+                e["valu_issue_per_simd_cycle"] = round(4 * a["SQ_ACTIVE_INST_VALU"] / (1024 * cyc), 4)
+            if ff and "FETCH_SIZE" in a:
+                e["hbm_read_bytes"] = int(a["FETCH_SIZE"] * ff * 1024)
+            if wf and "WRITE_SIZE" in a:
+                e["hbm_write_bytes"] = int(a["WRITE_SIZE"] * wf * 1024)
+            if "hbm_read_bytes" in e and "hbm_write_bytes" in e:
+                e["hbm_bytes_per_launch"] = e["hbm_read_bytes"] + e["hbm_write_bytes"]
+            out["kernels"][k] = e
+    path = os.path.join(ROOT, "profiles", f"{kind}_{config}.json")
+    with open(path, "w") as f:
+        json.dump(out, f, indent=1)
+    # a readable table beside the JSON
+    lines = [f"# rocprofv3 {kind.replace('_', ' ')}, workload {config}", "", "Commands (repo root, TMPDIR=/tmp):", ""]
+    cmds = [out["command"]] if kind == "kernel_trace" else out["commands"]
+    lines += [f"    {c}" for c in cmds] + [f"    {out['summary_command']}", ""]
+    if kind == "kernel_trace":
+        lines += [f"Timed window: {out['timed_window']}.", "",
+                  "| kernel | calls | timed avg (us) | all avg (us) | min (us) | max (us) |", "|---|---|---|---|---|---|"]
+        for k, v in sorted(out["kernels"].items(), key=lambda kv: -kv[1]["timed_avg_us"]):
+            lines.append(f"| {k} | {v['calls']} | {v['timed_avg_us']} | {v['all_avg_us']} | {v['min_us']} | {v['max_us']} |")
+    else:
+        cols = ["mfma_busy", "valu_issue_per_simd_cycle", "valu_per_mfma", "wait_inst_any_per_wave_cycle",
+                "wait_inst_lds_per_wave_cycle", "lds_active_per_cu_cycle", "lds_bank_conflict_per_active",
+                "hbm_read_bytes", "hbm_write_bytes"]
+        lines += ["mfma_busy = SQ_VALU_MFMA_BUSY_CYCLES / (1024 SIMDs x kernel cycles); valu_issue = 4 "
+                  "SQ_ACTIVE_INST_VALU / (1024 x cycles); wait_* = SQ_WAIT_INST_* / SQ_WAVE_CYCLES; lds_active = "
+                  "SQ_LDS_IDX_ACTIVE / (256 CUs x cycles); bank conflicts = SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE; "
+                  "kernel cycles = GRBM_GUI_ACTIVE / 8 XCDs; HBM bytes = FETCH_SIZE / WRITE_SIZE KiB x the copy "
+                  f"calibration factors ({out['calibration']['fetch_factor']:.3f}, "
+                  f"{out['calibration']['write_factor']:.3f}).", "",
+                  "| kernel | " + " | ".join(cols) + " |", "|---" * (len(cols) + 1) + "|"]
+        for k, v in out["kernels"].items():
+            lines.append(f"| {k} | " + " | ".join(str(v.get(c, "")) for c in cols) + " |")
+    with open(path[:-5] + ".md", "w") as f:
+        f.write("\n".join(lines) + "\n")
+    log(f"wrote {path} and {path[:-5]}.md")
 
 
 def calib_copy(device, nbytes=256 << 20):
@@ -353,7 +491,13 @@ def main():
                          "aggregation, instead of the bare op")
     ap.add_argument("--tau", type=float, default=0.5, help="--layer soft: temperature")
     ap.add_argument("--erosion", action="store_true", help="--layer soft: soft min-plus instead of max-plus")
+    ap.add_argument("--summarize", nargs=2, metavar=("KIND", "SRC"), default=None,
+                    help="write profiles/<KIND>_<config>.json from rocprofv3 CSV output: KIND kernel_trace (SRC = "
+                         "the --kernel-trace directory of this command) or counters (SRC = comma-separated --pmc "
+                         "directories); no GPU work")
     args = ap.parse_args()
+    if args.summarize:
+        return summarize_rocprof(args.summarize[0], args.config, args.summarize[1], args.steps, args.warmup)
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; the path is sharded over "
                                    "(batch x head) without collectives"}))
