@@ -87,10 +87,13 @@ int make_dims(int64_t B, int64_t N, int64_t D, int64_t H, int64_t M, float scale
   d.proj = causal & MORPHO_MODE_PROJ_HARDTANH01 ? kProjHardTanh01
            : causal & MORPHO_MODE_PROJ_IDENTITY ? kProjIdentity
                                                 : kProjSigmoid;
-  // projection tiles: 320 columns when that divides H*M + D, else 256; the
-  // interleaved column order needs whole heads and 8-column pieces per tile
+  // projection tiles: 256 x 320 when 320 divides H*M + D, else 256 x 256, and
+  // 128 x 128 when the large tiles would fill less than one round of the 256
+  // CUs and 128 divides H*M + D; the interleaved column order needs whole
+  // heads and 8-column pieces per tile
   const int NC = d.HM + d.D;
   d.PBN = NC % 320 == 0 ? 320 : 256;
+  if (((T + 255) / 256) * ((NC + d.PBN - 1) / d.PBN) < 256 && NC % 128 == 0) d.PBN = 128;
   d.PCPT = d.PVPT = 0;
   if (NC % d.PBN == 0) {
     const int ntn = NC / d.PBN;

@@ -68,15 +68,16 @@ hipError_t launch_transpose_weights(const Dims& d, const f16* W_phi, const f16* 
 }
 
 // ---------------------------------------------------------------- projection forward
-// [Z | V] = X [W_phi | W_V] on 256 x BN tiles (BN = 320 when it divides the
-// H*M + D columns, e.g. 1280 at B4 N4096 D1024 H16 m16, which makes the grid
-// exactly one round of 256 tiles; 256 otherwise). The epilogue takes the
-// tile through LDS in four 64-row slabs (the slab of wave row wm is that
-// wave row's accumulators), fp32 with row stride BN + 1 = 1 (mod 64) banks so
-// that both passes below read conflict-free.
-template <int BN>
-using ProjGemm = Gemm<256, BN, 4, true, true, 64, 2>;
-constexpr int kProjBM = 256;
+// [Z | V] = X [W_phi | W_V] on BM x BN tiles: 256 x 320 when 320 divides the
+// H*M + D columns (e.g. 1280 at B4 N4096 D1024 H16 m16, which makes the grid
+// exactly one round of 256 tiles), 256 x 256 otherwise, and 128 x 128 when
+// the large tiles would leave most CUs idle (few tokens: B8 N1024 D512 H8 m16
+// has 64 large tiles, 320 small ones). The epilogue takes the tile through
+// LDS in 64-row slabs (a slab holds the accumulators of the wave rows whose
+// rows it covers), fp32 with row stride BN + 1 = 1 (mod 64) banks so that both
+// passes below read conflict-free.
+template <int BM, int BN>
+using ProjGemm = Gemm<BM, BN, 4, true, true, 64, 2>;
 
 // e4m3 byte(s) of V_lo * 2^kVloExp, clamped to the format's range (e4m3 has
 // no infinity: an overflowing conversion gives NaN) and rounded toward zero:
@@ -100,11 +101,11 @@ __device__ __forceinline__ uint2 vlo_pack8(const float (&r)[8]) {
 
 // GEN: a cube projection other than the sigmoid, or the masked diagonal (the
 // variants take the projection from d.proj and the exact row maximum)
-template <int M, int DV, int BN, bool GEN>
+template <int M, int DV, int BM, int BN, bool GEN>
 __global__ __launch_bounds__(kGemmThreads) void proj_fwd_kernel(const f16* __restrict__ X,
                                                                const f16* __restrict__ gate_q,
                                                                const f16* __restrict__ gate_k, Dims d, ProjBuffers p) {
-  using G = ProjGemm<BN>;
+  using G = ProjGemm<BM, BN>;
   constexpr int SS = BN + 1;  // stage row stride (floats)
   static_assert(64 * SS * 4 <= G::kLdsBytes, "epilogue slab must fit the main loop's LDS");
   __shared__ __align__(16) char smem[G::kLdsBytes];
@@ -115,24 +116,25 @@ __global__ __launch_bounds__(kGemmThreads) void proj_fwd_kernel(const f16* __res
   const int NC = d.HM + d.D;
   const int T = (int)d.T;
   int tm, tn;
-  if (!gemm_tile_map(blockIdx.x, (T + kProjBM - 1) / kProjBM, (NC + BN - 1) / BN, tm, tn)) return;
-  const int n0 = tn * BN, m0 = tm * kProjBM;
+  if (!gemm_tile_map(blockIdx.x, (T + BM - 1) / BM, (NC + BN - 1) / BN, tm, tn)) return;
+  const int n0 = tn * BN, m0 = tm * BM;
   f32x16 acc[G::FI][G::FJ];
   G::run(X, d.D, p.wt, d.D, T, NC, m0, n0, 0, d.D, smem, acc);
 
   float* stage = reinterpret_cast<float*>(smem);
   const float c1 = 2.0f * d.scale * kLog2e;
-  static_assert(G::WTM == 64, "one wave row per 64-row slab");
-  for (int slab = 0; slab < kProjBM / 64; ++slab) {
+  static_assert(G::WTM == 64 || G::WTM == 32, "wave rows of 64 or 32 rows");
+  for (int slab = 0; slab < BM / 64; ++slab) {
     if (slab > 0) __syncthreads();  // the previous slab has been consumed
-    if (wm == slab) {
+    if (G::WTM * wm / 64 == slab) {  // uniform: this wave row's rows are in the slab
+      const int r0 = G::WTM * wm % 64;
 #pragma unroll
       for (int i = 0; i < G::FI; ++i)
 #pragma unroll
         for (int j = 0; j < G::FJ; ++j)
 #pragma unroll
           for (int r = 0; r < 16; ++r)
-            stage[(32 * i + acc_row(r, lane)) * SS + G::WTN * wn + 32 * j + (lane & 31)] = acc[i][j][r];
+            stage[(r0 + 32 * i + acc_row(r, lane)) * SS + G::WTN * wn + 32 * j + (lane & 31)] = acc[i][j][r];
     }
     __syncthreads();
     const int row0 = m0 + 64 * slab;
@@ -266,20 +268,23 @@ __global__ __launch_bounds__(kGemmThreads) void proj_fwd_kernel(const f16* __res
 template <int M, int DV>
 static hipError_t launch_proj_fwd_t(const Dims& d, const f16* X, const f16* gq, const f16* gk, const ProjBuffers& p,
                                     hipStream_t s) {
-  const int NC = d.HM + d.D, nrows = (int)((d.T + kProjBM - 1) / kProjBM);
+  const int NC = d.HM + d.D;
   const bool gen = d.proj != kProjSigmoid || d.mask_diag;
-  const dim3 g320(gemm_tile_grid(nrows, NC / 320)), g256(gemm_tile_grid(nrows, (NC + 255) / 256));
-  if (d.PBN == 320) {
-    if (gen)
-      hipLaunchKernelGGL((proj_fwd_kernel<M, DV, 320, true>), g320, dim3(kGemmThreads), 0, s, X, gq, gk, d, p);
-    else
-      hipLaunchKernelGGL((proj_fwd_kernel<M, DV, 320, false>), g320, dim3(kGemmThreads), 0, s, X, gq, gk, d, p);
-  } else {
-    if (gen)
-      hipLaunchKernelGGL((proj_fwd_kernel<M, DV, 256, true>), g256, dim3(kGemmThreads), 0, s, X, gq, gk, d, p);
-    else
-      hipLaunchKernelGGL((proj_fwd_kernel<M, DV, 256, false>), g256, dim3(kGemmThreads), 0, s, X, gq, gk, d, p);
-  }
+#define MORPHO_PROJ_LAUNCH(BM_, BN_)                                                                       \
+  do {                                                                                                     \
+    const dim3 g(gemm_tile_grid((int)((d.T + BM_ - 1) / BM_), (NC + BN_ - 1) / BN_));                      \
+    if (gen)                                                                                               \
+      hipLaunchKernelGGL((proj_fwd_kernel<M, DV, BM_, BN_, true>), g, dim3(kGemmThreads), 0, s, X, gq, gk, d, p);  \
+    else                                                                                                   \
+      hipLaunchKernelGGL((proj_fwd_kernel<M, DV, BM_, BN_, false>), g, dim3(kGemmThreads), 0, s, X, gq, gk, d, p); \
+  } while (0)
+  if (d.PBN == 320)
+    MORPHO_PROJ_LAUNCH(256, 320);
+  else if (d.PBN == 128)
+    MORPHO_PROJ_LAUNCH(128, 128);
+  else
+    MORPHO_PROJ_LAUNCH(256, 256);
+#undef MORPHO_PROJ_LAUNCH
   return hipGetLastError();
 }
 
