@@ -49,7 +49,7 @@ __device__ __forceinline__ float sum8(const f16x8& v) {
 // 16 rows one b128 read phase touches land on distinct bank groups.
 __device__ __forceinline__ int vswz(int r) { return (r ^ (r >> 3)) & 7; }
 
-template <int M, int DV>
+template <int M, int DV, bool SM = false>
 struct FwdCfg {
   static constexpr int CW = 2 * M + 8;    // code row width
   static constexpr int NCH = M / 8;       // 16-wide code chunks (hi, then lo)
@@ -57,8 +57,13 @@ struct FwdCfg {
   // Each wave owns QB blocks of 32 queries: every K / V fragment read from LDS
   // then feeds QB MFMAs. Two blocks where the registers allow it (m dv <=
   // 1024; at m = 32, dv = 64 two blocks spill).
-  static constexpr int QB = (M <= 32 && DV <= 64 && M * DV <= 1024) ? 2 : 1;
-  static constexpr int WAVES = 8 / QB;
+  // SM (small problems, fewer than two of the regular workgroups per CU): one
+  // query block per wave, four waves, three workgroups per CU, so the launch
+  // has twice the workgroups and still covers the CUs.
+  static constexpr int QB2 = (M <= 32 && DV <= 64 && M * DV <= 1024) ? 2 : 1;
+  static constexpr bool SMALL = SM && QB2 == 2;
+  static constexpr int QB = SMALL ? 1 : QB2;
+  static constexpr int WAVES = SMALL ? 4 : 8 / QB;
   static constexpr int QW = 32 * QB * WAVES;  // 256 queries per workgroup
   // A stage holds one key tile [KT][CW] (rows in swap23 order within each 32,
   // unpadded: CW = 8 (mod 16) halves keeps b128 reads conflict-free), one
@@ -82,9 +87,9 @@ struct FwdCfg {
   // fit in half the 160 KiB LDS (less 1 KiB for the rest); the eight-wave
   // shapes (one query block per wave) would have to fit 128 VGPRs and spill.
   static constexpr bool TWO = 2 * STAGE * 2 <= 79 * 1024 && QB == 2;
-  static constexpr int WG_PER_CU = TWO ? 2 : 1;
+  static constexpr int WG_PER_CU = SMALL ? 3 : TWO ? 2 : 1;
   static constexpr int WAVES_PER_EU = WG_PER_CU * WAVES / 4;
-  static constexpr int LDS_BUDGET = (TWO ? 79 : 158) * 1024;
+  static constexpr int LDS_BUDGET = (SMALL ? 52 : TWO ? 79 : 158) * 1024;
   static constexpr int NSTAGE = 3 * STAGE * 2 <= LDS_BUDGET ? 3 : 2;
   // both 32-key blocks of a tile in flight at once (fits the registers except
   // with the widest codes and values)
@@ -98,15 +103,15 @@ struct FwdCfg {
 // to arrive; one barrier per tile.
 // MAXPASS: key tiles only, track the row max of the exponent (exact path).
 // MD: the diagonal (key == query) is masked.
-template <int M, int DV, bool MAXPASS, bool MD>
+template <int M, int DV, bool MAXPASS, bool MD, bool SM>
 __device__ __forceinline__ void fwd_pass(const f16* __restrict__ ka, const f16* __restrict__ vt,
                                          const uint8_t* __restrict__ vlo, int64_t rowbase, int64_t vbase,
                                          int N, int NP, int causal, int kend, int q0, int qw0,
-                                         f16* smem, const f16x8 (&qf)[FwdCfg<M, DV>::QB][FwdCfg<M, DV>::NCH],
-                                         const f16x4 (&qaug)[FwdCfg<M, DV>::QB],
-                                         f32x16 (&o)[FwdCfg<M, DV>::QB][DV / 32], float (&lsum)[FwdCfg<M, DV>::QB],
-                                         float (&rmax)[FwdCfg<M, DV>::QB]) {
-  using C = FwdCfg<M, DV>;
+                                         f16* smem, const f16x8 (&qf)[FwdCfg<M, DV, SM>::QB][FwdCfg<M, DV, SM>::NCH],
+                                         const f16x4 (&qaug)[FwdCfg<M, DV, SM>::QB],
+                                         f32x16 (&o)[FwdCfg<M, DV, SM>::QB][DV / 32], float (&lsum)[FwdCfg<M, DV, SM>::QB],
+                                         float (&rmax)[FwdCfg<M, DV, SM>::QB]) {
+  using C = FwdCfg<M, DV, SM>;
   constexpr int QB = C::QB;
   constexpr int NPWX = MAXPASS ? C::NPW_K : C::NPW;
   const int tid = threadIdx.x, lane = tid & 63, h32 = lane >> 5, l32 = lane & 31;
@@ -387,14 +392,14 @@ __device__ __forceinline__ void fwd_pass(const f16* __restrict__ ka, const f16* 
   }
 }
 
-template <int M, int DV, bool MD>
-__global__ __launch_bounds__((64 * FwdCfg<M, DV>::WAVES))
-__attribute__((amdgpu_waves_per_eu(FwdCfg<M, DV>::WAVES_PER_EU, FwdCfg<M, DV>::WAVES_PER_EU)))
+template <int M, int DV, bool MD, bool SM>
+__global__ __launch_bounds__((64 * FwdCfg<M, DV, SM>::WAVES))
+__attribute__((amdgpu_waves_per_eu(FwdCfg<M, DV, SM>::WAVES_PER_EU, FwdCfg<M, DV, SM>::WAVES_PER_EU)))
 void attn_fwd_kernel(f16* __restrict__ qa, const f16* __restrict__ ka, const f16* __restrict__ vt,
                      const uint8_t* __restrict__ vlo,
                      const float4* __restrict__ tstat, f16* __restrict__ out, float* __restrict__ lse, int N, int NP,
                      int H, int D, int BH, int causal) {
-  using C = FwdCfg<M, DV>;
+  using C = FwdCfg<M, DV, SM>;
   constexpr int QB = C::QB;
   __shared__ __align__(16) f16 smem[C::NSTAGE * C::STAGE];
   const int tid = threadIdx.x, lane = tid & 63, h32 = lane >> 5, l32 = lane & 31;
@@ -448,7 +453,7 @@ void attn_fwd_kernel(f16* __restrict__ qa, const f16* __restrict__ ka, const f16
       qa0[qb] = qaug[qb];
       if (h32 == 0) { qa0[qb][2] = (f16)0.f; qa0[qb][3] = (f16)0.f; }
     }
-    fwd_pass<M, DV, true, MD>(ka, vt, vlo, rowbase, vbase, N, NP, causal, kend, q0, qw0, smem, qf, qa0, o, lsum, rmax);
+    fwd_pass<M, DV, true, MD, SM>(ka, vt, vlo, rowbase, vbase, N, NP, causal, kend, q0, qw0, smem, qf, qa0, o, lsum, rmax);
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
       const float m = fmaxf(rmax[qb], __shfl_xor(rmax[qb], 32));
@@ -459,7 +464,7 @@ void attn_fwd_kernel(f16* __restrict__ qa, const f16* __restrict__ ka, const f16
     }
     __syncthreads();  // every wave is done with the stages before they are refilled
   }
-  fwd_pass<M, DV, false, MD>(ka, vt, vlo, rowbase, vbase, N, NP, causal, kend, q0, qw0, smem, qf, qaug, o, lsum, rmax);
+  fwd_pass<M, DV, false, MD, SM>(ka, vt, vlo, rowbase, vbase, N, NP, causal, kend, q0, qw0, smem, qf, qaug, o, lsum, rmax);
 
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
@@ -491,17 +496,27 @@ void attn_fwd_kernel(f16* __restrict__ qa, const f16* __restrict__ ka, const f16
   }
 }
 
-template <int M, int DV>
-static hipError_t launch_attn_fwd_t(const Dims& d, const ProjBuffers& p, f16* out, float* lse, hipStream_t s) {
-  using C = FwdCfg<M, DV>;
+template <int M, int DV, bool SM>
+static hipError_t launch_attn_fwd_c(const Dims& d, const ProjBuffers& p, f16* out, float* lse, hipStream_t s) {
+  using C = FwdCfg<M, DV, SM>;
   const dim3 grid(xcd_grid((d.N + C::QW - 1) / C::QW, d.B * d.H));
   if (d.mask_diag)
-    hipLaunchKernelGGL((attn_fwd_kernel<M, DV, true>), grid, dim3(64 * C::WAVES), 0, s, p.qa, p.ka, p.vt, p.vlo,
+    hipLaunchKernelGGL((attn_fwd_kernel<M, DV, true, SM>), grid, dim3(64 * C::WAVES), 0, s, p.qa, p.ka, p.vt, p.vlo,
                        p.tstat, out, lse, d.N, d.NP, d.H, d.D, d.B * d.H, d.causal);
   else
-    hipLaunchKernelGGL((attn_fwd_kernel<M, DV, false>), grid, dim3(64 * C::WAVES), 0, s, p.qa, p.ka, p.vt, p.vlo,
-                       p.tstat, out, lse, d.N, d.NP, d.H, d.D, d.B * d.H, d.causal);
+    hipLaunchKernelGGL((attn_fwd_kernel<M, DV, false, SM>), grid, dim3(64 * C::WAVES), 0, s, p.qa, p.ka, p.vt,
+                       p.vlo, p.tstat, out, lse, d.N, d.NP, d.H, d.D, d.B * d.H, d.causal);
   return hipGetLastError();
+}
+
+template <int M, int DV>
+static hipError_t launch_attn_fwd_t(const Dims& d, const ProjBuffers& p, f16* out, float* lse, hipStream_t s) {
+  using C = FwdCfg<M, DV, false>;
+  if constexpr (FwdCfg<M, DV, true>::SMALL) {
+    const int64_t wgs = (int64_t)((d.N + C::QW - 1) / C::QW) * d.B * d.H;
+    if (wgs < 2 * 256) return launch_attn_fwd_c<M, DV, true>(d, p, out, lse, s);
+  }
+  return launch_attn_fwd_c<M, DV, false>(d, p, out, lse, s);
 }
 
 
