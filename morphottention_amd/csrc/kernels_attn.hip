@@ -687,7 +687,7 @@ struct BwdCfg {
 // the backward computed the projection itself); the dO rows come from
 // grad_out and their affine block {-delta} from bwd_prep's aug rows.
 template <int M, int DV, bool MD>
-__global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ qa, const f16* __restrict__ ka,
+__global__ __launch_bounds__(256, 2) void attn_bwd_kernel(const f16* __restrict__ qa, const f16* __restrict__ ka,
                                                        const f16* __restrict__ vt, const f16* __restrict__ aug,
                                                        const f16* __restrict__ grad_out, float* __restrict__ dq,
                                                        float* __restrict__ dk, float* __restrict__ dcb,
@@ -861,7 +861,7 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ q
   // tiles split over the waves, contraction over all 128 keys of the workgroup
   // (rows past N are zero in both operands). The phi operand never changes:
   // it is read once.
-  f16x8 dqa[C::DQT][C::KW / 32], dqb[C::DQT][C::KW / 32];
+  f16x8 dqa[C::DQT][C::KW / 32];
   int d_s[C::DQT][2];
 #pragma unroll
   for (int t = 0; t < C::DQT; ++t) {
@@ -880,12 +880,7 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ q
   // and the dq atomics on every sub-block.
   wait_vmcnt<0>();
   __syncthreads();  // sPk is complete
-#pragma unroll
-  for (int t = 0; t < C::DQT; ++t) {
-    const int ct = (w + 4 * t) / (C::QT / 16);
-#pragma unroll
-    for (int kc = 0; kc < C::KW / 32; ++kc) dqb[t][kc] = tfrag16<C::PRB>(sPk, 32 * kc, 16 * ct, lane);
-  }
+
   auto dq_load = [&](const char* sd) {
 #pragma unroll
     for (int t = 0; t < C::DQT; ++t)
@@ -936,7 +931,8 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ q
       const int qt = tile % (C::QT / 16);
       f32x4 acc = {};
 #pragma unroll
-      for (int kc = 0; kc < C::KW / 32; ++kc) acc = mfma16x16(dqa[t][kc], dqb[t][kc], acc);
+      for (int kc = 0; kc < C::KW / 32; ++kc)
+        acc = mfma16x16(dqa[t][kc], tfrag16<C::PRB>(sPk, 32 * kc, 16 * (tile / (C::QT / 16)), lane), acc);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         if (full) {
@@ -975,63 +971,90 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const f16* __restrict__ q
     const char* tO = tQ + C::OOFF;
     const char* tA = tQ + C::AOFF;
     char* tS = sdS[PAR];
+    // S = Q~ K~^T and dP - delta = dO~ V~^T of sub-block sb (rows: queries in
+    // swap23 order; lane: key)
+    auto scores = [&](int sb, f32x16& s, f32x16& dp) {
+      const char* qsb = tQ + 32 * sb * C::QRB;
+      f16x8 qfr[C::NCH];
 #pragma unroll
-    for (int sb = 0; sb < C::NSB; ++sb) {
-      const int q0 = qs + 32 * sb;
-      f16x8 ds16[2] = {f16x8{}, f16x8{}};
-      if (!((causal && kw0 > q0 + 31) || kw0 >= N || q0 >= N)) {  // wave-uniform: something unmasked
-        // S = Q~ K~^T (rows: queries in swap23 order; lane: key)
-        const char* qsb = tQ + 32 * sb * C::QRB;
-        f16x8 qfr[C::NCH];
+      for (int c = 0; c < C::NCH; ++c) qfr[c] = *reinterpret_cast<const f16x8*>(qsb + r_q[c]);
+      s = code_dot<M, false>(kf, qfr, f32x16{});
+      s = mfma8(*reinterpret_cast<const f16x4*>(qsb + r_qa), kaug, s);
+      const char* osb = tO + 32 * sb * C::ORB;
+      dp = f32x16{};
 #pragma unroll
-        for (int c = 0; c < C::NCH; ++c) qfr[c] = *reinterpret_cast<const f16x8*>(qsb + r_q[c]);
-        f32x16 s = code_dot<M, false>(kf, qfr, f32x16{});
-        s = mfma8(*reinterpret_cast<const f16x4*>(qsb + r_qa), kaug, s);
-        // dP - delta = dO~ V~^T
-        const char* osb = tO + 32 * sb * C::ORB;
-        f32x16 dp = {};
+      for (int c = 0; c < DV / 16; ++c) dp = mfma16(*reinterpret_cast<const f16x8*>(osb + r_o[c]), vf[c], dp);
+      dp = mfma8(*reinterpret_cast<const f16x4*>(tA + 32 * sb * 16 + r_oa), vaug, dp);
+    };
+    // P, dS = P (dP - delta), dV^T += dO^T P, dk^T += phi^T dS (rows: dv /
+    // code; lane: key)
+    auto grads = [&](int sb, const f32x16& s, const f32x16& dp, f16x8 (&ds16)[2]) {
+      f16x8 p16[2];
 #pragma unroll
-        for (int c = 0; c < DV / 16; ++c) dp = mfma16(*reinterpret_cast<const f16x8*>(osb + r_o[c]), vf[c], dp);
-        dp = mfma8(*reinterpret_cast<const f16x4*>(tA + 32 * sb * 16 + r_oa), vaug, dp);
-        const bool need_mask = (q0 + 32 > N) || (kw0 + 31 >= N) || (causal && kw0 + 31 > q0) ||
-                               (MD && kw0 <= q0 + 31 && kw0 + 31 >= q0);
-        if (need_mask) {  // wave-uniform; masked scores become -inf (P = 0)
-          // one select per score from a mask built with bitwise operators:
-          // written as a conditional store after a short-circuit ||, the
-          // MD instances compiled to divergent blocks whose stores were
-          // dropped for in-range lanes (causal and diagonal masks lost)
-          const int kx = kvalid ? key : (1 << 30);  // a key past N exceeds every limit
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int qq = q0 + swap23(acc_row(r, lane));
-            const int klim = causal ? qq : N - 1;  // the largest key this query sees
-            const bool drop = (qq >= N) | (kx > klim) | (MD && kx == qq);
-            s[r] = drop ? kNegInf : s[r];
-          }
-        }
-        f16x8 p16[2];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float pr = fast_exp2(s[r]);
-          p16[r >> 3][r & 7] = (f16)pr;
-          ds16[r >> 3][r & 7] = (f16)(pr * dp[r]);
-        }
-        // dV^T += dO^T P ; dk^T += phi^T dS  (rows: dv / code; lane: key)
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {
-#pragma unroll
-          for (int dvb = 0; dvb < DV / 32; ++dvb)
-            dva[dvb] = mfma16(tfrag(tO, t_o[dvb], (32 * sb + 16 * c) * C::ORB), p16[c], dva[dvb]);
-#pragma unroll
-          for (int mb = 0; mb < C::MB; ++mb)
-            dka[mb] = mfma16(tfrag(tQ, t_q[mb], (32 * sb + 16 * c) * C::QRB), ds16[c], dka[mb]);
-        }
+      for (int r = 0; r < 16; ++r) {
+        const float pr = fast_exp2(s[r]);
+        p16[r >> 3][r & 7] = (f16)pr;
+        ds16[r >> 3][r & 7] = (f16)(pr * dp[r]);
       }
-      // dS^T row of this key (zeros where nothing was computed): logical chunk
-      // 4 sb + 2 c + h32 at physical chunk (4 sb + 2 c + h32) ^ sz
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+#pragma unroll
+        for (int dvb = 0; dvb < DV / 32; ++dvb)
+          dva[dvb] = mfma16(tfrag(tO, t_o[dvb], (32 * sb + 16 * c) * C::ORB), p16[c], dva[dvb]);
+#pragma unroll
+        for (int mb = 0; mb < C::MB; ++mb)
+          dka[mb] = mfma16(tfrag(tQ, t_q[mb], (32 * sb + 16 * c) * C::QRB), ds16[c], dka[mb]);
+      }
+    };
+    // dS^T row of this key (zeros where nothing was computed): logical chunk
+    // 4 sb + 2 c + h32 at physical chunk (4 sb + 2 c + h32) ^ sz
+    auto put_ds = [&](int sb, const f16x8 (&ds16)[2]) {
 #pragma unroll
       for (int c = 0; c < 2; ++c)
         *reinterpret_cast<f16x8*>(tS + kr * C::SRB + 16 * ((4 * sb + 2 * c + h32) ^ sz)) = ds16[c];
+    };
+    // A step whose two sub-blocks are whole and unmasked for this wave (the
+    // bulk of the work) runs as one straight block: the scores of sub-block 1
+    // are on the MFMA while sub-block 0's exponentials run on the VALU.
+    const bool plain = C::NSB == 2 && qs + C::QT <= N && kw0 + 31 < N && (!causal || kw0 + 31 <= qs) &&
+                       (!MD || kw0 > qs + C::QT - 1 || kw0 + 31 < qs);  // wave-uniform
+    if (plain) {
+      f32x16 s0, dp0, s1, dp1;
+      f16x8 d0[2], d1[2];
+      scores(0, s0, dp0);
+      scores(1, s1, dp1);
+      grads(0, s0, dp0, d0);
+      grads(1, s1, dp1, d1);
+      put_ds(0, d0);
+      put_ds(1, d1);
+    } else {
+#pragma unroll
+      for (int sb = 0; sb < C::NSB; ++sb) {
+        const int q0 = qs + 32 * sb;
+        f16x8 ds16[2] = {f16x8{}, f16x8{}};
+        if (!((causal && kw0 > q0 + 31) || kw0 >= N || q0 >= N)) {  // wave-uniform: something unmasked
+          f32x16 s, dp;
+          scores(sb, s, dp);
+          const bool need_mask = (q0 + 32 > N) || (kw0 + 31 >= N) || (causal && kw0 + 31 > q0) ||
+                                 (MD && kw0 <= q0 + 31 && kw0 + 31 >= q0);
+          if (need_mask) {  // wave-uniform; masked scores become -inf (P = 0)
+            // one select per score from a mask built with bitwise operators:
+            // written as a conditional store after a short-circuit ||, the
+            // MD instances compiled to divergent blocks whose stores were
+            // dropped for in-range lanes (causal and diagonal masks lost)
+            const int kx = kvalid ? key : (1 << 30);  // a key past N exceeds every limit
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int qq = q0 + swap23(acc_row(r, lane));
+              const int klim = causal ? qq : N - 1;  // the largest key this query sees
+              const bool drop = (qq >= N) | (kx > klim) | (MD && kx == qq);
+              s[r] = drop ? kNegInf : s[r];
+            }
+          }
+          grads(sb, s, dp, ds16);
+        }
+        put_ds(sb, ds16);
+      }
     }
     if (step >= 1) dq_finish(step - 1);
   };
