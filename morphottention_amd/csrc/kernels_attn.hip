@@ -650,7 +650,12 @@ template <int M, int DV>
 struct BwdCfg {
   static constexpr int CW = 2 * M + 8;
   static constexpr int NCH = M / 8;             // 16-wide code chunks (hi, then lo)
-  static constexpr int MB = M / 32 + 1;         // 32-row blocks of dk^T (codes + the ones row at row M)
+  // dcb (the column sums of dS) comes from the ones row M of the query rows'
+  // affine block on the MFMA when that row shares a 32-row block with codes
+  // (M = 16); for M = 32 and 64 it would need a block of its own, so the VALU
+  // sums the same fp16 dS values instead (v_dot2 against ones).
+  static constexpr bool DCB_VALU = M % 32 == 0;
+  static constexpr int MB = DCB_VALU ? M / 32 : M / 32 + 1;  // 32-row blocks of dk^T
   static constexpr int QT = M <= 32 ? 64 : 32;  // queries per step
   static constexpr int NSB = QT / 32;           // 32-query sub-blocks per step
   // LDS rows (bytes): query rows padded to a power of two, dO rows, the
@@ -747,6 +752,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_kernel(const f16* __restrict_
   for (int i = 0; i < DV / 32; ++i) dva[i] = f32x16{};
 #pragma unroll
   for (int i = 0; i < C::MB; ++i) dka[i] = f32x16{};
+  float dcb_acc = 0.f;  // DCB_VALU: this lane's share of dcb[key]
 
   const int qstart = causal ? k0 : 0;
   const int nsteps = qstart < N ? (N - qstart + C::QT - 1) / C::QT : 0;
@@ -996,6 +1002,15 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_kernel(const f16* __restrict_
         p16[r >> 3][r & 7] = (f16)pr;
         ds16[r >> 3][r & 7] = (f16)(pr * dp[r]);
       }
+      if (C::DCB_VALU) {
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+        const h2 ones2 = {(f16)1.f, (f16)1.f};
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            dcb_acc = __builtin_amdgcn_fdot2(h2{ds16[c][2 * e], ds16[c][2 * e + 1]}, ones2, dcb_acc, false);
+      }
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
 #pragma unroll
@@ -1075,7 +1090,9 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_kernel(const f16* __restrict_
   }
 
   // ---- epilogue: dk, dcb (fp32, per key) and dV (fp16 into the dZ|dV buffer)
+  const float dcb_sum = dcb_acc + __shfl_xor(dcb_acc, 32);  // lanes l, l + 32: the same key
   if (kvalid) {
+    if (C::DCB_VALU && h32 == 0) dcb[rowbase + key] = dcb_sum;
 #pragma unroll
     for (int mb = 0; mb < C::MB; ++mb)
 #pragma unroll
