@@ -34,6 +34,9 @@
 namespace morpho {
 
 constexpr float kGapExact = 25.0f;  // base-2; above this a row takes the exact-max path
+// The backward forms a query step's dS row sums (for the diagonal correction)
+// only when one of its rows has a diagonal weight above this.
+constexpr float kRowSumWeight = 0.5f;
 
 __device__ __forceinline__ float sum8(const f16x8& v) {
   const f16x2 one2 = {(f16)1.f, (f16)1.f};
@@ -561,17 +564,24 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(const f16* __restrict__ g
     f16 dh, dl;
     split_hi_lo(-delta, dh, dl);
     const f16 zero = (f16)0.f;
-    *reinterpret_cast<f16x8*>(aug + bhn * 8) = f16x8{dh, dl, zero, zero, zero, zero, zero, zero};
     const float l = lse[bhn];
     const float4 ts = tstat[bhn];
+    // the diagonal weight P_ii = 2^(s_ii - lse) with s_ii = t + b (0 when the
+    // diagonal is masked or the row has no keys), and whether the row needs
+    // its dS row sum: with the diagonal in the softmax only a row with most of
+    // its weight there does (elsewhere the offset the sum measures is below
+    // 2^-10 of the row's gradient); without it every row keeps its sum. The
+    // flag sits in the unused third slot of the affine block.
+    const float pii = diag && l > -kFltMax ? fast_exp2(ts.w + ts.x - l) : 0.f;
+    const f16 need = (!diag || pii > kRowSumWeight) ? (f16)1.f : zero;
+    *reinterpret_cast<f16x8*>(aug + bhn * 8) = f16x8{dh, dl, need, zero, zero, zero, zero, zero};
     if (write_q) {
       f16 lh, ll;
       split_hi_lo(l > -kFltMax ? -(l - ts.x) : 0.f, lh, ll);  // a row without keys: masked anyway
       *reinterpret_cast<f16x2*>(qa + bhn * CW + M + 2) = f16x2{lh, ll};
     }
-    // the row-sum accumulator (zero) and the diagonal weight P_ii = 2^(s_ii - lse)
-    // with s_ii = t + b (0 when the diagonal is masked or the row has no keys)
-    dr[bhn] = make_float2(0.f, diag && l > -kFltMax ? fast_exp2(ts.w + ts.x - l) : 0.f);
+    // the row-sum accumulator (zero) and the diagonal weight
+    dr[bhn] = make_float2(0.f, pii);
   }
   // zero dq: T * H * M floats, M / 4 float4 per (token, head)
   float4* z = reinterpret_cast<float4*>(dq);
@@ -907,12 +917,21 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_kernel(const f16* __restrict_
   // owns it: all waves when M <= 32, waves 0 and 1 when M = 64, QT = 32). Every
   // column of the 16 x 16 result holds the row sums; lanes with (lane & 15) < 4
   // add rows 4 (lane / 16) + (lane & 3) to dr, one atomic per row. The other
-  // waves add 0 there, so every wave issues one such atomic per step.
+  // waves add 0 there, so every wave issues one such atomic.
+  // Only a step with a flagged query row (bwd_prep's flag in the third slot
+  // of the dO affine block; every workgroup sees the same flags, so such a
+  // row gets the sums of all key blocks) forms its sums; the others issue
+  // neither the MFMAs nor the atomic, and the tile wait of the step after
+  // next allows one atomic fewer in flight.
   const bool rs_wave = C::QT / 16 >= 4 || w < C::QT / 16;  // uniform
   const int rs_row = 16 * (w % (C::QT / 16)) + 4 * (lane >> 4) + (lane & 3);
+  bool rs_need = false;  // the flag of the step whose sums rowsum() forms next
+  bool rs_sent = false;  // whether the previous step issued a row-sum atomic
   // issued right after the fragments of step st are read, so that it overlaps
   // the next step's body
   auto rowsum = [&](int st) {
+    rs_sent = rs_need;
+    if (!rs_need) return;  // uniform
     const int qs = qstep(st);
     f32x4 racc = {};
     if (rs_wave) {
@@ -961,10 +980,14 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_kernel(const f16* __restrict_
     constexpr int PAR = decltype(PARc)::value;
     // this step's tiles have landed (the atomics of step - 2, issued after
     // them, may still be in flight) and this wave's dS^T writes are done
-    if (step >= 2)
-      wait_vmcnt_lgkm0<4 * C::DQT + 1>();
-    else
+    if (step >= 2) {
+      if (rs_sent)  // uniform
+        wait_vmcnt_lgkm0<4 * C::DQT + 1>();
+      else
+        wait_vmcnt_lgkm0<4 * C::DQT>();
+    } else {
       wait_vmcnt_lgkm0<0>();
+    }
     __builtin_amdgcn_s_barrier();
     if (step + 1 < nsteps) issue(step + 1);  // its stage last served step - 1
     if (step >= 1) {
@@ -977,6 +1000,9 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_kernel(const f16* __restrict_
     const char* tO = tQ + C::OOFF;
     const char* tA = tQ + C::AOFF;
     char* tS = sdS[PAR];
+    // this step's row-sum flag (one affine row per lane; rows repeat when
+    // QT = 32), for the next step's rowsum()
+    const bool rs_flag_here = __ballot((float)*reinterpret_cast<const f16*>(tA + 16 * lane + 4) != 0.f) != 0;
     // S = Q~ K~^T and dP - delta = dO~ V~^T of sub-block sb (rows: queries in
     // swap23 order; lane: key)
     auto scores = [&](int sb, f32x16& s, f32x16& dp) {
@@ -1072,6 +1098,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_kernel(const f16* __restrict_
       }
     }
     if (step >= 1) dq_finish(step - 1);
+    rs_need = rs_flag_here;
   };
 
   if (nsteps > 0) issue(0);
