@@ -320,16 +320,19 @@ hipError_t launch_proj_fwd(const Dims& d, const f16* X, const f16* gq, const f16
 // operands (phi_hi of t, the codes both products used, and 1), and the row
 // sum becomes r_t - c. P_tt = 2^(s_tt - lse_t) (s_tt = t_tt + b_t from the
 // projection's statistics) comes from bwd_prep, next to r_t.
-// A block covers kGateTokensPerBlock tokens and 256 projection columns. Each
-// thread owns 8 consecutive columns (one head) and every 8th token of the
-// block, so all loads and stores are 16-byte vectors: a wave covers 32
-// column groups of 2 tokens, i.e. whole 512-byte dZ rows and, per head, 2
-// consecutive rows of dq / dk. The per-thread gate sums meet in LDS in a
-// fixed order.
-__global__ __launch_bounds__(256) void proj_bwd_elem_kernel(const f16* __restrict__ gate_q,
-                                                            const f16* __restrict__ gate_k, Dims d, ProjBuffers p,
-                                                            BwdBuffers g, int row_corr) {
-  __shared__ float red[8][257];
+// A block of kElemThreads threads covers kGateTokensPerBlock tokens and 256
+// projection columns. Each thread owns 8 consecutive columns (one head) and
+// every kElemSubs-th token of the block, so all loads and stores are 16-byte
+// vectors: a wave covers 32 column groups of 2 tokens, i.e. whole 512-byte dZ
+// rows and, per head, 2 consecutive rows of dq / dk. The per-thread gate sums
+// meet in LDS in a fixed order. (1024 threads: with a few thousand blocks in
+// all, 256-thread blocks left one wave per SIMD to cover the memory latency.)
+constexpr int kElemThreads = 1024, kElemSubs = kElemThreads / 32;
+static_assert(kGateTokensPerBlock % kElemSubs == 0, "whole tokens per thread");
+__global__ __launch_bounds__(kElemThreads) void proj_bwd_elem_kernel(const f16* __restrict__ gate_q,
+                                                                     const f16* __restrict__ gate_k, Dims d,
+                                                                     ProjBuffers p, BwdBuffers g, int row_corr) {
+  __shared__ float red[kElemSubs][257];
   const int c8 = threadIdx.x & 31, sub = threadIdx.x >> 5;
   const int col = blockIdx.y * 256 + 8 * c8;  // first of this thread's 8 columns
   const bool active = col < d.HM;
@@ -341,9 +344,9 @@ __global__ __launch_bounds__(256) void proj_bwd_elem_kernel(const f16* __restric
 #pragma unroll
     for (int e = 0; e < 8; ++e) sG[e] = d.scale * (float)gate_q[col + e] * (float)gate_k[col + e];
     const int64_t t0 = (int64_t)blockIdx.x * kGateTokensPerBlock;
-#pragma unroll 2
-    for (int k = 0; k < kGateTokensPerBlock / 8; ++k) {
-      const int64_t t = t0 + sub + 8 * k;
+#pragma unroll
+    for (int k = 0; k < kGateTokensPerBlock / kElemSubs; ++k) {
+      const int64_t t = t0 + sub + kElemSubs * k;
       if (t >= d.T) break;
       const int b = (int)(t / d.N), n = (int)(t - (int64_t)b * d.N);
       const int64_t bhn = (int64_t)(b * d.H + h) * d.N + n;
@@ -379,10 +382,10 @@ __global__ __launch_bounds__(256) void proj_bwd_elem_kernel(const f16* __restric
   for (int e = 0; e < 8; ++e) red[sub][8 * c8 + e] = sg[e];
   __syncthreads();
   const int cc = blockIdx.y * 256 + threadIdx.x;
-  if (cc < d.HM) {
+  if (threadIdx.x < 256 && cc < d.HM) {
     float s = 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) s += red[i][threadIdx.x];
+    for (int i = 0; i < kElemSubs; ++i) s += red[i][threadIdx.x];
     g.gpart[(int64_t)blockIdx.x * d.HM + cc] = s;
   }
 }
@@ -390,7 +393,7 @@ __global__ __launch_bounds__(256) void proj_bwd_elem_kernel(const f16* __restric
 hipError_t launch_proj_bwd_elem(const Dims& d, const f16* gq, const f16* gk, const ProjBuffers& p,
                                 const BwdBuffers& g, bool row_corr, hipStream_t s) {
   dim3 grid((unsigned)((d.T + kGateTokensPerBlock - 1) / kGateTokensPerBlock), (d.HM + 255) / 256);
-  hipLaunchKernelGGL(proj_bwd_elem_kernel, grid, dim3(256), 0, s, gq, gk, d, p, g, row_corr ? 1 : 0);
+  hipLaunchKernelGGL(proj_bwd_elem_kernel, grid, dim3(kElemThreads), 0, s, gq, gk, d, p, g, row_corr ? 1 : 0);
   return hipGetLastError();
 }
 
@@ -552,9 +555,19 @@ __global__ __launch_bounds__(256) void dw_reduce_kernel(const float* __restrict_
   const int64_t total = (int64_t)D * NC;
   const int64_t idx = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
   if (idx >= total) return;
+  // splits summed in order; the loads of 8 splits are issued before their adds
   float4 s = *reinterpret_cast<const float4*>(wpart + idx);
-#pragma unroll 4
-  for (int z = 1; z < splits; ++z) {  // unrolled: several loads in flight, same order
+  int z = 1;
+  for (; z + 8 <= splits; z += 8) {
+    float4 v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = *reinterpret_cast<const float4*>(wpart + (int64_t)(z + i) * total + idx);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      s.x += v[i].x; s.y += v[i].y; s.z += v[i].z; s.w += v[i].w;
+    }
+  }
+  for (; z < splits; ++z) {
     const float4 v = *reinterpret_cast<const float4*>(wpart + (int64_t)z * total + idx);
     s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
   }
