@@ -109,7 +109,6 @@ hipError_t launch_bwd_gemm(const Dims& d, const ProjBuffers& p, const BwdBuffers
 hipError_t launch_dw_reduce(const Dims& d, const BwdBuffers& g, const _Float16* gate_q, const _Float16* gate_k,
                             _Float16* dW_phi, _Float16* dW_V, _Float16* d_gate_q, _Float16* d_gate_k, hipStream_t s);
 int dw_splits(const Dims& d);
-__host__ __device__ int dw_tiles(const Dims& d);
 
 // kernels_attn.hip
 hipError_t launch_attn_fwd(const Dims& d, const ProjBuffers& p, _Float16* out, float* lse, hipStream_t s);

@@ -407,14 +407,22 @@ hipError_t launch_proj_bwd_elem(const Dims& d, const f16* gq, const f16* gk, con
 // round-robin over the 8 XCDs, so the tiles of one split share their X and
 // dZ|dV panels in one L2) and stores an fp32 partial; dw_reduce sums the
 // partials in split order.
-using DxGemm = Gemm<256, 256, 4, true, true, 64, 2>;    // A = dZ|dV [T][NC], B = wcat = [W_phi | W_V] [D][NC]
-using DwGemm = Gemm<256, 256, 4, false, false, 64, 2>;  // A = X (k-major) [T][D], B = dZ|dV (k-major) [T][NC]
-constexpr int kDxBM = 256, kDxBN = 256, kDwBM = 256, kDwBN = 256;
-constexpr int kBwdLds = DxGemm::kLdsBytes > DwGemm::kLdsBytes ? DxGemm::kLdsBytes : DwGemm::kLdsBytes;
-constexpr int kDxStageStride = kDxBN + 8;  // halves: one 64-row slab of fp16 dX for 16-byte stores
-static_assert(64 * kDxStageStride * 2 <= kBwdLds, "dX slab must fit the main loop's LDS");
-
-__host__ __device__ int dw_tiles(const Dims& d) { return ((d.D + kDwBM - 1) / kDwBM) * ((d.HM + d.D + kDwBN - 1) / kDwBN); }
+// Square BT x BT tiles for both products: 256, or 128 when the 256 tiles (dX
+// tiles plus dW tiles times splits) would not fill one round of the 256 CUs
+// (few tokens: B8 N1024 D512 H8 m16 has 160 large workgroups, 576 small ones).
+// Either way the waves own 64-row wave tiles, which the dX epilogue's slabs
+// rely on.
+template <int BT>
+struct BwdTiles {
+  static constexpr int WM = BT == 256 ? 4 : 2;
+  using Dx = Gemm<BT, BT, WM, true, true, 64, 2>;    // A = dZ|dV [T][NC], B = wcat = [W_phi | W_V] [D][NC]
+  using Dw = Gemm<BT, BT, WM, false, false, 64, 2>;  // A = X (k-major) [T][D], B = dZ|dV (k-major) [T][NC]
+  static constexpr int kLds = Dx::kLdsBytes > Dw::kLdsBytes ? Dx::kLdsBytes : Dw::kLdsBytes;
+  static constexpr int kStageStride = BT + 8;  // halves: one 64-row slab of fp16 dX for 16-byte stores
+  static_assert(64 * kStageStride * 2 <= kLds, "dX slab must fit the main loop's LDS");
+  static_assert(Dx::WN == Dw::WN && Dx::WTM == 64 && Dw::WTM == 64, "shared wave grid, 64-row wave tiles");
+};
+static int dw_tiles(const Dims& d, int bt) { return ((d.D + bt - 1) / bt) * ((d.HM + d.D + bt - 1) / bt); }
 // Splits of the token (k) range: a multiple of 8, so that every XCD gets the
 // same number of splits (split z runs on XCD z % 8), with about as many
 // k-steps per dW split as a dX tile has (T / S ~ H m + D tokens, so the two
@@ -429,18 +437,28 @@ int dw_splits(const Dims& d) {
   return r < 1 ? 1 : r;
 }
 
+static int bwd_gemm_tile(const Dims& d) {
+  const int S = dw_splits(d), T = (int)d.T;
+  const int large = 8 * dw_tiles(d, 256) * ((S + 7) / 8) + (int)gemm_tile_grid((T + 255) / 256, (d.D + 255) / 256);
+  return large < 256 && d.D % 128 == 0 && (d.HM + d.D) % 128 == 0 ? 128 : 256;
+}
+
 struct BwdGemmArgs {
   const f16* X;
   const f16* wcat;
   f16* dX;
-  int n_dw, n_dx, kchunk;
+  int n_dw, n_dx, kchunk, dw_tiles;
 };
 
+template <int BT>
 __global__ __launch_bounds__(kGemmThreads) void bwd_gemm_kernel(Dims d, BwdBuffers g, BwdGemmArgs a) {
-  __shared__ __align__(16) char smem[kBwdLds];
+  using DxGemm = typename BwdTiles<BT>::Dx;
+  using DwGemm = typename BwdTiles<BT>::Dw;
+  constexpr int kDxBM = BT, kDxBN = BT, kDwBM = BT, kDwBN = BT;
+  constexpr int kDxStageStride = BwdTiles<BT>::kStageStride;
+  __shared__ __align__(16) char smem[BwdTiles<BT>::kLds];
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = w / DxGemm::WN, wn = w % DxGemm::WN;  // same wave grid for dX and dW
-  static_assert(DxGemm::WN == DwGemm::WN && DxGemm::WTM == 64, "shared wave grid, 64-row wave tiles");
   const int NC = d.HM + d.D;
   const int T = (int)d.T;
   const int id = blockIdx.x;
@@ -479,7 +497,7 @@ __global__ __launch_bounds__(kGemmThreads) void bwd_gemm_kernel(Dims d, BwdBuffe
   }
 
   // ---- dW split-K tile
-  const int ntn = (NC + kDwBN - 1) / kDwBN, tiles = dw_tiles(d);
+  const int ntn = (NC + kDwBN - 1) / kDwBN, tiles = a.dw_tiles;
   const int xcd = id & 7, slot = id >> 3;
   const int tl = slot % tiles, z = xcd + 8 * (slot / tiles);
   if (z >= g.splits) return;
@@ -506,11 +524,17 @@ hipError_t launch_bwd_gemm(const Dims& d, const ProjBuffers& p, const BwdBuffers
                            hipStream_t s) {
   BwdGemmArgs a;
   a.X = X; a.wcat = p.wcat; a.dX = dX;
-  const int S = g.splits, T = (int)d.T;
-  a.kchunk = ((T + S - 1) / S + DwGemm::kBK - 1) / DwGemm::kBK * DwGemm::kBK;
-  a.n_dw = 8 * dw_tiles(d) * ((S + 7) / 8);
-  a.n_dx = (int)gemm_tile_grid((T + kDxBM - 1) / kDxBM, (d.D + kDxBN - 1) / kDxBN);
-  hipLaunchKernelGGL(bwd_gemm_kernel, dim3((unsigned)(a.n_dw + a.n_dx)), dim3(kGemmThreads), 0, s, d, g, a);
+  const int S = g.splits, T = (int)d.T, bt = bwd_gemm_tile(d);
+  constexpr int kBK = BwdTiles<256>::Dw::kBK;
+  static_assert(BwdTiles<128>::Dw::kBK == kBK, "one k-step for both tile sizes");
+  a.kchunk = ((T + S - 1) / S + kBK - 1) / kBK * kBK;
+  a.dw_tiles = dw_tiles(d, bt);
+  a.n_dw = 8 * a.dw_tiles * ((S + 7) / 8);
+  a.n_dx = (int)gemm_tile_grid((T + bt - 1) / bt, (d.D + bt - 1) / bt);
+  if (bt == 128)
+    hipLaunchKernelGGL(bwd_gemm_kernel<128>, dim3((unsigned)(a.n_dw + a.n_dx)), dim3(kGemmThreads), 0, s, d, g, a);
+  else
+    hipLaunchKernelGGL(bwd_gemm_kernel<256>, dim3((unsigned)(a.n_dw + a.n_dx)), dim3(kGemmThreads), 0, s, d, g, a);
   return hipGetLastError();
 }
 
