@@ -679,33 +679,42 @@ struct BwdCfg {
   static constexpr int ORB = 2 * DV;
   static constexpr int SRB = 2 * QT;
   static constexpr int PRB = 2 * (M < 32 ? 32 : M);
-  static constexpr int KW = 128;                // keys per workgroup (4 waves x 32)
-  static constexpr int DQT = (QT / 16) * (M / 16) / 4;  // 16x16 dq tiles per wave per step
+  // Waves per workgroup, 32 keys each. Every workgroup adds one fp32 atomic
+  // per (query, code) of each step to dq, so the atomic count scales with the
+  // number of key blocks: at m = 64 (64 codes per query) 8 waves (256 keys)
+  // halve it, at one workgroup (two waves per SIMD) per CU.
+  static constexpr int NW = M == 64 && DV <= 64 ? 8 : 4;
+  static constexpr int NT = 64 * NW;                      // threads
+  static constexpr int KW = 32 * NW;                      // keys per workgroup
+  static constexpr int DQT = (QT / 16) * (M / 16) / NW;  // 16x16 dq tiles per wave per step
+  static_assert((QT / 16) * (M / 16) % NW == 0, "dq tiles must split evenly over the waves");
   // a stage = query tile, dO tile, affine tile; 1 KiB DMA pieces
   static constexpr int QP = QT * QRB / 1024, OP = QT * ORB / 1024;
-  static constexpr int QPW = QP / 4, OPW = (OP + 3) / 4;  // pieces per wave (dO: the first OP % 4 waves)
-  static_assert(QP % 4 == 0, "query pieces must split evenly over the waves");
+  static constexpr int QPW = QP / NW, OPW = (OP + NW - 1) / NW;  // pieces per wave (dO: the first OP % NW waves)
+  static_assert(QP % NW == 0, "query pieces must split evenly over the waves");
+  static constexpr int MIN_WG = NW == 4 ? 2 : 1;  // workgroups per CU (launch bound)
   static constexpr int OOFF = QT * QRB, AOFF = OOFF + QT * ORB;  // bytes
   static constexpr int STAGE = AOFF + 1024;
 };
 
-// Key-side (KV-outer) backward. A workgroup owns 128 keys (32 per wave, kept in
-// registers: codes, V_hi, dk / dV accumulators) and streams the query steps
-// of QT queries through two LDS stages filled by DMA. Step s:
+// Key-side (KV-outer) backward. A workgroup owns KW = 32 NW keys (32 per
+// wave, kept in registers: codes, V_hi, dk / dV accumulators) and streams the
+// query steps of QT queries through two LDS stages filled by DMA. Step s:
 //   wait for its tiles, barrier (also publishes dS^T of step s - 1), DMA the
 //   tiles of step s + 1, read the dq fragments of step s - 1, compute step s
 //   (S, dP, P, dS, dV += dO^T P, dk^T += phi^T dS, dS^T -> LDS), then finish
 //   dq of step s - 1 (MFMA over the workgroup's keys, fp32 atomics).
-// Every wave issues exactly 4 DQT + 1 atomics per step (masked lanes add 0.0 to
-// a valid address), so the tile wait can leave the latest step's atomics in
-// flight: vector-memory operations complete in issue order. The extra one
-// adds the row sums of dS of step s - 1 (over the workgroup's keys) to dr.
+// Every wave issues exactly 4 DQT dq atomics per step (masked lanes add 0.0 to
+// a valid address), plus one that adds the row sums of dS of step s - 1 (over
+// the workgroup's keys) to dr when that step has a flagged row, so the tile
+// wait can leave the latest step's atomics in flight: vector-memory
+// operations complete in issue order.
 // The query rows come from the projection's code rows, whose affine block
 // holds {1, 1, -(lse - b)} by now (written by the forward, or by bwd_prep when
 // the backward computed the projection itself); the dO rows come from
 // grad_out and their affine block {-delta} from bwd_prep's aug rows.
 template <int M, int DV, bool MD>
-__global__ __launch_bounds__(256, 2) void attn_bwd_kernel(const f16* __restrict__ qa, const f16* __restrict__ ka,
+__global__ __launch_bounds__((BwdCfg<M, DV>::NT), (BwdCfg<M, DV>::MIN_WG)) void attn_bwd_kernel(const f16* __restrict__ qa, const f16* __restrict__ ka,
                                                        const f16* __restrict__ vt, const f16* __restrict__ aug,
                                                        const f16* __restrict__ grad_out, float* __restrict__ dq,
                                                        float* __restrict__ dk, float* __restrict__ dcb,
@@ -753,7 +762,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_kernel(const f16* __restrict_
   }
   const f16x4 vaug = h32 == 0 ? f16x4{one, one, zero, zero} : f16x4{zero, zero, zero, zero};
   // phi_hi of the workgroup's keys for the dq product (zero past N)
-  for (int v = tid; v < C::KW * (M / 8); v += 256) {
+  for (int v = tid; v < C::KW * (M / 8); v += C::NT) {
     const int r = v / (M / 8), c = v % (M / 8);
     f16x8 x = {};
     if (k0 + r < N) x = *reinterpret_cast<const f16x8*>(qa + (rowbase + k0 + r) * C::CW + 8 * c);
@@ -788,13 +797,13 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_kernel(const f16* __restrict_
   unsigned qoff[C::QPW], ooff[C::OPW], aoff;
 #pragma unroll
   for (int i = 0; i < C::QPW; ++i) {
-    const int q = 64 * (w + 4 * i) + lane, r = q / (C::QRB / 16);
+    const int q = 64 * (w + C::NW * i) + lane, r = q / (C::QRB / 16);
     const int c = (q % (C::QRB / 16)) ^ rswz<C::QRB>(r);
     qoff[i] = (unsigned)((srow23(r) * C::CW + (8 * c < C::CW ? 8 * c : 0)) * 2);
   }
 #pragma unroll
   for (int j = 0; j < C::OPW; ++j) {
-    const int q = 64 * min(w + 4 * j, C::OP - 1) + lane, r = q / (C::ORB / 16);
+    const int q = 64 * min(w + C::NW * j, C::OP - 1) + lane, r = q / (C::ORB / 16);
     const int c = (q % (C::ORB / 16)) ^ rswz<C::ORB>(r);
     ooff[j] = (unsigned)(((int64_t)srow23(r) * D + 8 * c) * 2);
   }
@@ -806,27 +815,27 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_kernel(const f16* __restrict_
     if (qs + C::QT <= N) {  // uniform
       const f16* qbase = qa + (rowbase + qs) * C::CW;
 #pragma unroll
-      for (int i = 0; i < C::QPW; ++i) lds_dma16_so(qbase, qoff[i], dst + 1024u * (unsigned)(w + 4 * i));
+      for (int i = 0; i < C::QPW; ++i) lds_dma16_so(qbase, qoff[i], dst + 1024u * (unsigned)(w + C::NW * i));
       const f16* obase = grad_out + (tokbase + qs) * D + h * DV;
 #pragma unroll
       for (int j = 0; j < C::OPW; ++j)
-        if (w + 4 * j < C::OP) lds_dma16_so(obase, ooff[j], dst + C::OOFF + 1024u * (unsigned)(w + 4 * j));
+        if (w + C::NW * j < C::OP) lds_dma16_so(obase, ooff[j], dst + C::OOFF + 1024u * (unsigned)(w + C::NW * j));
       if (w == 0) lds_dma16_so(aug + (rowbase + qs) * 8, aoff, dst + C::AOFF);
     } else {  // ragged last step: rows past N read row N - 1 (every score they feed is masked)
 #pragma unroll
       for (int i = 0; i < C::QPW; ++i) {
-        const int q = 64 * (w + 4 * i) + lane, r = q / (C::QRB / 16);
+        const int q = 64 * (w + C::NW * i) + lane, r = q / (C::QRB / 16);
         const int c = (q % (C::QRB / 16)) ^ rswz<C::QRB>(r);
         const int qrow = min(qs + srow23(r), N - 1);
-        lds_dma16(qa + (rowbase + qrow) * C::CW + (8 * c < C::CW ? 8 * c : 0), dst + 1024u * (unsigned)(w + 4 * i));
+        lds_dma16(qa + (rowbase + qrow) * C::CW + (8 * c < C::CW ? 8 * c : 0), dst + 1024u * (unsigned)(w + C::NW * i));
       }
 #pragma unroll
       for (int j = 0; j < C::OPW; ++j)
-        if (w + 4 * j < C::OP) {
-          const int q = 64 * (w + 4 * j) + lane, r = q / (C::ORB / 16);
+        if (w + C::NW * j < C::OP) {
+          const int q = 64 * (w + C::NW * j) + lane, r = q / (C::ORB / 16);
           const int c = (q % (C::ORB / 16)) ^ rswz<C::ORB>(r);
           const int qrow = min(qs + srow23(r), N - 1);
-          lds_dma16(grad_out + (tokbase + qrow) * D + h * DV + 8 * c, dst + C::OOFF + 1024u * (unsigned)(w + 4 * j));
+          lds_dma16(grad_out + (tokbase + qrow) * D + h * DV + 8 * c, dst + C::OOFF + 1024u * (unsigned)(w + C::NW * j));
         }
       if (w == 0)
         lds_dma16(aug + (rowbase + min(qs + srow23(lane % C::QT), N - 1)) * 8, dst + C::AOFF);
@@ -877,14 +886,14 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_kernel(const f16* __restrict_
   const int sz = rswz<C::SRB>(kr);
 
   // ---- dq[q][code] += sum_key dS[q][key] phi[key][code]: 16 x 16 output
-  // tiles split over the waves, contraction over all 128 keys of the workgroup
-  // (rows past N are zero in both operands). The phi operand never changes:
-  // it is read once.
+  // tiles split over the waves, contraction over all KW keys of the workgroup
+  // (rows past N are zero in both operands). The phi operand never changes;
+  // it is re-read from the phi tile each step (registers are the scarcer).
   f16x8 dqa[C::DQT][C::KW / 32];
   int d_s[C::DQT][2];
 #pragma unroll
   for (int t = 0; t < C::DQT; ++t) {
-    const int tile = w + 4 * t;
+    const int tile = w + C::NW * t;
     const int qt = tile % (C::QT / 16), ct = tile / (C::QT / 16);
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
@@ -911,13 +920,13 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_kernel(const f16* __restrict_
   int a_off[C::DQT];
 #pragma unroll
   for (int t = 0; t < C::DQT; ++t) {
-    const int tile = w + 4 * t;
+    const int tile = w + C::NW * t;
     const int qt = tile % (C::QT / 16), ct = tile / (C::QT / 16);
     a_off[t] = (16 * qt + 4 * (lane >> 4)) * M + 16 * ct + (lane & 15);
   }
   // Row sums sum_j dS[q][j] over the workgroup's keys: the A fragments of the
-  // tile (qt, ct = 0) times a ones operand on the MFMA (tile w of the wave that
-  // owns it: all waves when M <= 32, waves 0 and 1 when M = 64, QT = 32). Every
+  // tile (qt, ct = 0) times a ones operand on the MFMA (tile w of the waves
+  // w < QT / 16 that own such a tile). Every
   // column of the 16 x 16 result holds the row sums; lanes with (lane & 15) < 4
   // add rows 4 (lane / 16) + (lane & 3) to dr, one atomic per row. The other
   // waves add 0 there, so every wave issues one such atomic.
@@ -926,7 +935,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_kernel(const f16* __restrict_
   // row gets the sums of all key blocks) forms its sums; the others issue
   // neither the MFMAs nor the atomic, and the tile wait of the step after
   // next allows one atomic fewer in flight.
-  const bool rs_wave = C::QT / 16 >= 4 || w < C::QT / 16;  // uniform
+  const bool rs_wave = w < C::QT / 16;  // uniform: tile w is the (qt, ct = 0) tile
   const int rs_row = 16 * (w % (C::QT / 16)) + 4 * (lane >> 4) + (lane & 3);
   bool rs_need = false;  // the flag of the step whose sums rowsum() forms next
   bool rs_sent = false;  // whether the previous step issued a row-sum atomic
@@ -955,7 +964,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_kernel(const f16* __restrict_
     const bool full = qs + C::QT <= N;  // uniform
 #pragma unroll
     for (int t = 0; t < C::DQT; ++t) {
-      const int tile = w + 4 * t;
+      const int tile = w + C::NW * t;
       const int qt = tile % (C::QT / 16);
       f32x4 acc = {};
 #pragma unroll
@@ -969,7 +978,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_kernel(const f16* __restrict_
           const int qq = qs + 16 * qt + 4 * (lane >> 4) + r;
           const bool ok = qq < N;
           // always issued (a fixed count per step); rows past N add 0 to row N - 1
-          unsafeAtomicAdd(dq + (rowbase + (ok ? qq : N - 1)) * M + 16 * ((w + 4 * t) / (C::QT / 16)) + (lane & 15),
+          unsafeAtomicAdd(dq + (rowbase + (ok ? qq : N - 1)) * M + 16 * ((w + C::NW * t) / (C::QT / 16)) + (lane & 15),
                           ok ? acc[r] : 0.f);
         }
       }
@@ -1151,10 +1160,10 @@ static hipError_t launch_attn_bwd_t(const Dims& d, const ProjBuffers& p, const f
   using C = BwdCfg<M, DV>;
   const dim3 grid(xcd_grid((d.N + C::KW - 1) / C::KW, d.B * d.H));
   if (d.mask_diag)
-    hipLaunchKernelGGL((attn_bwd_kernel<M, DV, true>), grid, dim3(256), 0, s, p.qa, p.ka, p.vt, g.aug, grad_out, g.dq,
+    hipLaunchKernelGGL((attn_bwd_kernel<M, DV, true>), grid, dim3(C::NT), 0, s, p.qa, p.ka, p.vt, g.aug, grad_out, g.dq,
                        g.dk, g.dcb, g.dr, g.dzv, d.N, d.NP, d.H, d.D, d.HM, d.B * d.H, d.causal);
   else
-    hipLaunchKernelGGL((attn_bwd_kernel<M, DV, false>), grid, dim3(256), 0, s, p.qa, p.ka, p.vt, g.aug, grad_out, g.dq,
+    hipLaunchKernelGGL((attn_bwd_kernel<M, DV, false>), grid, dim3(C::NT), 0, s, p.qa, p.ka, p.vt, g.aug, grad_out, g.dq,
                        g.dk, g.dcb, g.dr, g.dzv, d.N, d.NP, d.H, d.D, d.HM, d.B * d.H, d.causal);
   return hipGetLastError();
 }
