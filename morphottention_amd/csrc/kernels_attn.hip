@@ -681,13 +681,16 @@ struct BwdCfg {
   static constexpr int PRB = 2 * (M < 32 ? 32 : M);
   // Waves per workgroup, 32 keys each. Every workgroup adds one fp32 atomic
   // per (query, code) of each step to dq, so the atomic count scales with the
-  // number of key blocks: at m = 64 (64 codes per query) 8 waves (256 keys)
-  // halve it, at one workgroup (two waves per SIMD) per CU.
-  static constexpr int NW = M == 64 && DV <= 64 ? 8 : 4;
+  // number of key blocks: at m = 32 and 64 8 waves (256 keys) halve it, at
+  // one workgroup (two waves per SIMD) per CU.
+  static constexpr int NW = M >= 32 && DV <= 64 ? 8 : 4;
   static constexpr int NT = 64 * NW;                      // threads
   static constexpr int KW = 32 * NW;                      // keys per workgroup
-  static constexpr int DQT = (QT / 16) * (M / 16) / NW;  // 16x16 dq tiles per wave per step
-  static_assert((QT / 16) * (M / 16) % NW == 0, "dq tiles must split evenly over the waves");
+  // 16x16 dq tiles of a step, and per wave: when there are fewer tiles than
+  // waves (m = 32: 4 tiles, 8 waves) the waves w >= DQTILES have no dq work.
+  static constexpr int DQTILES = (QT / 16) * (M / 16);
+  static constexpr int DQT = DQTILES >= NW ? DQTILES / NW : 1;
+  static_assert(DQTILES < NW || DQTILES % NW == 0, "dq tiles must split evenly over the waves");
   // a stage = query tile, dO tile, affine tile; 1 KiB DMA pieces
   static constexpr int QP = QT * QRB / 1024, OP = QT * ORB / 1024;
   static constexpr int QPW = QP / NW, OPW = (OP + NW - 1) / NW;  // pieces per wave (dO: the first OP % NW waves)
@@ -704,11 +707,11 @@ struct BwdCfg {
 //   tiles of step s + 1, read the dq fragments of step s - 1, compute step s
 //   (S, dP, P, dS, dV += dO^T P, dk^T += phi^T dS, dS^T -> LDS), then finish
 //   dq of step s - 1 (MFMA over the workgroup's keys, fp32 atomics).
-// Every wave issues exactly 4 DQT dq atomics per step (masked lanes add 0.0 to
-// a valid address), plus one that adds the row sums of dS of step s - 1 (over
-// the workgroup's keys) to dr when that step has a flagged row, so the tile
-// wait can leave the latest step's atomics in flight: vector-memory
-// operations complete in issue order.
+// Every wave with dq tiles issues exactly 4 DQT dq atomics per step (masked
+// lanes add 0.0 to a valid address), and every wave one that adds the row
+// sums of dS of step s - 1 (over the workgroup's keys) to dr when that step
+// has a flagged row, so the tile wait can leave the latest step's atomics in
+// flight: vector-memory operations complete in issue order.
 // The query rows come from the projection's code rows, whose affine block
 // holds {1, 1, -(lse - b)} by now (written by the forward, or by bwd_prep when
 // the backward computed the projection itself); the dO rows come from
@@ -909,7 +912,10 @@ __global__ __launch_bounds__((BwdCfg<M, DV>::NT), (BwdCfg<M, DV>::MIN_WG)) void 
   wait_vmcnt<0>();
   __syncthreads();  // sPk is complete
 
+  // waves with dq tiles (wave-uniform); the others issue no dq atomics
+  const bool dq_wave = w < C::DQTILES;
   auto dq_load = [&](const char* sd) {
+    if (!dq_wave) return;
 #pragma unroll
     for (int t = 0; t < C::DQT; ++t)
 #pragma unroll
@@ -959,6 +965,7 @@ __global__ __launch_bounds__((BwdCfg<M, DV>::NT), (BwdCfg<M, DV>::MIN_WG)) void 
       unsafeAtomicAdd(&dr[2 * (rowbase + (qq < N ? qq : N - 1))], rs_wave && qq < N ? rsum : 0.f);
   };
   auto dq_finish = [&](int st) {
+    if (!dq_wave) return;
     const int qs = qstep(st);
     float* base = dq + (rowbase + qs) * M;
     const bool full = qs + C::QT <= N;  // uniform
@@ -993,10 +1000,17 @@ __global__ __launch_bounds__((BwdCfg<M, DV>::NT), (BwdCfg<M, DV>::MIN_WG)) void 
     // this step's tiles have landed (the atomics of step - 2, issued after
     // them, may still be in flight) and this wave's dS^T writes are done
     if (step >= 2) {
-      if (rs_sent)  // uniform
-        wait_vmcnt_lgkm0<4 * C::DQT + 1>();
-      else
-        wait_vmcnt_lgkm0<4 * C::DQT>();
+      if (dq_wave) {  // uniform
+        if (rs_sent)
+          wait_vmcnt_lgkm0<4 * C::DQT + 1>();
+        else
+          wait_vmcnt_lgkm0<4 * C::DQT>();
+      } else {
+        if (rs_sent)
+          wait_vmcnt_lgkm0<1>();
+        else
+          wait_vmcnt_lgkm0<0>();
+      }
     } else {
       wait_vmcnt_lgkm0<0>();
     }
