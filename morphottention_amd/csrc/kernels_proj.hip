@@ -138,36 +138,40 @@ __global__ __launch_bounds__(kGemmThreads) void proj_fwd_kernel(const f16* __res
     }
     __syncthreads();
     const int row0 = m0 + 64 * slab;
-    // soft-hypercube codes: one (token, head) per item (a head's M columns
-    // are contiguous in both column orders)
-    constexpr int kHeadsPerTile = BN / M;
-    for (int idx = tid; idx < 64 * kHeadsPerTile; idx += kGemmThreads) {
-      const int hh = idx / 64, r = idx % 64;
+    // soft-hypercube codes: one (token, head, 8-code chunk) per thread; the
+    // M / 8 chunks of a (token, head) sit on consecutive lanes, which meet in
+    // xor shuffles for the row sums (a head's M columns are contiguous in
+    // both column orders). One thread per (token, head) had left 3/4 of the
+    // workgroup idle at m = 64.
+    constexpr int kHeadsPerTile = BN / M, kChunks = M / 8;
+    static_assert(kGemmThreads % kChunks == 0, "a (token, head) never straddles two passes");
+    for (int idx = tid; idx < 64 * kHeadsPerTile * kChunks; idx += kGemmThreads) {
+      const int j = idx % kChunks, item = idx / kChunks;
+      const int hh = item / 64, r = item % 64;
       const int col0 = proj_col(d, tn, hh * M);
       const int t = row0 + r;
-      if (col0 >= d.HM || t >= T) continue;
+      const bool active = col0 < d.HM && t < T;  // the same for every chunk of the item
       const int h = col0 / M;
       const int b = t / d.N, n = t - b * d.N;
       const int64_t bhn = (int64_t)(b * d.H + h) * d.N + n;
-      const float* z = stage + r * SS + hh * M;
-      f16* qrow = p.qa + bhn * CW;
-      f16* krow = p.ka + bhn * CW;
+      const int c8 = 8 * j;
       float sumb = 0.f, tii = 0.f, U = 0.f;
-#pragma unroll
-      for (int c8 = 0; c8 < M; c8 += 8) {
+      if (active) {
+        const float* z = stage + r * SS + hh * M + c8;
+        const f16x8 gq8 = *reinterpret_cast<const f16x8*>(gate_q + h * M + c8);
+        const f16x8 gk8 = *reinterpret_cast<const f16x8*>(gate_k + h * M + c8);
         f16x8 phh, phl, kch, kcl;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const int c = c8 + e;
-          const float phi = GEN ? cube_project(z[c], d.proj) : sigmoidf_(z[c]);
-          const float G = (float)gate_q[h * M + c] * (float)gate_k[h * M + c];
+          const float phi = GEN ? cube_project(z[e], d.proj) : sigmoidf_(z[e]);
+          const float G = (float)gq8[e] * (float)gk8[e];
           const float wgt = d.scale * G;
           const float cg = c1 * G;
-          f16 a, b;
+          f16 a, bb;
           if (GEN) {  // HardTanh01's clamped fma could convert to fp16 in one rounding
-            split_exact(phi, a, b);
+            split_exact(phi, a, bb);
             phh[e] = a;
-            phl[e] = b;
+            phl[e] = bb;
           } else {  // a quotient: nothing to fuse the conversion with
             phh[e] = (f16)phi;
             phl[e] = (f16)(phi - (float)phh[e]);
@@ -182,11 +186,20 @@ __global__ __launch_bounds__(kGemmThreads) void proj_fwd_kernel(const f16* __res
           U += fmaxf(0.f, wgt * (2.f * phi - 1.f));
         }
         // rows: [phi_hi | aug | phi_lo] and [kc_hi | aug | kc_lo]
+        f16* qrow = p.qa + bhn * CW;
+        f16* krow = p.ka + bhn * CW;
         *reinterpret_cast<f16x8*>(qrow + c8) = phh;
         *reinterpret_cast<f16x8*>(qrow + M + 8 + c8) = phl;
         *reinterpret_cast<f16x8*>(krow + c8) = kch;
         *reinterpret_cast<f16x8*>(krow + M + 8 + c8) = kcl;
       }
+#pragma unroll
+      for (int sh = 1; sh < kChunks; sh <<= 1) {  // the item's lanes are all active or all idle
+        sumb += __shfl_xor(sumb, sh);
+        tii += __shfl_xor(tii, sh);
+        U += __shfl_xor(U, sh);
+      }
+      if (!active || j != 0) continue;
       // base-2 quantities: token bias b = -log2e * sum_c w_c phi_c; self score
       // t_ii and the upper bound U of any score in this query's row (without
       // the row constant, which cancels in the softmax). U bounds the row only
@@ -203,8 +216,8 @@ __global__ __launch_bounds__(kGemmThreads) void proj_fwd_kernel(const f16* __res
       split_hi_lo(-R, rh, rl);
       split_hi_lo(bias, bh_, bl_);
       const f16 one = (f16)1.f, zero = (f16)0.f;
-      *reinterpret_cast<f16x8*>(qrow + M) = f16x8{one, one, rh, rl, zero, zero, zero, zero};
-      *reinterpret_cast<f16x8*>(krow + M) = f16x8{bh_, bl_, one, one, zero, zero, zero, zero};
+      *reinterpret_cast<f16x8*>(p.qa + bhn * CW + M) = f16x8{one, one, rh, rl, zero, zero, zero, zero};
+      *reinterpret_cast<f16x8*>(p.ka + bhn * CW + M) = f16x8{bh_, bl_, one, one, zero, zero, zero, zero};
       p.tstat[bhn] = make_float4(bias, R, gap, t_ii);
     }
     // values, transposed: vt[bh][dd][n] = V_hi, and the remainder V - V_hi as
