@@ -216,6 +216,21 @@ def test_shape_matrix(m, dv, causal):
           *oracle(x, params, H, m, 0.8, causal, dout))
 
 
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+@pytest.mark.parametrize("m,dv", [(32, 64), (64, 32), (64, 64)])
+def test_eight_wave_backward_key_blocks(m, dv, causal):
+    """At m = 32 and 64 (dv <= 64) a backward workgroup has eight waves and
+    owns 256 keys, and at m = 32 only four of them have dq tiles. N = 300
+    gives two key blocks, the second ragged (44 keys, so waves past N), and
+    query steps of 32 that end ragged as well."""
+    B, N, H = 2, 300, 2
+    _say(f"[case] eight-wave backward m={m} dv={dv} causal={causal} N={N}")
+    x, params, dout = make_inputs(B, N, H * dv, H, m, seed=400 + m + dv, gates=(1.0, 0.4))
+    out, lse, grads = run_hip(x, params, H, m, 0.8, causal, dout)
+    check(f"eight-wave m{m} dv{dv} {'causal' if causal else 'full'}", out, lse, grads,
+          *oracle(x, params, H, m, 0.8, causal, dout))
+
+
 @pytest.mark.parametrize("N", [1, 2, 31, 33, 127, 129, 257])
 def test_ragged_lengths(N):
     B, H, m, dv = 3, 4, 16, 64
