@@ -437,14 +437,16 @@ struct BwdTiles {
 };
 static int dw_tiles(const Dims& d, int bt) { return ((d.D + bt - 1) / bt) * ((d.HM + d.D + bt - 1) / bt); }
 // Splits of the token (k) range: a multiple of 8, so that every XCD gets the
-// same number of splits (split z runs on XCD z % 8), with about as many
-// k-steps per dW split as a dX tile has (T / S ~ H m + D tokens, so the two
-// kinds of workgroup balance), and at least 256 tokens per split. Fewer than
-// 8 splits had left XCDs without dW work: C5 bwd_gemm 2.04 -> 0.91 ms, C4
-// 0.140 -> 0.107 ms, C3 0.124 -> 0.110 ms.
+// same number of splits (split z runs on XCD z % 8), with at least as many
+// k-steps per dW split as a dX tile has (T / S >= H m + D tokens), and at
+// least 256 tokens per split. Fewer than 8 splits had left XCDs without dW
+// work (C5 bwd_gemm 2.04 -> 0.91 ms, C4 0.140 -> 0.107 ms); rounding T / (8 NC)
+// down rather than to nearest halves the partials where it is 1.5 - 2
+// (B4 N4096 D1024 H16 m16: 8 instead of 16 splits, bwd_gemm 0.108 -> 0.099 ms
+// and dw_reduce 17 -> 11 us).
 int dw_splits(const Dims& d) {
   const int NC = d.HM + d.D, by_k = (int)((d.T + 255) / 256);
-  const int s8 = (int)((d.T + 4 * NC) / (8 * NC));  // round(T / (8 NC))
+  const int s8 = (int)(d.T / (8 * NC));  // floor(T / (8 NC))
   const int s = 8 * (s8 < 1 ? 1 : s8);
   const int r = s < by_k ? s : by_k;
   return r < 1 ? 1 : r;
