@@ -63,11 +63,15 @@ struct FwdCfg {
   // SM (small problems, fewer than two of the regular workgroups per CU): one
   // query block per wave, four waves, three workgroups per CU, so the launch
   // has twice the workgroups and still covers the CUs.
+  // W4 (m >= 32, dv <= 64, one block per wave): four-wave workgroups, two or
+  // three per CU (LDS permitting), rather than one of eight waves; the waves
+  // of a CU then wait at independent barriers (C4 forward -4.5 %, C5 -3 %).
   static constexpr int QB2 = (M <= 32 && DV <= 64 && M * DV <= 1024) ? 2 : 1;
   static constexpr bool SMALL = SM && QB2 == 2;
   static constexpr int QB = SMALL ? 1 : QB2;
-  static constexpr int WAVES = SMALL ? 4 : 8 / QB;
-  static constexpr int QW = 32 * QB * WAVES;  // 256 queries per workgroup
+  static constexpr bool W4 = QB2 == 1 && M >= 32 && DV <= 64;
+  static constexpr int WAVES = (SMALL || W4) ? 4 : 8 / QB;
+  static constexpr int QW = 32 * QB * WAVES;  // 128 or 256 queries per workgroup
   // A stage holds one key tile [KT][CW] (rows in swap23 order within each 32,
   // unpadded: CW = 8 (mod 16) halves keeps b128 reads conflict-free), one
   // V_hi^T tile [DV][KT] fp16 (chunk-swizzled) and one V_lo block [DV][64]
@@ -89,10 +93,13 @@ struct FwdCfg {
   // Two workgroups per CU (four waves each, 256 VGPRs) when two stages of each
   // fit in half the 160 KiB LDS (less 1 KiB for the rest); the eight-wave
   // shapes (one query block per wave) would have to fit 128 VGPRs and spill.
+  // W4: three workgroups when two stages fit a third of the LDS (m = 32,
+  // 142 VGPRs), else two.
   static constexpr bool TWO = 2 * STAGE * 2 <= 79 * 1024 && QB == 2;
-  static constexpr int WG_PER_CU = SMALL ? 3 : TWO ? 2 : 1;
+  static constexpr int W4WG = 2 * STAGE * 2 <= 52 * 1024 ? 3 : 2;
+  static constexpr int WG_PER_CU = W4 ? W4WG : SMALL ? 3 : TWO ? 2 : 1;
   static constexpr int WAVES_PER_EU = WG_PER_CU * WAVES / 4;
-  static constexpr int LDS_BUDGET = (SMALL ? 52 : TWO ? 79 : 158) * 1024;
+  static constexpr int LDS_BUDGET = (WG_PER_CU == 3 ? 52 : WG_PER_CU == 2 ? 79 : 158) * 1024;
   static constexpr int NSTAGE = 3 * STAGE * 2 <= LDS_BUDGET ? 3 : 2;
   // both 32-key blocks of a tile in flight at once (fits the registers except
   // with the widest codes and values)
