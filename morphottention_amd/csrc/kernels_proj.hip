@@ -84,19 +84,25 @@ using ProjGemm = Gemm<BM, BN, 4, true, true, 64, 2>;
 // the stored remainder is never larger than V - V_hi, so V_hi + remainder
 // rounds back to V_hi in fp16 (a single key's output is then exactly V_hi,
 // the value the backward's dP = dO V_hi^T sees).
+// The conversion with stochastic rounding adds the given random bits below
+// the last kept mantissa bit and truncates; with zero random bits it is the
+// truncation of the magnitude, i.e. rounding toward zero, in one instruction
+// (bit-identical, over every 7th float bit pattern of both signs, to the
+// nearest conversion stepped one code toward zero where that overshot).
+__device__ __forceinline__ float vlo_scaled(float r) { return fminf(fmaxf(r * (float)(1 << kVloExp), -448.f), 448.f); }
 __device__ __forceinline__ unsigned vlo_code(float r) {
-  const float x = fminf(fmaxf(r * (float)(1 << kVloExp), -448.f), 448.f);
-  unsigned c = (unsigned)__builtin_amdgcn_cvt_pk_fp8_f32(x, 0.f, 0, false) & 0xffu;  // nearest
-  if (fabsf(__builtin_amdgcn_cvt_f32_fp8((int)c, 0)) > fabsf(x)) c -= 1u;  // one code toward zero
-  return c;
+  return (unsigned)__builtin_amdgcn_cvt_sr_fp8_f32(vlo_scaled(r), 0, 0, 0) & 0xffu;
 }
 __device__ __forceinline__ uint2 vlo_pack8(const float (&r)[8]) {
-  unsigned w[2];
+  int w[2];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
-    w[i] = vlo_code(r[4 * i]) | (vlo_code(r[4 * i + 1]) << 8) | (vlo_code(r[4 * i + 2]) << 16) |
-           (vlo_code(r[4 * i + 3]) << 24);
-  return make_uint2(w[0], w[1]);
+  for (int i = 0; i < 2; ++i) {  // byte k of the dword = r[4 i + k]
+    w[i] = __builtin_amdgcn_cvt_sr_fp8_f32(vlo_scaled(r[4 * i]), 0, 0, 0);
+    w[i] = __builtin_amdgcn_cvt_sr_fp8_f32(vlo_scaled(r[4 * i + 1]), 0, w[i], 1);
+    w[i] = __builtin_amdgcn_cvt_sr_fp8_f32(vlo_scaled(r[4 * i + 2]), 0, w[i], 2);
+    w[i] = __builtin_amdgcn_cvt_sr_fp8_f32(vlo_scaled(r[4 * i + 3]), 0, w[i], 3);
+  }
+  return make_uint2((unsigned)w[0], (unsigned)w[1]);
 }
 
 // GEN: a cube projection other than the sigmoid, or the masked diagonal (the
@@ -107,7 +113,8 @@ __global__ __launch_bounds__(kGemmThreads) void proj_fwd_kernel(const f16* __res
                                                                const f16* __restrict__ gate_k, Dims d, ProjBuffers p) {
   using G = ProjGemm<BM, BN>;
   constexpr int SS = BN + 1;  // stage row stride (floats)
-  static_assert(64 * SS * 4 <= G::kLdsBytes, "epilogue slab must fit the main loop's LDS");
+  // epilogue LDS: the 64-row slab, then the tile's gate products G = gq gk
+  static_assert(64 * SS * 4 + BN * 4 <= G::kLdsBytes, "epilogue slab and gate table must fit the main loop's LDS");
   __shared__ __align__(16) char smem[G::kLdsBytes];
   constexpr int CW = 2 * M + 8;
 
@@ -122,8 +129,18 @@ __global__ __launch_bounds__(kGemmThreads) void proj_fwd_kernel(const f16* __res
   G::run(X, d.D, p.wt, d.D, T, NC, m0, n0, 0, d.D, smem, acc);
 
   float* stage = reinterpret_cast<float*>(smem);
+  float* gtab = stage + 64 * SS;
   const float c1 = 2.0f * d.scale * kLog2e;
   static_assert(G::WTM == 64 || G::WTM == 32, "wave rows of 64 or 32 rows");
+  // Code columns of this tile: local columns [0, ncode), whole heads (PCPT per
+  // tile in the interleaved order; in the natural order those below HM).
+  const int ncode = d.PCPT > 0 ? d.PCPT : max(0, min(BN, d.HM - n0));
+  // Gate products of the code columns, read from global memory once per tile
+  // rather than in every slab (the first slab's barrier publishes them).
+  for (int lc = tid; lc < ncode; lc += kGemmThreads) {
+    const int col = proj_col(d, tn, lc);  // = h M + c, the gates' index
+    gtab[lc] = (float)gate_q[col] * (float)gate_k[col];
+  }
   for (int slab = 0; slab < BM / 64; ++slab) {
     if (slab > 0) __syncthreads();  // the previous slab has been consumed
     if (G::WTM * wm / 64 == slab) {  // uniform: this wave row's rows are in the slab
@@ -143,14 +160,14 @@ __global__ __launch_bounds__(kGemmThreads) void proj_fwd_kernel(const f16* __res
     // xor shuffles for the row sums (a head's M columns are contiguous in
     // both column orders). One thread per (token, head) had left 3/4 of the
     // workgroup idle at m = 64.
-    constexpr int kHeadsPerTile = BN / M, kChunks = M / 8;
+    constexpr int kChunks = M / 8;
     static_assert(kGemmThreads % kChunks == 0, "a (token, head) never straddles two passes");
-    for (int idx = tid; idx < 64 * kHeadsPerTile * kChunks; idx += kGemmThreads) {
+    for (int idx = tid; idx < 8 * ncode; idx += kGemmThreads) {  // 64 rows x (ncode / M heads) x (M / 8 chunks)
       const int j = idx % kChunks, item = idx / kChunks;
       const int hh = item / 64, r = item % 64;
       const int col0 = proj_col(d, tn, hh * M);
       const int t = row0 + r;
-      const bool active = col0 < d.HM && t < T;  // the same for every chunk of the item
+      const bool active = t < T;  // the same for every chunk of the item
       const int h = col0 / M;
       const int b = t / d.N, n = t - b * d.N;
       const int64_t bhn = (int64_t)(b * d.H + h) * d.N + n;
@@ -158,13 +175,14 @@ __global__ __launch_bounds__(kGemmThreads) void proj_fwd_kernel(const f16* __res
       float sumb = 0.f, tii = 0.f, U = 0.f;
       if (active) {
         const float* z = stage + r * SS + hh * M + c8;
-        const f16x8 gq8 = *reinterpret_cast<const f16x8*>(gate_q + h * M + c8);
-        const f16x8 gk8 = *reinterpret_cast<const f16x8*>(gate_k + h * M + c8);
+        const float4 ga = *reinterpret_cast<const float4*>(gtab + hh * M + c8);
+        const float4 gb = *reinterpret_cast<const float4*>(gtab + hh * M + c8 + 4);
+        const float g8[8] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w};
         f16x8 phh, phl, kch, kcl;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const float phi = GEN ? cube_project(z[e], d.proj) : sigmoidf_(z[e]);
-          const float G = (float)gq8[e] * (float)gk8[e];
+          const float G = g8[e];
           const float wgt = d.scale * G;
           const float cg = c1 * G;
           f16 a, bb;
@@ -225,19 +243,22 @@ __global__ __launch_bounds__(kGemmThreads) void proj_fwd_kernel(const f16* __res
     // consecutive tokens; 8 neighbouring threads cover the slab's 64
     // consecutive tokens of a column (128 contiguous bytes of vt, one 64-byte
     // row of vlo), a wave 8 columns.
-    if (proj_col(d, tn, BN - 1) >= d.HM) {  // the tile has value columns (uniform)
+    // A thread keeps its group of 8 tokens (tid % 8) and steps over the
+    // tile's value columns [ncode, BN).
+    const int rg = tid & 7, tb = row0 + 8 * rg;
+    if (ncode < BN && tb < T) {
       const bool vec = d.N % 8 == 0;
       const int ntile = d.NP / 64;
-      for (int idx = tid; idx < 8 * BN; idx += kGemmThreads) {
-        const int rg = idx & 7, cc = idx >> 3;
-        const int col = proj_col(d, tn, cc), tb = row0 + 8 * rg;
-        if (col < d.HM || n0 + cc >= NC || tb >= T) continue;
+      const int tbb = tb / d.N, tbn = tb - tbb * d.N;  // batch row and position of token tb
+      for (int cc = ncode + (tid >> 3); cc < BN; cc += kGemmThreads / 8) {
+        if (n0 + cc >= NC) break;  // columns past NC only at the end of the tile
+        const int col = proj_col(d, tn, cc);
         const int vcol = col - d.HM, h = vcol / DV, dd = vcol % DV;
         const float* src = stage + 8 * rg * SS + cc;
         if (vec) {
           // N % 8 == 0 and tb % 8 == 0: the 8 tokens share one batch row and
           // land on 8 consecutive bytes of a vlo row
-          const int b = tb / d.N, n = tb - b * d.N;
+          const int b = tbb, n = tbn;
           const int64_t bh = (int64_t)(b * d.H + h);
           f16x8 vh;
           float vl[8];
