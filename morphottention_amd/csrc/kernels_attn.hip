@@ -897,8 +897,7 @@ __global__ __launch_bounds__((BwdCfg<M, DV>::NT), (BwdCfg<M, DV>::MIN_WG)) void 
 
   // ---- dq[q][code] += sum_key dS[q][key] phi[key][code]: 16 x 16 output
   // tiles split over the waves, contraction over all KW keys of the workgroup
-  // (rows past N are zero in both operands). The phi operand never changes;
-  // it is re-read from the phi tile each step (registers are the scarcer).
+  // (rows past N are zero in both operands).
   f16x8 dqa[C::DQT][C::KW / 32];
   int d_s[C::DQT][2];
 #pragma unroll
@@ -921,6 +920,19 @@ __global__ __launch_bounds__((BwdCfg<M, DV>::NT), (BwdCfg<M, DV>::MIN_WG)) void 
 
   // waves with dq tiles (wave-uniform); the others issue no dq atomics
   const bool dq_wave = w < C::DQTILES;
+  // The dq product's phi operand never changes. At m = 16 it stays in
+  // registers (4 fragments, 16 VGPRs; C3 attn_bwd -3 %); with eight waves
+  // (m = 32, 64: 256 keys, twice the fragments) it is re-read from the phi
+  // tile each step (registers are the scarcer there).
+  constexpr bool PHIREG = M == 16;
+  f16x8 phib[PHIREG ? C::DQT : 1][PHIREG ? C::KW / 32 : 1];
+  if constexpr (PHIREG) {
+#pragma unroll
+    for (int t = 0; t < C::DQT; ++t)
+#pragma unroll
+      for (int kc = 0; kc < C::KW / 32; ++kc)
+        phib[t][kc] = tfrag16<C::PRB>(sPk, 32 * kc, 16 * ((w + C::NW * t) / (C::QT / 16)), lane);
+  }
   auto dq_load = [&](const char* sd) {
     if (!dq_wave) return;
 #pragma unroll
@@ -982,8 +994,14 @@ __global__ __launch_bounds__((BwdCfg<M, DV>::NT), (BwdCfg<M, DV>::MIN_WG)) void 
       const int qt = tile % (C::QT / 16);
       f32x4 acc = {};
 #pragma unroll
-      for (int kc = 0; kc < C::KW / 32; ++kc)
-        acc = mfma16x16(dqa[t][kc], tfrag16<C::PRB>(sPk, 32 * kc, 16 * (tile / (C::QT / 16)), lane), acc);
+      for (int kc = 0; kc < C::KW / 32; ++kc) {
+        f16x8 phi_op;
+        if constexpr (PHIREG)
+          phi_op = phib[t][kc];
+        else
+          phi_op = tfrag16<C::PRB>(sPk, 32 * kc, 16 * (tile / (C::QT / 16)), lane);
+        acc = mfma16x16(dqa[t][kc], phi_op, acc);
+      }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         if (full) {
@@ -1053,8 +1071,7 @@ __global__ __launch_bounds__((BwdCfg<M, DV>::NT), (BwdCfg<M, DV>::MIN_WG)) void 
     };
     // P, dS = P (dP - delta), dV^T += dO^T P, dk^T += phi^T dS (rows: dv /
     // code; lane: key)
-    auto grads = [&](int sb, const f32x16& s, const f32x16& dp, f16x8 (&ds16)[2]) {
-      f16x8 p16[2];
+    auto soft = [&](const f32x16& s, const f32x16& dp, f16x8 (&p16)[2], f16x8 (&ds16)[2]) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const float pr = fast_exp2(s[r]);
@@ -1070,6 +1087,8 @@ __global__ __launch_bounds__((BwdCfg<M, DV>::NT), (BwdCfg<M, DV>::MIN_WG)) void 
           for (int e = 0; e < 4; ++e)
             dcb_acc = __builtin_amdgcn_fdot2(h2{ds16[c][2 * e], ds16[c][2 * e + 1]}, ones2, dcb_acc, false);
       }
+    };
+    auto prods = [&](int sb, const f16x8 (&p16)[2], const f16x8 (&ds16)[2]) {
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
 #pragma unroll
@@ -1080,6 +1099,11 @@ __global__ __launch_bounds__((BwdCfg<M, DV>::NT), (BwdCfg<M, DV>::MIN_WG)) void 
           dka[mb] = mfma16(tfrag(tQ, t_q[mb], (32 * sb + 16 * c) * C::QRB), ds16[c], dka[mb]);
       }
     };
+    auto grads = [&](int sb, const f32x16& s, const f32x16& dp, f16x8 (&ds16)[2]) {
+      f16x8 p16[2];
+      soft(s, dp, p16, ds16);
+      prods(sb, p16, ds16);
+    };
     // dS^T row of this key (zeros where nothing was computed): logical chunk
     // 4 sb + 2 c + h32 at physical chunk (4 sb + 2 c + h32) ^ sz
     auto put_ds = [&](int sb, const f16x8 (&ds16)[2]) {
@@ -1089,16 +1113,22 @@ __global__ __launch_bounds__((BwdCfg<M, DV>::NT), (BwdCfg<M, DV>::MIN_WG)) void 
     };
     // A step whose two sub-blocks are whole and unmasked for this wave (the
     // bulk of the work) runs as one straight block: the scores of sub-block 1
-    // are on the MFMA while sub-block 0's exponentials run on the VALU.
+    // are on the MFMA while sub-block 0's exponentials run on the VALU. Both
+    // sub-blocks' exponentials come before their dV / dk products, so the fp32
+    // scores are dead by then (m = 16: 256 -> 240 VGPRs, room for the dq
+    // product's phi operand).
     const bool plain = C::NSB == 2 && qs + C::QT <= N && kw0 + 31 < N && (!causal || kw0 + 31 <= qs) &&
                        (!MD || kw0 > qs + C::QT - 1 || kw0 + 31 < qs);  // wave-uniform
     if (plain) {
       f32x16 s0, dp0, s1, dp1;
       f16x8 d0[2], d1[2];
+      f16x8 p0[2], p1[2];
       scores(0, s0, dp0);
       scores(1, s1, dp1);
-      grads(0, s0, dp0, d0);
-      grads(1, s1, dp1, d1);
+      soft(s0, dp0, p0, d0);
+      soft(s1, dp1, p1, d1);
+      prods(0, p0, d0);
+      prods(1, p1, d1);
       put_ds(0, d0);
       put_ds(1, d1);
     } else {
