@@ -65,7 +65,8 @@ struct FwdCfg {
   // has twice the workgroups and still covers the CUs.
   // W4 (m >= 32, dv <= 64, one block per wave): four-wave workgroups, two or
   // three per CU (LDS permitting), rather than one of eight waves; the waves
-  // of a CU then wait at independent barriers (C4 forward -4.5 %, C5 -3 %).
+  // of a CU then wait at independent barriers (B1 N16384 H16 m32 causal:
+  // forward -6 %; B16 N2048 H32 m64: -7 %).
   static constexpr int QB2 = (M <= 32 && DV <= 64 && M * DV <= 1024) ? 2 : 1;
   static constexpr bool SMALL = SM && QB2 == 2;
   static constexpr int QB = SMALL ? 1 : QB2;
