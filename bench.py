@@ -31,6 +31,8 @@ CONFIGS = {
     "C5": (16, 2048, 2048, 32, 64, 2.0, False, 4, 4.0),
 }
 PEAK_FP16_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
+# the kernel whose roofline the line reports (the longest of a step at every GPU config)
+DOMINANT = "attn_bwd"
 PEAK_HBM_GBS = 8000.0
 # v_exp_f32 at quarter rate: 256 CUs x 16 lanes/clk x 2.4 GHz (BASELINE.md roofline constants)
 PEAK_EXP_PER_S = 9.8e12
@@ -164,16 +166,20 @@ PMC_PASSES = [
 
 def rocprof_commands(config):
     """The profiling commands whose output --summarize condenses (repo root,
-    TMPDIR=/tmp; each PMC pass in a process of its own)."""
-    base = f"python bench.py --config {config} --no-cpu-baseline"
+    TMPDIR=/tmp; each PMC pass in a process of its own). The kernel trace runs
+    the bench command itself (for C3 the driver's exact command), its JSON line
+    kept beside the trace so that the HIP-event figure of the same process can
+    be set against the tracer's timestamps."""
+    cfg = "" if config == "C3" else f" --config {config}"
     kt = (f"rocprofv3 --kernel-trace --stats -f csv -d gpurun_out/prof/kt_{config} -o run -- "
-          f"{base} --steps 5 --warmup 2 --timing-steps 1")
+          f"python bench.py --gpus 1 --steps 20 --warmup 5{cfg} > gpurun_out/prof/kt_{config}.json")
+    base = f"python bench.py --config {config} --no-cpu-baseline"
     pmc = [f"rocprofv3 --pmc {ctrs} -f csv -d gpurun_out/prof/pmc{i + 1}_{config} -o run -- "
            f"{base} --steps 1 --warmup 1 --timing-steps 1 --calib-copy" for i, ctrs in enumerate(PMC_PASSES)]
     return kt, pmc
 
 
-def summarize_rocprof(kind, config, src, steps, warmup):
+def summarize_rocprof(kind, config, src, steps, warmup, traced_json=None):
     """Condense rocprofv3 CSV output into the committed summary
     profiles/<kind>_<config>.(json|md). kind "kernel_trace": `src` is the
     --kernel-trace output directory; per kernel, the mean duration over the
@@ -192,7 +198,8 @@ def summarize_rocprof(kind, config, src, steps, warmup):
                 (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
         out = {"config": config, "command": rocprof_commands(config)[0],
                "summary_command": f"python bench.py --config {config} --steps {steps} --warmup {warmup} "
-                                  f"--summarize kernel_trace {src}",
+                                  f"--summarize kernel_trace {src}" +
+                                  (f" --traced-json {traced_json}" if traced_json else ""),
                "timed_window":
                f"dispatches {warmup}..{warmup + steps - 1} of each kernel", "kernels": {}}
         for k, v in per.items():
@@ -201,7 +208,18 @@ def summarize_rocprof(kind, config, src, steps, warmup):
                 continue
             out["kernels"][k] = {"calls": len(v), "timed_avg_us": round(sum(w) / len(w), 2),
                                  "all_avg_us": round(sum(v) / len(v), 2), "min_us": round(min(v), 2),
-                                 "max_us": round(max(v), 2)}
+                                 "max_us": round(max(v), 2), "timed_us": [round(x, 1) for x in w]}
+        if traced_json:
+            # the traced process's own line: its dominant kernel's HIP-event
+            # mean over the same timed launches, against the tracer's
+            line = [ln for ln in open(traced_json) if ln.startswith("{")][-1]
+            roof = json.loads(line)["roofline"]
+            name = f"{roof['kernel']}_kernel"
+            tr = out["kernels"][name]["timed_avg_us"]
+            ev = roof["avg_ms"] * 1e3
+            out["same_process"] = {"kernel": name, "hip_event_avg_us": round(ev, 2), "trace_avg_us": tr,
+                                   "trace_over_events": round(tr / ev, 4), "line_frac": roof["frac"],
+                                   "line_ms_per_step": json.loads(line)["ms_per_step"]}
     else:
         dirs = src.split(",")
         vals = {}
@@ -253,6 +271,12 @@ def summarize_rocprof(kind, config, src, steps, warmup):
     cmds = [out["command"]] if kind == "kernel_trace" else out["commands"]
     lines += [f"    {c}" for c in cmds] + [f"    {out['summary_command']}", ""]
     if kind == "kernel_trace":
+        sp = out.get("same_process")
+        if sp:
+            lines += [f"Same process: {sp['kernel']} HIP events (bound to its dispatches, over the timed steps) "
+                      f"{sp['hip_event_avg_us']} us, trace {sp['trace_avg_us']} us (trace / events "
+                      f"{sp['trace_over_events']}); that line's frac {sp['line_frac']}, ms_per_step "
+                      f"{sp['line_ms_per_step']}.", ""]
         lines += [f"Timed window: {out['timed_window']}.", "",
                   "| kernel | calls | timed avg (us) | all avg (us) | min (us) | max (us) |", "|---|---|---|---|---|---|"]
         for k, v in sorted(out["kernels"].items(), key=lambda kv: -kv[1]["timed_avg_us"]):
@@ -491,13 +515,16 @@ def main():
                          "aggregation, instead of the bare op")
     ap.add_argument("--tau", type=float, default=0.5, help="--layer soft: temperature")
     ap.add_argument("--erosion", action="store_true", help="--layer soft: soft min-plus instead of max-plus")
+    ap.add_argument("--traced-json", default=None,
+                    help="--summarize kernel_trace: the JSON line the traced bench command printed")
     ap.add_argument("--summarize", nargs=2, metavar=("KIND", "SRC"), default=None,
                     help="write profiles/<KIND>_<config>.json from rocprofv3 CSV output: KIND kernel_trace (SRC = "
                          "the --kernel-trace directory of this command) or counters (SRC = comma-separated --pmc "
                          "directories); no GPU work")
     args = ap.parse_args()
     if args.summarize:
-        return summarize_rocprof(args.summarize[0], args.config, args.summarize[1], args.steps, args.warmup)
+        return summarize_rocprof(args.summarize[0], args.config, args.summarize[1], args.steps, args.warmup,
+                                 args.traced_json)
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only; the path is sharded over "
                                    "(batch x head) without collectives"}))
@@ -531,7 +558,13 @@ def main():
         step()
     torch.cuda.synchronize()
 
-    # --- timed region: exactly K fwd+bwd steps
+    # --- timed region: exactly K fwd+bwd steps. The dominant kernel carries
+    # HIP events bound to its own dispatches (hipExtLaunchKernel on the launch
+    # stream), so its average duration comes from these very launches. Only it
+    # is timed here: a timed dispatch waits a few microseconds in the queue.
+    capi.timing_only(DOMINANT)
+    capi.timing_enable(True)
+    capi.timing_read()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     e0.record()
@@ -540,6 +573,10 @@ def main():
     e1.record()
     torch.cuda.synchronize()
     ms_step = e0.elapsed_time(e1) / args.steps
+    dom_recs = [t for name, t in capi.timing_read() if name == DOMINANT]
+    capi.timing_enable(False)
+    capi.timing_only(None)
+    assert len(dom_recs) == args.steps, f"{len(dom_recs)} {DOMINANT} launches timed in {args.steps} steps"
 
     # --- forward only (reported beside)
     with torch.no_grad():
@@ -553,7 +590,8 @@ def main():
         torch.cuda.synchronize()
     ms_fwd = e0.elapsed_time(e1) / args.steps
 
-    # --- per-kernel durations with HIP events on the launch stream
+    # --- every kernel's duration, from HIP events bound to the dispatches of
+    # `--timing-steps` further steps (a per-kernel table beside the line)
     capi.timing_enable(True)
     capi.timing_read()
     for _ in range(args.timing_steps):
@@ -570,8 +608,10 @@ def main():
         f = kernel_flops(name, B, N, D, H, m, causal)
         kernels[name] = {"avg_ms": round(avg, 5), "launches_per_step": len(v) / args.timing_steps,
                          "tflops": round(f / (avg * 1e-3) / 1e12, 1) if f else None}
-    dominant = max(per, key=lambda k: sum(per[k]))
-    dom_avg = sum(per[dominant]) / len(per[dominant])
+    dominant = DOMINANT
+    if per and max(per, key=lambda k: sum(per[k])) != dominant:
+        log(f"note: {max(per, key=lambda k: sum(per[k]))} took longer than {dominant} in the timing steps")
+    dom_avg = sum(dom_recs) / len(dom_recs)
     dom_flops = kernel_flops(dominant, B, N, D, H, m, causal)
     achieved = dom_flops / (dom_avg * 1e-3) / 1e12
     f_fwd, f_bwd = step_flops(B, N, D, H, m, causal)
@@ -583,9 +623,11 @@ def main():
     log(f"step {ms_step:.4f} ms  fwd {ms_fwd:.4f} ms  step-level {(f_fwd + f_bwd) / (ms_step * 1e-3) / 1e12:.1f} "
         f"TFLOP/s")
 
+    log(f"{dominant} over the timed steps: {dom_avg:.4f} ms ({len(dom_recs)} launches, HIP events)")
     roofline = {"bound": "mfma", "kernel": dominant, "achieved": round(achieved, 2), "peak": PEAK_FP16_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
-                "traffic": load_traffic(dominant, args.config)}
+                "traffic": load_traffic(dominant, args.config),
+                "avg_ms": round(dom_avg, 5), "timed_launches": len(dom_recs)}
     trace_ms = load_trace_avg(dominant, args.config)
     if trace_ms:
         # the same kernel's mean over the timed steps of the committed

@@ -175,12 +175,20 @@ int morpho_soft_backward(const void* grad_out, const void* X, const void* W_phi,
 
 /* Per-kernel timing for measurement harnesses. No reference counterpart.
  * When enabled (process-wide), every kernel the library launches, from any
- * thread, is bracketed by HIP events on its stream. morpho_timing_read
+ * thread, carries a start and a stop HIP event bound to its dispatch
+ * (hipExtLaunchKernel: the kernel's own start and end, no marker packets
+ * between kernels, so the timed stream runs as it does untimed).
+ * morpho_timing_read
  * synchronises on the recorded events and returns up to `max_entries`
  * (name, milliseconds) pairs, oldest first, then clears the record; names
  * point to static strings. */
 int morpho_timing_enable(int enable);
 int morpho_timing_read(const char** names, float* ms, int max_entries);
+/* Restricts the timing to the launches of one name (as morpho_timing_read
+ * reports it, e.g. "attn_bwd"); NULL or "" times every launch again. Each
+ * timed dispatch costs a few microseconds of queue time before it, so a
+ * harness that times a whole run times only the kernel it reports. */
+int morpho_timing_only(const char* name);
 
 #ifdef __cplusplus
 }

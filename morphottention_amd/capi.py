@@ -51,6 +51,8 @@ def lib() -> ctypes.CDLL:
                                            + [ctypes.c_float, ctypes.c_int, ctypes.c_int, vp, vp, sz, vp])
         L.morpho_timing_enable.restype = ctypes.c_int
         L.morpho_timing_enable.argtypes = [ctypes.c_int]
+        L.morpho_timing_only.restype = ctypes.c_int
+        L.morpho_timing_only.argtypes = [ctypes.c_char_p]
         L.morpho_timing_read.restype = ctypes.c_int
         L.morpho_timing_read.argtypes = [ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_float),
                                          ctypes.c_int]
@@ -76,6 +78,11 @@ def soft_backward_workspace_size(B: int, N: int, D: int, H: int, cube_m: int, ha
 
 def timing_enable(enable: bool) -> None:
     lib().morpho_timing_enable(int(enable))
+
+
+def timing_only(name: str | None) -> None:
+    """Time only the launches reported under ``name`` (None: all of them)."""
+    lib().morpho_timing_only(name.encode() if name else None)
 
 
 def timing_read(max_entries: int = 4096) -> list[tuple[str, float]]:

@@ -25,10 +25,12 @@ thread_local std::string g_last_error;
 struct TimingRec {
   const char* name;
   hipEvent_t start, stop;
+  bool bound;  // a launch took the start event (the record then has a measurement)
 };
 // Timing state is process-wide: autograd runs the backward on its own thread.
 std::atomic<bool> g_timing{false};
 std::mutex g_timing_mu;
+std::string g_timing_only;         // guarded by g_timing_mu; empty: every launcher
 std::vector<TimingRec> g_recs;     // guarded by g_timing_mu
 std::vector<hipEvent_t> g_pool;    // guarded by g_timing_mu
 thread_local int g_open_rec = -1;  // index of this thread's open record
@@ -186,21 +188,35 @@ int run_projection(const Dims& d, const void* X, const void* W_phi, const void* 
 
 }  // namespace
 
-void timing_begin(const char* name, hipStream_t s) {
+void timing_begin(const char* name, hipStream_t) {
   g_open_rec = -1;
   if (!g_timing.load(std::memory_order_relaxed)) return;
   std::lock_guard<std::mutex> lock(g_timing_mu);
-  TimingRec r{name, take_event(), take_event()};
-  if (r.start) (void)hipEventRecord(r.start, s);
+  if (!g_timing_only.empty() && g_timing_only != name) return;
+  TimingRec r{name, take_event(), take_event(), false};
+  if (!r.start || !r.stop) {  // no events: nothing to bind
+    if (r.start) g_pool.push_back(r.start);
+    if (r.stop) g_pool.push_back(r.stop);
+    return;
+  }
   g_recs.push_back(r);
   g_open_rec = (int)g_recs.size() - 1;
 }
 
-void timing_end(hipStream_t s) {
-  if (g_open_rec < 0) return;
+void timing_end(hipStream_t) { g_open_rec = -1; }
+
+hipEvent_t timing_take_start() {
+  if (g_open_rec < 0) return nullptr;
   std::lock_guard<std::mutex> lock(g_timing_mu);
-  if (g_open_rec < (int)g_recs.size() && g_recs[g_open_rec].stop) (void)hipEventRecord(g_recs[g_open_rec].stop, s);
-  g_open_rec = -1;
+  if (g_open_rec >= (int)g_recs.size() || g_recs[g_open_rec].bound) return nullptr;
+  g_recs[g_open_rec].bound = true;
+  return g_recs[g_open_rec].start;
+}
+
+hipEvent_t timing_stop_event() {
+  if (g_open_rec < 0) return nullptr;
+  std::lock_guard<std::mutex> lock(g_timing_mu);
+  return g_open_rec < (int)g_recs.size() ? g_recs[g_open_rec].stop : nullptr;
 }
 
 }  // namespace morpho
@@ -287,7 +303,13 @@ int scratch_for_current_device(void** ptr) {
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (!g_scratch_ptr[dev]) {
     void* p = nullptr;
+    // The first call on a device may come from code under stream capture
+    // (which is what the entry point is for): the lookup is no stream work,
+    // so this thread's capture mode is relaxed around it and then restored.
+    hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+    const bool swapped = hipThreadExchangeStreamCaptureMode(&mode) == hipSuccess;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (swapped) (void)hipThreadExchangeStreamCaptureMode(&mode);
     if (e != hipSuccess || p == nullptr)
       return fail(MORPHO_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
     g_scratch_ptr[dev] = p;
@@ -534,11 +556,17 @@ MORPHO_EXPORT int morpho_timing_enable(int enable) {
   return MORPHO_OK;
 }
 
+MORPHO_EXPORT int morpho_timing_only(const char* name) {
+  std::lock_guard<std::mutex> lock(g_timing_mu);
+  g_timing_only = name ? name : "";
+  return MORPHO_OK;
+}
+
 MORPHO_EXPORT int morpho_timing_read(const char** names, float* ms, int max_entries) {
   std::lock_guard<std::mutex> lock(g_timing_mu);
   int n = 0;
   for (const TimingRec& r : g_recs) {
-    if (n < max_entries && r.start && r.stop) {
+    if (n < max_entries && r.bound) {
       float t = 0.f;
       if (hipEventSynchronize(r.stop) == hipSuccess && hipEventElapsedTime(&t, r.start, r.stop) == hipSuccess) {
         if (names) names[n] = r.name;

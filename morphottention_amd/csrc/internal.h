@@ -2,6 +2,7 @@
 // C ABI layer. Nothing here is exported from the shared library.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -157,9 +158,23 @@ hipError_t launch_soft_tau_reduce(const float* prep, int nprep, const float* bwd
 int soft_prep_blocks(const Dims& d);  // partial sums written by the prep (one float each)
 int soft_bwd_slots(const Dims& d);    // workgroup slots of both backward kernels (two floats each)
 
-// Timing hooks (capi.hip): bracket one launch with events when enabled.
+// Timing hooks (capi.hip). When timing is enabled, timing_begin opens a
+// record (a name and two events) for the launcher call that follows, and the
+// kernel launches inside it take the record's events through
+// hipExtLaunchKernel: the first launch takes the start event, every launch the
+// stop event, so the record spans the launcher's kernels. The events are bound
+// to the dispatches themselves; no marker packets run between kernels (marker
+// events had left about 10 us between consecutive kernels).
 void timing_begin(const char* name, hipStream_t s);
 void timing_end(hipStream_t s);
+hipEvent_t timing_take_start();  // the open record's start event, for its first launch only (else null)
+hipEvent_t timing_stop_event();  // the open record's stop event (null without an open record)
+
+// Every kernel launch of the library: hipLaunchKernelGGL semantics (errors are
+// read with hipGetLastError), with the timing record's events when one is open.
+#define MORPHO_KLAUNCH(KERNEL, GRID, BLOCK, SHMEM, STREAM, ...)                                       \
+  hipExtLaunchKernelGGL(KERNEL, GRID, BLOCK, SHMEM, STREAM, ::morpho::timing_take_start(),            \
+                        ::morpho::timing_stop_event(), 0u, __VA_ARGS__)
 
 // Instantiations of a launcher template FN<M, DV> for every supported shape.
 #define MORPHO_MDV_DISPATCH(FN, ...)                                                         \

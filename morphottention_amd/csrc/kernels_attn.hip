@@ -512,10 +512,10 @@ static hipError_t launch_attn_fwd_c(const Dims& d, const ProjBuffers& p, f16* ou
   using C = FwdCfg<M, DV, SM>;
   const dim3 grid(xcd_grid((d.N + C::QW - 1) / C::QW, d.B * d.H));
   if (d.mask_diag)
-    hipLaunchKernelGGL((attn_fwd_kernel<M, DV, true, SM>), grid, dim3(64 * C::WAVES), 0, s, p.qa, p.ka, p.vt, p.vlo,
+    MORPHO_KLAUNCH((attn_fwd_kernel<M, DV, true, SM>), grid, dim3(64 * C::WAVES), 0, s, p.qa, p.ka, p.vt, p.vlo,
                        p.tstat, out, lse, d.N, d.NP, d.H, d.D, d.B * d.H, d.causal);
   else
-    hipLaunchKernelGGL((attn_fwd_kernel<M, DV, false, SM>), grid, dim3(64 * C::WAVES), 0, s, p.qa, p.ka, p.vt,
+    MORPHO_KLAUNCH((attn_fwd_kernel<M, DV, false, SM>), grid, dim3(64 * C::WAVES), 0, s, p.qa, p.ka, p.vt,
                        p.vlo, p.tstat, out, lse, d.N, d.NP, d.H, d.D, d.B * d.H, d.causal);
   return hipGetLastError();
 }
@@ -601,7 +601,7 @@ template <int M, int DV>
 static hipError_t launch_bwd_prep_t(const Dims& d, const ProjBuffers& p, const f16* grad_out, const f16* out,
                                     const float* lse, const BwdBuffers& g, int write_q, hipStream_t s) {
   const int64_t n = d.T * (d.D / 8);
-  hipLaunchKernelGGL((bwd_prep_kernel<M, DV>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, grad_out, out, lse,
+  MORPHO_KLAUNCH((bwd_prep_kernel<M, DV>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, grad_out, out, lse,
                      p.tstat, g.aug, p.qa, write_q, g.dq, reinterpret_cast<float2*>(g.dr), d.mask_diag ? 0 : 1,
                      d.T, d.N, d.H, d.D);
   return hipGetLastError();
@@ -1212,11 +1212,11 @@ static hipError_t launch_attn_bwd_t(const Dims& d, const ProjBuffers& p, const f
   using C = BwdCfg<M, DV>;
   const dim3 grid(xcd_grid((d.N + C::KW - 1) / C::KW, d.B * d.H));
   if (d.mask_diag)
-    hipLaunchKernelGGL((attn_bwd_kernel<M, DV, true>), grid, dim3(C::NT), 0, s, p.qa, p.ka, p.vt, g.aug, grad_out, g.dq,
-                       g.dk, g.dcb, g.dr, g.dzv, d.N, d.NP, d.H, d.D, d.HM, d.B * d.H, d.causal);
+    MORPHO_KLAUNCH((attn_bwd_kernel<M, DV, true>), grid, dim3(C::NT), 0, s, p.qa, p.ka, p.vt, g.aug, grad_out,
+                   g.dq, g.dk, g.dcb, g.dr, g.dzv, d.N, d.NP, d.H, d.D, d.HM, d.B * d.H, d.causal);
   else
-    hipLaunchKernelGGL((attn_bwd_kernel<M, DV, false>), grid, dim3(C::NT), 0, s, p.qa, p.ka, p.vt, g.aug, grad_out, g.dq,
-                       g.dk, g.dcb, g.dr, g.dzv, d.N, d.NP, d.H, d.D, d.HM, d.B * d.H, d.causal);
+    MORPHO_KLAUNCH((attn_bwd_kernel<M, DV, false>), grid, dim3(C::NT), 0, s, p.qa, p.ka, p.vt, g.aug, grad_out,
+                   g.dq, g.dk, g.dcb, g.dr, g.dzv, d.N, d.NP, d.H, d.D, d.HM, d.B * d.H, d.causal);
   return hipGetLastError();
 }
 

@@ -63,7 +63,7 @@ __global__ __launch_bounds__(256) void transpose_weights_kernel(const f16* __res
 hipError_t launch_transpose_weights(const Dims& d, const f16* W_phi, const f16* W_V, f16* wt, f16* wcat,
                                     hipStream_t s) {
   dim3 grid((d.HM + d.D + 63) / 64, (d.D + 63) / 64);
-  hipLaunchKernelGGL(transpose_weights_kernel, grid, dim3(256), 0, s, W_phi, W_V, wt, wcat, d);
+  MORPHO_KLAUNCH(transpose_weights_kernel, grid, dim3(256), 0, s, W_phi, W_V, wt, wcat, d);
   return hipGetLastError();
 }
 
@@ -308,9 +308,9 @@ static hipError_t launch_proj_fwd_t(const Dims& d, const f16* X, const f16* gq, 
   do {                                                                                                     \
     const dim3 g(gemm_tile_grid((int)((d.T + BM_ - 1) / BM_), (NC + BN_ - 1) / BN_));                      \
     if (gen)                                                                                               \
-      hipLaunchKernelGGL((proj_fwd_kernel<M, DV, BM_, BN_, true>), g, dim3(kGemmThreads), 0, s, X, gq, gk, d, p);  \
+      MORPHO_KLAUNCH((proj_fwd_kernel<M, DV, BM_, BN_, true>), g, dim3(kGemmThreads), 0, s, X, gq, gk, d, p);  \
     else                                                                                                   \
-      hipLaunchKernelGGL((proj_fwd_kernel<M, DV, BM_, BN_, false>), g, dim3(kGemmThreads), 0, s, X, gq, gk, d, p); \
+      MORPHO_KLAUNCH((proj_fwd_kernel<M, DV, BM_, BN_, false>), g, dim3(kGemmThreads), 0, s, X, gq, gk, d, p); \
   } while (0)
   if (d.PBN == 320)
     MORPHO_PROJ_LAUNCH(256, 320);
@@ -427,7 +427,7 @@ __global__ __launch_bounds__(kElemThreads) void proj_bwd_elem_kernel(const f16* 
 hipError_t launch_proj_bwd_elem(const Dims& d, const f16* gq, const f16* gk, const ProjBuffers& p,
                                 const BwdBuffers& g, bool row_corr, hipStream_t s) {
   dim3 grid((unsigned)((d.T + kGateTokensPerBlock - 1) / kGateTokensPerBlock), (d.HM + 255) / 256);
-  hipLaunchKernelGGL(proj_bwd_elem_kernel, grid, dim3(kElemThreads), 0, s, gq, gk, d, p, g, row_corr ? 1 : 0);
+  MORPHO_KLAUNCH(proj_bwd_elem_kernel, grid, dim3(kElemThreads), 0, s, gq, gk, d, p, g, row_corr ? 1 : 0);
   return hipGetLastError();
 }
 
@@ -465,11 +465,18 @@ static int dw_tiles(const Dims& d, int bt) { return ((d.D + bt - 1) / bt) * ((d.
 // down rather than to nearest halves the partials where it is 1.5 - 2
 // (B4 N4096 D1024 H16 m16: 8 instead of 16 splits, bwd_gemm 0.108 -> 0.099 ms
 // and dw_reduce 17 -> 11 us).
+// Capped so that the dW workgroups need not exceed about 32 per XCD
+// (8 ceil(32 / tiles) splits): beyond that more splits add no parallelism, only
+// fp32 partials (splits x D x (H m + D) x 4 bytes) and reduce traffic, which
+// would otherwise grow with the token count (T = 1M at D = 1024 would need
+// about 800 splits and 4 GiB).
 int dw_splits(const Dims& d) {
   const int NC = d.HM + d.D, by_k = (int)((d.T + 255) / 256);
-  const int s8 = (int)(d.T / (8 * NC));  // floor(T / (8 NC))
-  const int s = 8 * (s8 < 1 ? 1 : s8);
-  const int r = s < by_k ? s : by_k;
+  const int64_t s8 = d.T / (8 * (int64_t)NC);  // floor(T / (8 NC))
+  const int tiles = dw_tiles(d, 256);
+  const int64_t cap = 8 * (int64_t)((32 + tiles - 1) / tiles);
+  const int64_t s = 8 * (s8 < 1 ? 1 : s8 > cap / 8 ? cap / 8 : s8);
+  const int r = (int)(s < by_k ? s : by_k);
   return r < 1 ? 1 : r;
 }
 
@@ -568,9 +575,9 @@ hipError_t launch_bwd_gemm(const Dims& d, const ProjBuffers& p, const BwdBuffers
   a.n_dw = 8 * a.dw_tiles * ((S + 7) / 8);
   a.n_dx = (int)gemm_tile_grid((T + bt - 1) / bt, (d.D + bt - 1) / bt);
   if (bt == 128)
-    hipLaunchKernelGGL(bwd_gemm_kernel<128>, dim3((unsigned)(a.n_dw + a.n_dx)), dim3(kGemmThreads), 0, s, d, g, a);
+    MORPHO_KLAUNCH(bwd_gemm_kernel<128>, dim3((unsigned)(a.n_dw + a.n_dx)), dim3(kGemmThreads), 0, s, d, g, a);
   else
-    hipLaunchKernelGGL(bwd_gemm_kernel<256>, dim3((unsigned)(a.n_dw + a.n_dx)), dim3(kGemmThreads), 0, s, d, g, a);
+    MORPHO_KLAUNCH(bwd_gemm_kernel<256>, dim3((unsigned)(a.n_dw + a.n_dx)), dim3(kGemmThreads), 0, s, d, g, a);
   return hipGetLastError();
 }
 
@@ -643,7 +650,7 @@ hipError_t launch_dw_reduce(const Dims& d, const BwdBuffers& g, const f16* gq, c
   const int nw = (int)((total / 4 + 255) / 256);
   const int ngate = (d.HM + 15) / 16;
   const int nblk = (int)((d.T + kGateTokensPerBlock - 1) / kGateTokensPerBlock);
-  hipLaunchKernelGGL(dw_reduce_kernel, dim3((unsigned)(nw + ngate)), dim3(256), 0, s, g.wpart, g.splits, d.D, d.HM,
+  MORPHO_KLAUNCH(dw_reduce_kernel, dim3((unsigned)(nw + ngate)), dim3(256), 0, s, g.wpart, g.splits, d.D, d.HM,
                      dW_phi, dW_V, nw, g.gpart, nblk, d.scale, gq, gk, dgq, dgk);
   return hipGetLastError();
 }

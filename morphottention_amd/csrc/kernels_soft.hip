@@ -252,10 +252,10 @@ static hipError_t launch_soft_fwd_t(const Dims& d, const ProjBuffers& p, const f
   using C = SoftCfg<M, DV>;
   const dim3 grid(xcd_grid((d.N + C::QW - 1) / C::QW, d.B * d.H));
   if (d.mask_diag)
-    hipLaunchKernelGGL((soft_fwd_kernel<M, DV, true>), grid, dim3(256), 0, s, p.qa, p.ka, p.vt, p.vlo, p.tstat, tau,
+    MORPHO_KLAUNCH((soft_fwd_kernel<M, DV, true>), grid, dim3(256), 0, s, p.qa, p.ka, p.vt, p.vlo, p.tstat, tau,
                        out, zb, d.N, d.NP, d.H, d.D, d.B * d.H, d.causal, (float)sgn, run_flag);
   else
-    hipLaunchKernelGGL((soft_fwd_kernel<M, DV, false>), grid, dim3(256), 0, s, p.qa, p.ka, p.vt, p.vlo, p.tstat, tau,
+    MORPHO_KLAUNCH((soft_fwd_kernel<M, DV, false>), grid, dim3(256), 0, s, p.qa, p.ka, p.vt, p.vlo, p.tstat, tau,
                        out, zb, d.N, d.NP, d.H, d.D, d.B * d.H, d.causal, (float)sgn, run_flag);
   return hipGetLastError();
 }
@@ -324,7 +324,7 @@ __global__ __launch_bounds__(256) void soft_colext_kernel(const f16* __restrict_
 
 hipError_t launch_soft_colext(const Dims& d, const ProjBuffers& p, const SoftState& st, hipStream_t s) {
   const int ncol = d.B * d.H * d.DV;
-  hipLaunchKernelGGL(soft_colext_kernel, dim3((unsigned)((ncol + 3) / 4)), dim3(256), 0, s, p.vt, p.vlo, st.vmax,
+  MORPHO_KLAUNCH(soft_colext_kernel, dim3((unsigned)((ncol + 3) / 4)), dim3(256), 0, s, p.vt, p.vlo, st.vmax,
                      st.vmin, st.flag, d.N, d.NP, d.DV, ncol);
   return hipGetLastError();
 }
@@ -361,7 +361,7 @@ __global__ __launch_bounds__(256) void soft_fvals_kernel(const f16* __restrict__
 hipError_t launch_soft_fvals(const Dims& d, const ProjBuffers& p, const float* tau, int sgn, const SoftState& st,
                              hipStream_t s) {
   const int64_t n = (int64_t)d.B * d.H * d.DV * (d.NP / 8);
-  hipLaunchKernelGGL(soft_fvals_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p.vt, p.vlo, tau, st, d.N,
+  MORPHO_KLAUNCH(soft_fvals_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p.vt, p.vlo, tau, st, d.N,
                      d.NP, d.DV, n, (float)sgn);
   return hipGetLastError();
 }
@@ -537,10 +537,10 @@ static hipError_t launch_soft_fwd_fast_t(const Dims& d, const ProjBuffers& p, co
   using C = FastCfg<M, DV>;
   const dim3 grid(xcd_grid((d.N + C::QW - 1) / C::QW, d.B * d.H));
   if (d.mask_diag)
-    hipLaunchKernelGGL((soft_fwd_fast_kernel<M, DV, true>), grid, dim3(256), 0, s, p.qa, p.ka, p.vt, p.vlo, p.tstat,
+    MORPHO_KLAUNCH((soft_fwd_fast_kernel<M, DV, true>), grid, dim3(256), 0, s, p.qa, p.ka, p.vt, p.vlo, p.tstat,
                        tau, st, out, zb, d.N, d.NP, d.H, d.D, d.B * d.H, d.causal, (float)sgn);
   else
-    hipLaunchKernelGGL((soft_fwd_fast_kernel<M, DV, false>), grid, dim3(256), 0, s, p.qa, p.ka, p.vt, p.vlo, p.tstat,
+    MORPHO_KLAUNCH((soft_fwd_fast_kernel<M, DV, false>), grid, dim3(256), 0, s, p.qa, p.ka, p.vt, p.vlo, p.tstat,
                        tau, st, out, zb, d.N, d.NP, d.H, d.D, d.B * d.H, d.causal, (float)sgn);
   return hipGetLastError();
 }
@@ -623,7 +623,7 @@ template <int M, int DV>
 static hipError_t launch_soft_bwd_prep_t(const Dims& d, const f16* grad_out, const float* zb, const BwdBuffers& g,
                                          float* part, const float* tau, int sgn, const SoftState* st, uint16_t* gh,
                                          uint16_t* gl, hipStream_t s) {
-  hipLaunchKernelGGL((soft_bwd_prep_kernel<DV>), dim3((unsigned)soft_prep_blocks(d)), dim3(256), 0, s, grad_out, zb,
+  MORPHO_KLAUNCH((soft_bwd_prep_kernel<DV>), dim3((unsigned)soft_prep_blocks(d)), dim3(256), 0, s, grad_out, zb,
                      g.dcb, g.dq, part, d.T, d.N, d.H, d.D, d.M, tau, (float)sgn, st ? st->vmax : nullptr,
                      st ? st->vmin : nullptr, st ? st->arow : nullptr, st ? reinterpret_cast<bf16*>(gh) : nullptr,
                      st ? reinterpret_cast<bf16*>(gl) : nullptr);
@@ -885,11 +885,11 @@ static hipError_t launch_soft_bwd_t(const Dims& d, const ProjBuffers& p, const f
                                     hipStream_t s) {
   const dim3 grid((unsigned)soft_bwd_slots_t<M, DV>(d));
   if (d.mask_diag)
-    hipLaunchKernelGGL((soft_bwd_kernel<M, DV, true>), grid, dim3(256), 0, s, p.qa, p.ka, p.vt, p.vlo, p.tstat, tau,
+    MORPHO_KLAUNCH((soft_bwd_kernel<M, DV, true>), grid, dim3(256), 0, s, p.qa, p.ka, p.vt, p.vlo, p.tstat, tau,
                        grad_out, zb, g.dq, g.dk, g.dcb, g.dzv, part, d.N, d.NP, d.H, d.D, d.HM, d.B * d.H, d.causal,
                        (float)sgn, run_flag);
   else
-    hipLaunchKernelGGL((soft_bwd_kernel<M, DV, false>), grid, dim3(256), 0, s, p.qa, p.ka, p.vt, p.vlo, p.tstat, tau,
+    MORPHO_KLAUNCH((soft_bwd_kernel<M, DV, false>), grid, dim3(256), 0, s, p.qa, p.ka, p.vt, p.vlo, p.tstat, tau,
                        grad_out, zb, g.dq, g.dk, g.dcb, g.dzv, part, d.N, d.NP, d.H, d.D, d.HM, d.B * d.H, d.causal,
                        (float)sgn, run_flag);
   return hipGetLastError();
@@ -1235,11 +1235,11 @@ static hipError_t launch_soft_bwd_fast_t(const Dims& d, const ProjBuffers& p, co
   const auto* h = reinterpret_cast<const bf16*>(gh);
   const auto* l = reinterpret_cast<const bf16*>(gl);
   if (d.mask_diag)
-    hipLaunchKernelGGL((soft_bwd_fast_kernel<M, DV, true>), grid, dim3(256), 0, s, p.qa, p.ka, p.vt, p.vlo, p.tstat,
+    MORPHO_KLAUNCH((soft_bwd_fast_kernel<M, DV, true>), grid, dim3(256), 0, s, p.qa, p.ka, p.vt, p.vlo, p.tstat,
                        tau, st, h, l, g.dq, g.dk, g.dcb, g.dzv, part, d.N, d.NP, d.H, d.D, d.HM, d.B * d.H,
                        d.causal, (float)sgn);
   else
-    hipLaunchKernelGGL((soft_bwd_fast_kernel<M, DV, false>), grid, dim3(256), 0, s, p.qa, p.ka, p.vt, p.vlo, p.tstat,
+    MORPHO_KLAUNCH((soft_bwd_fast_kernel<M, DV, false>), grid, dim3(256), 0, s, p.qa, p.ka, p.vt, p.vlo, p.tstat,
                        tau, st, h, l, g.dq, g.dk, g.dcb, g.dzv, part, d.N, d.NP, d.H, d.D, d.HM, d.B * d.H,
                        d.causal, (float)sgn);
   return hipGetLastError();
@@ -1262,12 +1262,12 @@ __global__ void fill_kernel(float* __restrict__ p, int n, float v) {
 }
 hipError_t launch_fill_zero(float* p, int n, hipStream_t s) {
   if (n <= 0) return hipSuccess;
-  hipLaunchKernelGGL(fill_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p, n, 0.f);
+  MORPHO_KLAUNCH(fill_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p, n, 0.f);
   return hipGetLastError();
 }
 __global__ void flag_kernel(int* __restrict__ p, int v) { *p = v; }
 hipError_t launch_set_flag(int* p, int v, hipStream_t s) {
-  hipLaunchKernelGGL(flag_kernel, dim3(1), dim3(1), 0, s, p, v);
+  MORPHO_KLAUNCH(flag_kernel, dim3(1), dim3(1), 0, s, p, v);
   return hipGetLastError();
 }
 
@@ -1311,7 +1311,7 @@ __global__ __launch_bounds__(256) void soft_tau_reduce_kernel(const float* __res
 
 hipError_t launch_soft_tau_reduce(const float* prep, int nprep, const float* bwd, int nbwd, const float* tau, int sgn,
                                   float* dtau, hipStream_t s) {
-  hipLaunchKernelGGL(soft_tau_reduce_kernel, dim3(1), dim3(256), 0, s, prep, nprep, bwd, nbwd, tau, (float)sgn, dtau);
+  MORPHO_KLAUNCH(soft_tau_reduce_kernel, dim3(1), dim3(256), 0, s, prep, nprep, bwd, nbwd, tau, (float)sgn, dtau);
   return hipGetLastError();
 }
 

@@ -67,6 +67,28 @@ def test_workspace_sizes():
     assert capi.forward_workspace_size(4, 4096, 256, 16, 16) == 0       # head_dim_v 16 unsupported
 
 
+@pytest.mark.parametrize("D,H,m", [(1024, 16, 16), (2048, 32, 64)])
+def test_backward_workspace_grows_only_with_per_token_buffers(D, H, m):
+    """The split-K partials of the weight gradient (splits x D x (H m + D) fp32)
+    are capped: past a few hundred thousand tokens the backward workspace
+    grows only by its per-token buffers (dZ|dV rows, dq, dk, dcb, the row sums,
+    the dO affine rows and the per-block gate partials), not by partials whose
+    split count follows the token count."""
+    from morphottention_amd import capi
+    N = 4096
+    HM, NC = H * m, H * m + D
+    # bytes per token of the buffers that must scale with T (the gate partials
+    # are one row of H m floats per 64 tokens)
+    per_token = 2 * NC + H * 16 + 2 * 4 * HM + 4 * H + 8 * H + 4 * HM / 64
+    w1 = capi.backward_workspace_size(64, N, D, H, m, True)
+    w2 = capi.backward_workspace_size(256, N, D, H, m, True)
+    assert w1 > 0 and w2 > 0
+    grow = (w2 - w1) / (192 * N)
+    assert grow <= per_token * 1.001 + 1, (grow, per_token)
+    # and the partials stay small in absolute terms at a million tokens
+    assert w2 - 256 * N * per_token < 512 << 20
+
+
 def _call_forward(L, ptr, *, M=16, D=64, H=2, ws=1 << 20, mode=0):
     vp = ctypes.c_void_p(ptr)
     lse = ctypes.c_void_p(ptr)
@@ -140,6 +162,9 @@ def test_reference_import_path():
     assert morpho_attention is morphottention_amd.morpho_attention
     assert morphottention.autograd.MorphoAttention is MorphoAttention
     assert ops is torch.ops.morphottention and add_op_namespace_prefix("forward") == "morphottention::forward"
+    # the reference autograd's fallback loader name (autograd.py:10-13, _cmake_ops.py:15-30)
+    from morphottention._cmake_ops import add_op_namespace_prefix as prefix2, ops as ops2
+    assert ops2 is ops and prefix2 is add_op_namespace_prefix
     mod = MorphoAttention(64, 2, 16, dtype=torch.float16, device="cpu")
     with pytest.raises(ValueError, match="CUDA tensor"):
         mod(torch.randn(1, 4, 64, dtype=torch.float16))

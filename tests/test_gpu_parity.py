@@ -73,19 +73,20 @@ def rel_err(g, ref):
     return (g - ref).abs().max().item() / max(ref.abs().max().item(), 1e-300)
 
 
-def check_phi_path_fp64(name, grads, ref32_grads, ref64_grads, heads=None, m=None):
-    """The HIP soft-hypercube gradients must be at least as close to the fp64
-    evaluation as the fp32 oracle is: per tensor, the bar is the fp32 oracle's
-    own relative error against fp64, or GRAD_TOL where that is smaller. With
-    ``heads = (h0, h1)`` only those heads' slices are compared (the fp64
-    reference was evaluated for them alone)."""
+def check_phi_path_fp64(name, grads, ref32_grads, ref64_grads, heads=None, m=None, bars=None):
+    """The HIP soft-hypercube gradients against the fp64 evaluation of the
+    oracle, per tensor at GRAD_TOL, or at ``bars[name]`` where given (the fp16
+    storage budget of tests/phi_budget.py for the saturated fixture). The fp32
+    oracle's own error against fp64 is printed beside. With ``heads = (h0,
+    h1)`` only those heads' slices are compared (the fp64 reference was
+    evaluated for them alone)."""
     for n in PHI_PATH:
         i = GRAD_NAMES.index(n)
         sl = (slice(None),) if heads is None else (
             (slice(None), slice(heads[0] * m, heads[1] * m)) if n == "dW_phi" else (slice(heads[0], heads[1]),))
         g, r32, r64 = grads[i][sl], ref32_grads[i][sl], ref64_grads[i][sl]
         e_hip, e_32 = rel_err(g, r64), rel_err(r32, r64)
-        bar = max(GRAD_TOL, e_32)
+        bar = GRAD_TOL if bars is None else max(GRAD_TOL, bars[n])
         _say(f"[parity-fp64] {name}: {n} HIP {e_hip:.3e} vs fp32 oracle {e_32:.3e} (bar {bar:.3e}, "
              f"max|ref| {r64.abs().max().item():.3e})")
         assert torch.isfinite(g).all()
@@ -164,9 +165,15 @@ def test_golden_fixture(path):
     check(os.path.basename(path), out, lse, grads, torch.from_numpy(d["out"]).cuda(),
           torch.from_numpy(d["lse"]).cuda(), ref, ill_conditioned=ill)
     if ill:
-        # the fixture holds fp64 gradients: compare HIP and the fp32 oracle with them
+        # the fixture holds fp64 gradients. There the phi path's accuracy is
+        # set by fp16 storage of dS and dZ (subnormal for the tiny terms of
+        # one-hot rows): the bar is 1.5 times the fp64 emulation of exactly
+        # those storage points (tests/phi_budget.py; 4.7e-2 for dW_phi, 2.7e-2
+        # for the gates), not the fp32 oracle's own error (0.54).
+        import phi_budget
+        budget = phi_budget.phi_path_budget(path)
         _, _, ref32 = oracle(t["x"], params, H, m, scale, causal, t["dout"])
-        check_phi_path_fp64(os.path.basename(path), grads, ref32, ref)
+        check_phi_path_fp64(os.path.basename(path), grads, ref32, ref, bars={n: 1.5 * v for n, v in budget.items()})
 
 
 # ------------------------------------------------------------------ BASELINE configs
@@ -192,14 +199,17 @@ def test_baseline_config(name):
     ill = c.get("ill", ())
     check(name, out, lse, grads, ref_out, ref_lse, ref_grads, ill_conditioned=ill)
     if ill:
-        # fp64 oracle on the first 8 heads (all batch rows): their dW_phi
-        # columns and gate rows are exact, and 8 heads bound its run time
-        heads = (0, 8)
-        _say(f"[case] {name}: fp64 oracle, heads {heads}")
-        _, _, ref64 = mo.morpho_attention_ref_grads(x, *params, c["H"], c["m"], scale=c["scale"],
-                                                    causal=c["causal"], dout=dout, dtype=torch.float64,
-                                                    batch_chunk=1, head_chunk=8, heads=heads)
-        check_phi_path_fp64(name, grads, ref_grads, ref64, heads=heads, m=c["m"])
+        # fp64 oracle on every head, 8 at a time (all batch rows): each
+        # chunk's dW_phi columns and gate rows are exact, and each is asserted
+        # at GRAD_TOL against them
+        for h0 in range(0, c["H"], 8):
+            heads = (h0, min(h0 + 8, c["H"]))
+            _say(f"[case] {name}: fp64 oracle, heads {heads}")
+            _, _, ref64 = mo.morpho_attention_ref_grads(x, *params, c["H"], c["m"], scale=c["scale"],
+                                                        causal=c["causal"], dout=dout, dtype=torch.float64,
+                                                        batch_chunk=1, head_chunk=8, heads=heads)
+            check_phi_path_fp64(f"{name} heads {heads}", grads, ref_grads, ref64, heads=heads, m=c["m"])
+            del ref64
 
 
 # ------------------------------------------------------------------ shape / option matrix
@@ -240,6 +250,34 @@ def test_ragged_lengths(N):
         out, lse, grads = run_hip(x, params, H, m, 1.0, causal, dout)
         check(f"ragged N={N} causal={causal}", out, lse, grads, *oracle(x, params, H, m, 1.0, causal, dout),
               zero_phi_path=(N == 1))
+
+
+def test_single_key_output_is_v_hi_bitwise():
+    """With one key the softmax weight is exactly 1, and the output is
+    fp16(V_hi + r 2^-12), r the e4m3 remainder of V - V_hi rounded toward zero:
+    it must round back to V_hi bit for bit, the value the backward's dP = dO
+    V_hi^T sees. 64 x 1024 values at inputs x3 sweep the remainder over its
+    range, both signs, subnormal e4m3 codes included; a remainder rounded to
+    nearest instead overshoots the fp16 rounding midpoint for values of V
+    near it. V_hi and r are read from the forward workspace (carved as
+    capi.hip's carve_proj: qa, ka, then vt [B H, dv, NP] fp16 and vlo
+    [B H, NP / 64, dv, 64] e4m3; key 0 sits at column and byte 0)."""
+    B, N, D, H, m = 64, 1, 1024, 16, 16
+    _say("[case] single key: out == V_hi bitwise")
+    x, params, _ = make_inputs(B, N, D, H, m, seed=21, x_mult=3.0)
+    out, _, ws = torch.ops.morphottention.forward_train(x, *params, H, m, 1.0, False)
+    torch.cuda.synchronize()
+    al = lambda n: (n + 255) // 256 * 256  # noqa: E731
+    bh, dv, NP, CW = B * H, D // H, 64, 2 * m + 8
+    o_vt = 2 * al(bh * N * CW * 2)
+    o_vlo = o_vt + al(bh * dv * NP * 2)
+    vt = ws[o_vt:o_vt + bh * dv * NP * 2].view(torch.float16).view(bh, dv, NP)[:, :, 0]
+    vlo = ws[o_vlo:o_vlo + bh * dv * NP].view(torch.float8_e4m3fn).view(bh, dv, NP)[:, :, 0].float()
+    assert (vlo != 0).float().mean().item() > 0.9  # the remainders are carried
+    assert (vlo.abs() < 2.0 ** -6).any()  # subnormal e4m3 codes occur
+    # the stored pair rounds back to V_hi, and the kernel's output is exactly V_hi
+    assert torch.equal((vt.float() + vlo * 2.0 ** -12).half(), vt)
+    assert torch.equal(out.view(bh, dv), vt)
 
 
 def test_scale_zero_is_a_mean():
