@@ -206,6 +206,15 @@ __device__ __forceinline__ f32x16 code_dot(const f16x8 (&kf)[M / 8], const f16x8
   return acc;
 }
 
+// The exponent's code part from the hi chunks alone (hi.hi): fp16 codes, so
+// ~2^-11 relative per term instead of ~2^-22.
+template <int M, bool KEY_A>
+__device__ __forceinline__ f32x16 code_dot_hi(const f16x8 (&kf)[M / 8], const f16x8 (&qf)[M / 8], f32x16 acc) {
+#pragma unroll
+  for (int i = 0; i < M / 16; ++i) acc = KEY_A ? mfma16(kf[i], qf[i], acc) : mfma16(qf[i], kf[i], acc);
+  return acc;
+}
+
 // Workgroups are dispatched round-robin over the 8 XCDs (id % 8), each with
 // its own L2. Map a 1-D grid of 8 * ceil(BH / 8) * nblk workgroups so that all
 // blocks of one (batch, head) run on the same XCD and share its L2: XCD x

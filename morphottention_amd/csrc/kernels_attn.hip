@@ -724,7 +724,12 @@ struct BwdCfg {
 // holds {1, 1, -(lse - b)} by now (written by the forward, or by bwd_prep when
 // the backward computed the projection itself); the dO rows come from
 // grad_out and their affine block {-delta} from bwd_prep's aug rows.
-template <int M, int DV, bool MD>
+// HILO: the recomputed scores use the codes' hi and lo chunks (exact to
+// ~2^-22, as in the forward); without it only the hi chunks (one MFMA instead
+// of three per 16 codes). The backward's P is then exp2 of a score off by
+// ~2^-11 of its code terms, which moves the gradients by ~1e-3 relative for
+// codes in [0, 1] at m = 16 (the launcher uses it only there).
+template <int M, int DV, bool MD, bool HILO>
 __global__ __launch_bounds__((BwdCfg<M, DV>::NT), (BwdCfg<M, DV>::MIN_WG)) void attn_bwd_kernel(const f16* __restrict__ qa, const f16* __restrict__ ka,
                                                        const f16* __restrict__ vt, const f16* __restrict__ aug,
                                                        const f16* __restrict__ grad_out, float* __restrict__ dq,
@@ -751,6 +756,7 @@ __global__ __launch_bounds__((BwdCfg<M, DV>::NT), (BwdCfg<M, DV>::MIN_WG)) void 
   const f16 one = (f16)1.f, zero = (f16)0.f;
 
   // ---- per-wave key-side operands, loaded once
+  constexpr int KCH = HILO ? C::NCH : C::NCH / 2;  // code chunks the scores read
   f16x8 kf[C::NCH];
   f16x4 kaug = {};
   f16x8 vf[DV / 16];
@@ -761,7 +767,7 @@ __global__ __launch_bounds__((BwdCfg<M, DV>::NT), (BwdCfg<M, DV>::MIN_WG)) void 
   if (kvalid) {
     const f16* krow = ka + (rowbase + key) * C::CW;
 #pragma unroll
-    for (int c = 0; c < C::NCH; ++c) kf[c] = *reinterpret_cast<const f16x8*>(krow + chunk_off<M>(c) + 8 * h32);
+    for (int c = 0; c < KCH; ++c) kf[c] = *reinterpret_cast<const f16x8*>(krow + chunk_off<M>(c) + 8 * h32);
     kaug = *reinterpret_cast<const f16x4*>(krow + M + 4 * h32);
     // V_hi[key][16c + 8 h32 + j] from the transposed layout (a wave reads 32
     // consecutive keys of each value column)
@@ -1059,10 +1065,10 @@ __global__ __launch_bounds__((BwdCfg<M, DV>::NT), (BwdCfg<M, DV>::MIN_WG)) void 
     // swap23 order; lane: key)
     auto scores = [&](int sb, f32x16& s, f32x16& dp) {
       const char* qsb = tQ + 32 * sb * C::QRB;
-      f16x8 qfr[C::NCH];
+      f16x8 qfr[C::NCH] = {};
 #pragma unroll
-      for (int c = 0; c < C::NCH; ++c) qfr[c] = *reinterpret_cast<const f16x8*>(qsb + r_q[c]);
-      s = code_dot<M, false>(kf, qfr, f32x16{});
+      for (int c = 0; c < KCH; ++c) qfr[c] = *reinterpret_cast<const f16x8*>(qsb + r_q[c]);
+      s = HILO ? code_dot<M, false>(kf, qfr, f32x16{}) : code_dot_hi<M, false>(kf, qfr, f32x16{});
       s = mfma8(*reinterpret_cast<const f16x4*>(qsb + r_qa), kaug, s);
       const char* osb = tO + 32 * sb * C::ORB;
       dp = f32x16{};
@@ -1206,18 +1212,28 @@ __global__ __launch_bounds__((BwdCfg<M, DV>::NT), (BwdCfg<M, DV>::MIN_WG)) void 
   }
 }
 
-template <int M, int DV>
-static hipError_t launch_attn_bwd_t(const Dims& d, const ProjBuffers& p, const f16* grad_out, const BwdBuffers& g,
+template <int M, int DV, bool HILO>
+static hipError_t launch_attn_bwd_c(const Dims& d, const ProjBuffers& p, const f16* grad_out, const BwdBuffers& g,
                                     hipStream_t s) {
   using C = BwdCfg<M, DV>;
   const dim3 grid(xcd_grid((d.N + C::KW - 1) / C::KW, d.B * d.H));
   if (d.mask_diag)
-    MORPHO_KLAUNCH((attn_bwd_kernel<M, DV, true>), grid, dim3(C::NT), 0, s, p.qa, p.ka, p.vt, g.aug, grad_out,
+    MORPHO_KLAUNCH((attn_bwd_kernel<M, DV, true, HILO>), grid, dim3(C::NT), 0, s, p.qa, p.ka, p.vt, g.aug, grad_out,
                    g.dq, g.dk, g.dcb, g.dr, g.dzv, d.N, d.NP, d.H, d.D, d.HM, d.B * d.H, d.causal);
   else
-    MORPHO_KLAUNCH((attn_bwd_kernel<M, DV, false>), grid, dim3(C::NT), 0, s, p.qa, p.ka, p.vt, g.aug, grad_out,
+    MORPHO_KLAUNCH((attn_bwd_kernel<M, DV, false, HILO>), grid, dim3(C::NT), 0, s, p.qa, p.ka, p.vt, g.aug, grad_out,
                    g.dq, g.dk, g.dcb, g.dr, g.dzv, d.N, d.NP, d.H, d.D, d.HM, d.B * d.H, d.causal);
   return hipGetLastError();
+}
+
+// Scores from the hi chunks alone at m = 16 with the sigmoid projection
+// (codes in [0, 1]; the forward's scores stay exact); hi and lo elsewhere.
+template <int M, int DV>
+static hipError_t launch_attn_bwd_t(const Dims& d, const ProjBuffers& p, const f16* grad_out, const BwdBuffers& g,
+                                    hipStream_t s) {
+  if constexpr (M == 16)
+    if (d.proj == kProjSigmoid) return launch_attn_bwd_c<M, DV, false>(d, p, grad_out, g, s);
+  return launch_attn_bwd_c<M, DV, true>(d, p, grad_out, g, s);
 }
 
 hipError_t launch_attn_bwd(const Dims& d, const ProjBuffers& p, const f16* grad_out, const BwdBuffers& g,
