@@ -628,6 +628,20 @@ __device__ __forceinline__ int rswz(int r) {
   else if constexpr (RB == 128) return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
   else return ((r & 3) << 2) | ((r >> 2) & 3);
 }
+// Chunk swizzle of the dS^T tile (rows of RB = 128 or 64 bytes: one key's dS
+// over a 64- or 32-query step). It is written with ds_write_b128, which
+// serves 8 consecutive lanes per cycle within a 128-byte bank window (a
+// probe under rocprofv3: rswz's pattern, conflict-free for b128 reads, cost
+// 16 LDS cycles per write, 8 of them conflicts), and read with the
+// transposing 16x16x32 pattern of rswz's case (b). Each aligned group of 8
+// rows takes 8 (RB = 128) or, per row parity, 4 (RB = 64) distinct chunks,
+// and rows r and r + 8 differ in the chunk pair the transposing read touches.
+template <int RB>
+__device__ __forceinline__ int sswz(int r) {
+  static_assert(RB == 64 || RB == 128, "dS^T row bytes");
+  if constexpr (RB == 128) return (r & 7) ^ (((r >> 3) & 1) << 2);
+  else return ((r >> 1) & 3) ^ (((r >> 3) & 1) << 1);
+}
 __host__ __device__ constexpr int pow2_bytes(int x) { return x <= 64 ? 64 : 2 * pow2_bytes((x + 1) / 2); }
 // stored row of logical row r in a tile whose rows are in swap23 order within each 32
 __device__ __forceinline__ int srow23(int r) { return (r & ~31) | swap23(r & 31); }
@@ -900,7 +914,7 @@ __global__ __launch_bounds__((BwdCfg<M, DV>::NT), (BwdCfg<M, DV>::MIN_WG)) void 
   for (int c = 0; c < DV / 16; ++c) r_o[c] = l32 * C::ORB + 16 * ((2 * c + h32) ^ oz);
   const int r_oa = l32 * 16 + 8 * h32;
   const int kr = 32 * w + l32;  // this lane's dS^T row (its key)
-  const int sz = rswz<C::SRB>(kr);
+  const int sz = sswz<C::SRB>(kr);
 
   // ---- dq[q][code] += sum_key dS[q][key] phi[key][code]: 16 x 16 output
   // tiles split over the waves, contraction over all KW keys of the workgroup
@@ -915,7 +929,7 @@ __global__ __launch_bounds__((BwdCfg<M, DV>::NT), (BwdCfg<M, DV>::MIN_WG)) void 
     for (int hh = 0; hh < 2; ++hh) {
       const int row = 8 * (lane >> 4) + ((lane & 15) >> 2) + 4 * hh;
       const int col = 16 * qt + 4 * (lane & 3);
-      d_s[t][hh] = row * C::SRB + 16 * ((col >> 3) ^ rswz<C::SRB>(row)) + 2 * (col & 7);
+      d_s[t][hh] = row * C::SRB + 16 * ((col >> 3) ^ sswz<C::SRB>(row)) + 2 * (col & 7);
     }
   }
   // The key-side operands above are loaded under a condition; without a wait
@@ -1060,7 +1074,9 @@ __global__ __launch_bounds__((BwdCfg<M, DV>::NT), (BwdCfg<M, DV>::MIN_WG)) void 
     char* tS = sdS[PAR];
     // this step's row-sum flag (one affine row per lane; rows repeat when
     // QT = 32), for the next step's rowsum()
-    const bool rs_flag_here = __ballot((float)*reinterpret_cast<const f16*>(tA + 16 * lane + 4) != 0.f) != 0;
+    // (a whole 16-byte affine row per lane: a 2-byte read at a 16-byte stride
+    // was a 4-way bank conflict)
+    const bool rs_flag_here = __ballot((float)reinterpret_cast<const f16x8*>(tA)[lane][2] != 0.f) != 0;
     // S = Q~ K~^T and dP - delta = dO~ V~^T of sub-block sb (rows: queries in
     // swap23 order; lane: key)
     auto scores = [&](int sb, f32x16& s, f32x16& dp) {
