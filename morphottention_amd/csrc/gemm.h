@@ -2,11 +2,16 @@
 //
 // C[m][n] = sum_k A(m, k) B(k, n) over one BM x BN output tile per workgroup
 // of 8 waves (512 threads, two per SIMD) in a WM x WN arrangement, each wave
-// owning a (BM / WM) x (BN / WN) block of 32x32x16 MFMA accumulators. k
-// advances by 64 through two LDS stages that the waves fill by DMA
-// (global_load_lds_dwordx4, 1 KiB per wave instruction): the stage of k-step
-// t + 1 is issued right after the barrier that opens k-step t and lands while
-// t is computed, so no VGPRs hold prefetched data.
+// owning a (BM / WM) x (BN / WN) block of 16x16 accumulators
+// (v_mfma_f32_16x16x32_f16). k advances by 64 through two LDS stages that the
+// waves fill by DMA (global_load_lds_dwordx4, 1 KiB per wave instruction):
+// the stage of k-step t + 1 is issued right after the barrier that opens
+// k-step t and lands while t is computed, so no VGPRs hold prefetched data.
+//
+// Why 16x16x32: sustained over the whole chip, v_mfma_f32_16x16x32_f16 runs
+// at 2.24 PFLOP/s and v_mfma_f32_32x32x16_f16 at 1.82 PFLOP/s (independent
+// chains from registers, 45 ms runs); the same main loop with the former is
+// 5-7 % faster (B4 N4096 D1024 projection and dX shapes, 8192^3).
 //
 // Why these shapes: a 256 x 256 (or 256 x 320) tile moves 64 (72) KiB from L2
 // per 8.4 (10.5) MFLOP. With 256 x 128 tiles the L2 -> CU traffic at the
@@ -19,9 +24,9 @@
 //    the 16 lanes of a read phase hit 16 distinct 4-bank groups.
 //  * k-major ("KM", element (k, row) at p[k * ld + row], e.g. X read as X^T):
 //    LDS rows k of ROWS halves (ROWS a power of two >= 128), chunk c of row k
-//    stored at c ^ ((k & 3) << 2). Fragments come from ds_read_b64_tr_b16 (the
-//    transposing read); the 32 lanes of a phase cover 4 rows x 64 bytes on 64
-//    distinct banks.
+//    stored at c ^ ((k & 3) << 2) ^ (((k >> 3) & 1) << 1). Fragments come from
+//    ds_read_b64_tr_b16 (the transposing read); the 32 lanes of a phase cover
+//    rows {k..k+3, k+8..k+11} x 32 bytes on 64 distinct banks.
 // Rows past the operand's extent load clamped (finite) data that only feeds
 // discarded outputs; k past kend is zeroed in LDS on the last k-step.
 #pragma once
@@ -42,6 +47,7 @@ struct OpTile {
   // KC chunk swizzle: with 8 chunks per row (BK = 64) rows r and r + 1 share a
   // swizzle and 16 rows span 8 values; with 4 (BK = 32) rows r .. r + 3 share.
   __device__ __forceinline__ static int kc_swz(int r) { return BK == 64 ? (r >> 1) & 7 : (r >> 2) & 3; }
+  __device__ __forceinline__ static int km_swz(int k) { return ((k & 3) << 2) ^ (((k >> 3) & 1) << 1); }
   static_assert(KC || (ROWS >= 128 && (ROWS & (ROWS - 1)) == 0), "KM swizzle needs 2^n >= 16 chunks per row");
 
   // Tile row and k of LDS chunk q = 64 piece + lane.
@@ -50,8 +56,8 @@ struct OpTile {
       r = q / kRowChunks;
       k8 = 8 * ((q % kRowChunks) ^ kc_swz(r));  // first k of the chunk
     } else {
-      k8 = q / kRowChunks;                           // the chunk's k
-      r = 8 * ((q % kRowChunks) ^ ((k8 & 3) << 2));  // first row of the chunk
+      k8 = q / kRowChunks;                        // the chunk's k
+      r = 8 * ((q % kRowChunks) ^ km_swz(k8));    // first row of the chunk
     }
   }
 
@@ -86,23 +92,21 @@ struct OpTile {
     }
   }
 
-  // MFMA 32x32x16 operand for the 32-row block at tile row (or column) mn0,
-  // k chunk kc (k = 16 kc .. 16 kc + 15): lane l supplies row mn0 + l % 32,
-  // k = 16 kc + 8 (l / 32) + j.
-  __device__ __forceinline__ static f16x8 frag(const char* s, int mn0, int kc, int lane) {
+  // MFMA 16x16x32 operand for the 16-row block at tile row (or column) mn0,
+  // k chunk kq (k = 32 kq .. 32 kq + 31): lane l supplies row mn0 + l % 16,
+  // k = 32 kq + 8 (l / 16) + j.
+  __device__ __forceinline__ static f16x8 frag(const char* s, int mn0, int kq, int lane) {
     if (KC) {
-      const int row = mn0 + (lane & 31);  // mn0 % 32 == 0, so kc_swz(row) == kc_swz(lane & 31)
-      const int c = (2 * kc + (lane >> 5)) ^ kc_swz(lane & 31);
+      const int row = mn0 + (lane & 15);  // mn0 % 16 == 0, so kc_swz(row) == kc_swz(lane & 15)
+      const int c = (4 * kq + (lane >> 4)) ^ kc_swz(lane & 15);
       return *reinterpret_cast<const f16x8*>(s + row * (BK * 2) + 16 * c);
     } else {
-      const int g = lane >> 4;
-      const int k = 16 * kc + 8 * (g >> 1) + ((lane & 15) >> 2);
-      const int col = mn0 + 16 * (g & 1) + 4 * (lane & 3);
-      const int c = (col >> 3) ^ (((lane >> 2) & 3) << 2);  // (k & 3) == (lane >> 2) & 3
-      const char* p = s + k * (ROWS * 2) + 16 * c + 2 * (col & 7);
+      const int k = 32 * kq + 8 * (lane >> 4) + ((lane & 15) >> 2);
+      const int col = mn0 + 4 * (lane & 3);
+      auto at = [&](int kk) { return s + kk * (ROWS * 2) + 16 * ((col >> 3) ^ km_swz(kk)) + 2 * (col & 7); };
       typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
-      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p + 4 * ROWS * 2));
+      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(at(k)));
+      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(at(k + 4)));
       return __builtin_bit_cast(f16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
     }
   }
@@ -118,7 +122,7 @@ struct Gemm {
   static constexpr int kStageBytes = TA::kBytes + TB::kBytes;
   static constexpr int kLdsBytes = kStages * kStageBytes;
   static constexpr int WTM = BM / WM, WTN = BN / WN;  // wave tile
-  static constexpr int FI = WTM / 32, FJ = WTN / 32;
+  static constexpr int FI = WTM / 16, FJ = WTN / 16;  // 16x16 accumulator blocks
   // DMA pieces of a stage, A's first; wave w issues pieces w, w + 8, ...
   // A's piece count is a multiple of 8, so whether a wave's i-th piece is A or
   // B is known at compile time; the first kP % 8 waves issue one piece more.
@@ -127,7 +131,7 @@ struct Gemm {
   static constexpr int kPBmax = (TB::kDma + kGemmWaves - 1) / kGemmWaves;
   static constexpr int kNhi = (kP + kGemmWaves - 1) / kGemmWaves, kNlo = kP / kGemmWaves;
   static_assert(TA::kDma % kGemmWaves == 0, "A pieces must split evenly over the waves");
-  static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile must be whole 32x32 blocks");
+  static_assert(WTM % 16 == 0 && WTN % 16 == 0 && BK % 32 == 0, "wave tile of whole 16x16 blocks, k-step of whole 32s");
   static_assert((STAGES - 2) * kNhi < 64, "vmcnt range");
 
   // wait until this wave's pieces of the stage issued `ahead` stages before
@@ -141,18 +145,18 @@ struct Gemm {
   }
 
   // Wave w owns rows WTM * (w / WN) .. and columns WTN * (w % WN) .. of the
-  // tile; acc[i][j] holds C rows m0 + WTM * (w / WN) + 32 i + acc_row(r, lane),
-  // columns n0 + WTN * (w % WN) + 32 j + lane % 32.
+  // tile; acc[i][j][r] holds C row m0 + WTM * (w / WN) + 16 i + 4 (lane / 16) + r,
+  // column n0 + WTN * (w % WN) + 16 j + lane % 16.
   // Operands: A (M rows) and B (N rows = columns of C), each one matrix
   // (p, ld); k runs over [kbeg, kend). lds: kLdsBytes, 16-byte aligned.
   __device__ __forceinline__ static void run(const f16* Ap, int64_t lda, const f16* Bp, int64_t ldb, int M, int N,
-                                             int m0, int n0, int kbeg, int kend, char* lds, f32x16 (&acc)[FI][FJ]) {
+                                             int m0, int n0, int kbeg, int kend, char* lds, f32x4 (&acc)[FI][FJ]) {
     const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = w / WN, wn = w % WN;
 #pragma unroll
     for (int i = 0; i < FI; ++i)
 #pragma unroll
-      for (int j = 0; j < FJ; ++j) acc[i][j] = f32x16{};
+      for (int j = 0; j < FJ; ++j) acc[i][j] = f32x4{};
     const int nk = (kend - kbeg + kBK - 1) / kBK;
     if (nk <= 0) return;
     const unsigned sbase = (unsigned)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
@@ -215,16 +219,16 @@ struct Gemm {
       }
       if (t + STAGES - 1 < nk) issue(t + STAGES - 1);
 #pragma unroll
-      for (int kc = 0; kc < kBK / 16; ++kc) {
+      for (int kq = 0; kq < kBK / 32; ++kq) {
         f16x8 a[FI], b[FJ];
 #pragma unroll
-        for (int i = 0; i < FI; ++i) a[i] = TA::frag(sa, WTM * wm + 32 * i, kc, lane);
+        for (int i = 0; i < FI; ++i) a[i] = TA::frag(sa, WTM * wm + 16 * i, kq, lane);
 #pragma unroll
-        for (int j = 0; j < FJ; ++j) b[j] = TB::frag(sb, WTN * wn + 32 * j, kc, lane);
+        for (int j = 0; j < FJ; ++j) b[j] = TB::frag(sb, WTN * wn + 16 * j, kq, lane);
 #pragma unroll
         for (int i = 0; i < FI; ++i)
 #pragma unroll
-          for (int j = 0; j < FJ; ++j) acc[i][j] = mfma16(a[i], b[j], acc[i][j]);
+          for (int j = 0; j < FJ; ++j) acc[i][j] = mfma16x16(a[i], b[j], acc[i][j]);
       }
     }
     // every wave is done with the stages before the caller reuses the LDS

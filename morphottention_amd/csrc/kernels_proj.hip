@@ -74,8 +74,10 @@ hipError_t launch_transpose_weights(const Dims& d, const f16* W_phi, const f16* 
 // the large tiles would leave most CUs idle (few tokens: B8 N1024 D512 H8 m16
 // has 64 large tiles, 320 small ones). The epilogue takes the tile through
 // LDS in 64-row slabs (a slab holds the accumulators of the wave rows whose
-// rows it covers), fp32 with row stride BN + 1 = 1 (mod 64) banks so that both
-// passes below read conflict-free.
+// rows it covers), fp32 with row stride BN + 5 = 5 (mod 64) banks: the value
+// pass below reads 8 rows x 8 columns per wave instruction on 64 distinct
+// banks, and the accumulator stores (16 columns x 4 row groups) are at most
+// 2-way.
 template <int BM, int BN>
 using ProjGemm = Gemm<BM, BN, 4, true, true, 64, 2>;
 
@@ -112,7 +114,7 @@ __global__ __launch_bounds__(kGemmThreads) void proj_fwd_kernel(const f16* __res
                                                                const f16* __restrict__ gate_q,
                                                                const f16* __restrict__ gate_k, Dims d, ProjBuffers p) {
   using G = ProjGemm<BM, BN>;
-  constexpr int SS = BN + 1;  // stage row stride (floats)
+  constexpr int SS = BN + 5;  // stage row stride (floats)
   // epilogue LDS: the 64-row slab, then the tile's gate products G = gq gk
   static_assert(64 * SS * 4 + BN * 4 <= G::kLdsBytes, "epilogue slab and gate table must fit the main loop's LDS");
   __shared__ __align__(16) char smem[G::kLdsBytes];
@@ -125,7 +127,7 @@ __global__ __launch_bounds__(kGemmThreads) void proj_fwd_kernel(const f16* __res
   int tm, tn;
   if (!gemm_tile_map(blockIdx.x, (T + BM - 1) / BM, (NC + BN - 1) / BN, tm, tn)) return;
   const int n0 = tn * BN, m0 = tm * BM;
-  f32x16 acc[G::FI][G::FJ];
+  f32x4 acc[G::FI][G::FJ];
   G::run(X, d.D, p.wt, d.D, T, NC, m0, n0, 0, d.D, smem, acc);
 
   float* stage = reinterpret_cast<float*>(smem);
@@ -150,8 +152,8 @@ __global__ __launch_bounds__(kGemmThreads) void proj_fwd_kernel(const f16* __res
 #pragma unroll
         for (int j = 0; j < G::FJ; ++j)
 #pragma unroll
-          for (int r = 0; r < 16; ++r)
-            stage[(r0 + 32 * i + acc_row(r, lane)) * SS + G::WTN * wn + 32 * j + (lane & 31)] = acc[i][j][r];
+          for (int r = 0; r < 4; ++r)
+            stage[(r0 + 16 * i + 4 * (lane >> 4) + r) * SS + G::WTN * wn + 16 * j + (lane & 15)] = acc[i][j][r];
     }
     __syncthreads();
     const int row0 = m0 + 64 * slab;
@@ -511,7 +513,7 @@ __global__ __launch_bounds__(kGemmThreads) void bwd_gemm_kernel(Dims d, BwdBuffe
     int tm, tn;
     if (!gemm_tile_map(id - a.n_dw, (T + kDxBM - 1) / kDxBM, (d.D + kDxBN - 1) / kDxBN, tm, tn)) return;
     const int m0 = tm * kDxBM, n0 = tn * kDxBN;
-    f32x16 acc[DxGemm::FI][DxGemm::FJ];
+    f32x4 acc[DxGemm::FI][DxGemm::FJ];
     DxGemm::run(g.dzv, NC, a.wcat, NC, T, d.D, m0, n0, 0, NC, smem, acc);
     // fp16 through LDS in 64-row slabs (slab = wave row), then 16-byte row stores
     f16* st = reinterpret_cast<f16*>(smem);
@@ -523,8 +525,8 @@ __global__ __launch_bounds__(kGemmThreads) void bwd_gemm_kernel(Dims d, BwdBuffe
 #pragma unroll
           for (int j = 0; j < DxGemm::FJ; ++j)
 #pragma unroll
-            for (int r = 0; r < 16; ++r)
-              st[(32 * i + acc_row(r, lane)) * kDxStageStride + DxGemm::WTN * wn + 32 * j + (lane & 31)] =
+            for (int r = 0; r < 4; ++r)
+              st[(16 * i + 4 * (lane >> 4) + r) * kDxStageStride + DxGemm::WTN * wn + 16 * j + (lane & 15)] =
                   (f16)acc[i][j][r];
       }
       __syncthreads();
@@ -546,7 +548,7 @@ __global__ __launch_bounds__(kGemmThreads) void bwd_gemm_kernel(Dims d, BwdBuffe
   if (z >= g.splits) return;
   const int m0 = (tl / ntn) * kDwBM, n0 = (tl % ntn) * kDwBN;
   const int kbeg = min(z * a.kchunk, T), kend = min(kbeg + a.kchunk, T);
-  f32x16 acc[DwGemm::FI][DwGemm::FJ];
+  f32x4 acc[DwGemm::FI][DwGemm::FJ];
   DwGemm::run(a.X, d.D, g.dzv, NC, d.D, NC, m0, n0, kbeg, kend, smem, acc);
   const int64_t tot = (int64_t)d.D * NC;
   float* part = g.wpart + (int64_t)z * tot;
@@ -554,10 +556,10 @@ __global__ __launch_bounds__(kGemmThreads) void bwd_gemm_kernel(Dims d, BwdBuffe
   for (int i = 0; i < DwGemm::FI; ++i)
 #pragma unroll
     for (int j = 0; j < DwGemm::FJ; ++j) {
-      const int col = n0 + DwGemm::WTN * wn + 32 * j + (lane & 31);
+      const int col = n0 + DwGemm::WTN * wn + 16 * j + (lane & 15);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = m0 + DwGemm::WTM * wm + 32 * i + acc_row(r, lane);
+      for (int r = 0; r < 4; ++r) {
+        const int row = m0 + DwGemm::WTM * wm + 16 * i + 4 * (lane >> 4) + r;
         if (row < d.D && col < NC) part[(int64_t)row * NC + col] = acc[i][j][r];
       }
     }
