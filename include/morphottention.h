@@ -57,7 +57,17 @@ enum morpho_mode {
    * product form on MFMA (which falls back to them by itself when it cannot
    * guarantee its precision). No reference counterpart; for tests and
    * measurement. */
-  MORPHO_MODE_SOFT_EXACT = 16
+  MORPHO_MODE_SOFT_EXACT = 16,
+  /* morpho_backward only (ignored by the forward, rejected by the soft entry
+   * points): the gradients are the same bits on every run with the same
+   * inputs. The backward's dq and dS row sums are then summed from per-key-
+   * block partials in a fixed order instead of by fp32 atomics; the workspace
+   * grows by (N / keys per block) x the dq buffer
+   * (morpho_backward_workspace_size_for_mode). Without the bit only those
+   * two sums depend on the order of atomics. No reference counterpart: the
+   * reference adds dX and the weight gradients with fp16 atomics
+   * (attention.cu:389-480), so its gradients vary from run to run. */
+  MORPHO_MODE_DETERMINISTIC = 32
 };
 
 enum morpho_status {
@@ -120,6 +130,12 @@ int morpho_forward_noalloc(const void* X, const void* W_phi, const void* gate_q,
  * = 0 this includes room to recompute the projection. */
 size_t morpho_backward_workspace_size(int64_t B, int64_t N, int64_t D, int64_t H, int64_t cube_m,
                                       int have_forward_workspace);
+
+/* The same for the mode bits `causal` that morpho_backward will be given
+ * (0 on invalid sizes or bits). Only MORPHO_MODE_DETERMINISTIC changes the
+ * size: it adds the per-key-block partials. No reference counterpart. */
+size_t morpho_backward_workspace_size_for_mode(int64_t B, int64_t N, int64_t D, int64_t H, int64_t cube_m,
+                                               int have_forward_workspace, int causal);
 
 /* Backward. Replaces attention_backward_kernel_launcher (attention.cuh:33-38)
  * and the launch part of morpho_backward (attention.cpp:59-117).

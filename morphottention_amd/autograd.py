@@ -89,13 +89,17 @@ torch.library.register_autograd(add_op_namespace_prefix("forward"), _forward_bac
 # cube projections (cube.cuh:9-17), which it never wires to its API.
 _MASK_DIAG = 2
 _PROJECTIONS = {"sigmoid": 0, "hardtanh01": 4, "identity": 8}
+# No reference counterpart: a backward whose gradients are the same bits on
+# every run (the dq and row sums from per-key-block partials added in a fixed
+# order instead of fp32 atomics; more workspace).
+_DETERMINISTIC = 32
 
 
-def variant_bits(projection: str = "sigmoid", mask_diag: bool = False) -> int:
+def variant_bits(projection: str = "sigmoid", mask_diag: bool = False, deterministic: bool = False) -> int:
     """Variant argument for ``forward_train`` / ``backward_train``."""
     if projection not in _PROJECTIONS:
         raise ValueError(f"projection must be one of {sorted(_PROJECTIONS)} (got {projection!r})")
-    return _PROJECTIONS[projection] | (_MASK_DIAG if mask_diag else 0)
+    return _PROJECTIONS[projection] | (_MASK_DIAG if mask_diag else 0) | (_DETERMINISTIC if deterministic else 0)
 
 
 class MorphoAttentionFunction(torch.autograd.Function):
@@ -141,17 +145,20 @@ class MorphoAttention(nn.Module):
         compile-time variants).
     :param mask_diag: drop each query's own key (the reference's unwired
         ``MASK_DIAG``).
+    :param deterministic: bitwise run-to-run reproducible gradients (no
+        reference counterpart; the backward needs more workspace).
     """
 
     def __init__(self, dim: int, num_heads: int, cube_m: int, *, scale: float = 1.0, causal: bool = False,
                  dtype: torch.dtype = torch.float16, device: torch.device | str | None = None,
-                 projection: str = "sigmoid", mask_diag: bool = False) -> None:
+                 projection: str = "sigmoid", mask_diag: bool = False, deterministic: bool = False) -> None:
         super().__init__()
         if dim % num_heads != 0:
             raise ValueError(f"dim ({dim}) must be divisible by num_heads ({num_heads})")
-        self.variant = variant_bits(projection, mask_diag)
+        self.variant = variant_bits(projection, mask_diag, deterministic)
         self.projection = projection
         self.mask_diag = mask_diag
+        self.deterministic = deterministic
         self.dim = dim
         self.num_heads = num_heads
         self.cube_m = cube_m
@@ -178,13 +185,15 @@ class MorphoAttention(nn.Module):
 
 
 def morpho_attention(x, W_phi, gate_q, gate_k, W_V, num_heads: int, cube_m: int, *, scale: float = 1.0,
-                     causal: bool = False, projection: str = "sigmoid", mask_diag: bool = False) -> torch.Tensor:
+                     causal: bool = False, projection: str = "sigmoid", mask_diag: bool = False,
+                     deterministic: bool = False) -> torch.Tensor:
     """Apply Morphottention attention with autograd support.
 
     :param x: input activations of shape (B, N, D) on a ROCm device.
     :param projection: ``"sigmoid"`` (default), ``"hardtanh01"`` or ``"identity"``.
     :param mask_diag: drop each query's own key.
+    :param deterministic: bitwise run-to-run reproducible gradients.
     :returns: the attention output, differentiable w.r.t. ``x`` and the parameters.
     """
     return MorphoAttentionFunction.apply(x, W_phi, gate_q, gate_k, W_V, num_heads, cube_m, scale, causal,
-                                         variant_bits(projection, mask_diag))
+                                         variant_bits(projection, mask_diag, deterministic))

@@ -32,6 +32,8 @@ def lib() -> ctypes.CDLL:
         L.morpho_forward_workspace_size.argtypes = [i64] * 5
         L.morpho_backward_workspace_size.restype = sz
         L.morpho_backward_workspace_size.argtypes = [i64] * 5 + [ctypes.c_int]
+        L.morpho_backward_workspace_size_for_mode.restype = sz
+        L.morpho_backward_workspace_size_for_mode.argtypes = [i64] * 5 + [ctypes.c_int, ctypes.c_int]
         L.morpho_forward.restype = ctypes.c_int
         L.morpho_forward.argtypes = [vp] * 5 + [vp, vp] + [i64] * 5 + [ctypes.c_float, ctypes.c_int, vp, sz, vp]
         L.morpho_forward_noalloc.restype = ctypes.c_int
@@ -64,8 +66,13 @@ def forward_workspace_size(B: int, N: int, D: int, H: int, cube_m: int) -> int:
     return int(lib().morpho_forward_workspace_size(B, N, D, H, cube_m))
 
 
-def backward_workspace_size(B: int, N: int, D: int, H: int, cube_m: int, have_forward_workspace: bool) -> int:
-    return int(lib().morpho_backward_workspace_size(B, N, D, H, cube_m, int(have_forward_workspace)))
+def backward_workspace_size(B: int, N: int, D: int, H: int, cube_m: int, have_forward_workspace: bool,
+                            mode: int | None = None) -> int:
+    """Bytes of backward workspace; ``mode`` (the bits morpho_backward gets) matters
+    only with MORPHO_MODE_DETERMINISTIC, which adds the per-key-block partials."""
+    if mode is None:
+        return int(lib().morpho_backward_workspace_size(B, N, D, H, cube_m, int(have_forward_workspace)))
+    return int(lib().morpho_backward_workspace_size_for_mode(B, N, D, H, cube_m, int(have_forward_workspace), mode))
 
 
 def soft_forward_workspace_size(B: int, N: int, D: int, H: int, cube_m: int) -> int:

@@ -71,8 +71,9 @@ int make_dims(int64_t B, int64_t N, int64_t D, int64_t H, int64_t M, float scale
   if (T > (int64_t)1 << 30 || D > 65536 || H * M > 65536)
     return fail(MORPHO_ERR_INVALID_ARGUMENT, "problem too large for 32-bit token indexing");
   if (!__builtin_isfinite(scale)) return fail(MORPHO_ERR_INVALID_ARGUMENT, "scale must be a finite number");
-  if ((causal & ~15) != 0 || (causal & 12) == 12)
-    return fail(MORPHO_ERR_INVALID_ARGUMENT, "invalid mode bits 0x%x (causal | mask_diag | one projection)", causal);
+  if ((causal & ~(15 | MORPHO_MODE_DETERMINISTIC)) != 0 || (causal & 12) == 12)
+    return fail(MORPHO_ERR_INVALID_ARGUMENT,
+                "invalid mode bits 0x%x (causal | mask_diag | one projection | deterministic)", causal);
   d.B = (int)B;
   d.N = (int)N;
   d.NP = (int)((N + 63) / 64 * 64);
@@ -89,6 +90,7 @@ int make_dims(int64_t B, int64_t N, int64_t D, int64_t H, int64_t M, float scale
   d.proj = causal & MORPHO_MODE_PROJ_HARDTANH01 ? kProjHardTanh01
            : causal & MORPHO_MODE_PROJ_IDENTITY ? kProjIdentity
                                                 : kProjSigmoid;
+  d.det = causal & MORPHO_MODE_DETERMINISTIC ? 1 : 0;
   // projection tiles: 256 x 320 when 320 divides H*M + D, else 256 x 256, and
   // 128 x 128 when the large tiles would fill less than one round of the 256
   // CUs and 128 divides H*M + D; the interleaved column order needs whole
@@ -147,6 +149,12 @@ size_t bwd_bytes(const Dims& d) {
   s += align_up((size_t)d.T * (d.HM + d.D) * 2);       // dzv
   s += align_up(nblk * d.HM * 4);                      // gpart
   s += align_up((size_t)dw_splits(d) * d.D * (d.HM + d.D) * 4);  // wpart
+  if (d.det) {
+    const DetLayout l = attn_bwd_det_layout(d);
+    const size_t prow = (size_t)l.nkb * d.B * d.H * l.nq;
+    s += align_up(prow * d.M * 4);  // dqpart
+    s += align_up(prow * 4);        // drpart
+  }
   return s;
 }
 
@@ -162,8 +170,15 @@ BwdBuffers carve_bwd(void* base, const Dims& d) {
   g.dr = reinterpret_cast<float*>(p); p += align_up(bhn * 8);
   g.dzv = reinterpret_cast<_Float16*>(p); p += align_up((size_t)d.T * (d.HM + d.D) * 2);
   g.gpart = reinterpret_cast<float*>(p); p += align_up(nblk * d.HM * 4);
-  g.wpart = reinterpret_cast<float*>(p);
+  g.wpart = reinterpret_cast<float*>(p); p += align_up((size_t)dw_splits(d) * d.D * (d.HM + d.D) * 4);
   g.splits = dw_splits(d);
+  g.dqpart = g.drpart = nullptr;
+  if (d.det) {
+    const DetLayout l = attn_bwd_det_layout(d);
+    const size_t prow = (size_t)l.nkb * d.B * d.H * l.nq;
+    g.dqpart = reinterpret_cast<float*>(p); p += align_up(prow * d.M * 4);
+    g.drpart = reinterpret_cast<float*>(p);
+  }
   return g;
 }
 
@@ -251,6 +266,16 @@ MORPHO_EXPORT size_t morpho_backward_workspace_size(int64_t B, int64_t N, int64_
   Dims d;
   std::string keep = g_last_error;
   const int st = make_dims(B, N, D, H, cube_m, 1.0f, 0, d);
+  g_last_error = keep;
+  if (st != MORPHO_OK) return 0;
+  return bwd_bytes(d) + (have_forward_workspace ? 0 : proj_bytes(d));
+}
+
+MORPHO_EXPORT size_t morpho_backward_workspace_size_for_mode(int64_t B, int64_t N, int64_t D, int64_t H,
+                                                             int64_t cube_m, int have_forward_workspace, int causal) {
+  Dims d;
+  std::string keep = g_last_error;
+  const int st = make_dims(B, N, D, H, cube_m, 1.0f, causal, d);
   g_last_error = keep;
   if (st != MORPHO_OK) return 0;
   return bwd_bytes(d) + (have_forward_workspace ? 0 : proj_bytes(d));
@@ -380,6 +405,7 @@ MORPHO_EXPORT int morpho_backward(const void* grad_out, const void* X, const voi
   // projection computed here still holds its own
   MORPHO_LAUNCH("bwd_prep", launch_bwd_prep(d, p, go, static_cast<const _Float16*>(out), lse, g, have_fwd ? 0 : 1, s));
   MORPHO_LAUNCH("attn_bwd", launch_attn_bwd(d, p, go, g, s));
+  if (d.det) MORPHO_LAUNCH("dq_reduce", launch_dq_det_reduce(d, g, s));
   MORPHO_LAUNCH("proj_bwd_elem", launch_proj_bwd_elem(d, static_cast<const _Float16*>(gate_q),
                                                       static_cast<const _Float16*>(gate_k), p, g, true, s));
   MORPHO_LAUNCH("bwd_gemm", launch_bwd_gemm(d, p, g, static_cast<const _Float16*>(X), static_cast<_Float16*>(dX), s));
@@ -454,6 +480,7 @@ MORPHO_EXPORT int morpho_soft_forward(const void* X, const void* W_phi, const vo
   bool exact = false;
   int st = make_dims(B, N, D, H, cube_m, scale, soft_mode(mode, exact), d);
   if (st != MORPHO_OK) return st;
+  if (d.det) return fail(MORPHO_ERR_UNSUPPORTED, "MORPHO_MODE_DETERMINISTIC applies to the softmax backward only");
   if (!X || !W_phi || !gate_q || !gate_k || !W_V || !out || !zb) return fail(MORPHO_ERR_INVALID_ARGUMENT, "Null pointer");
   if ((st = check_soft_args(tau, sgn)) != MORPHO_OK) return st;
   if (misaligned(X) || misaligned(W_phi) || misaligned(W_V) || misaligned(out) || misaligned(zb))
@@ -494,6 +521,7 @@ MORPHO_EXPORT int morpho_soft_backward(const void* grad_out, const void* X, cons
   bool exact = false;
   int st = make_dims(B, N, D, H, cube_m, scale, soft_mode(mode, exact), d);
   if (st != MORPHO_OK) return st;
+  if (d.det) return fail(MORPHO_ERR_UNSUPPORTED, "MORPHO_MODE_DETERMINISTIC applies to the softmax backward only");
   if (!grad_out || !X || !W_phi || !gate_q || !gate_k || !W_V || !zb)
     return fail(MORPHO_ERR_INVALID_ARGUMENT, "Null input pointer");
   if (!dX || !dW_phi || !d_gate_q || !d_gate_k || !dW_V || !dtau)

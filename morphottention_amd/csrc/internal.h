@@ -22,6 +22,7 @@ struct Dims {
   int causal;
   int mask_diag;          // drop key j == query i
   int proj;               // cube projection: kProjSigmoid, kProjHardTanh01 or kProjIdentity
+  int det;                // deterministic backward: dq and row sums from per-key-block partials
   // Column order of the forward projection's B operand (wt rows): tiles of
   // PBN columns; when PCPT > 0 tile j holds code columns [j PCPT, (j+1) PCPT)
   // then value columns [j PVPT, (j+1) PVPT), so every tile does the same
@@ -91,6 +92,14 @@ struct BwdBuffers {
   float* gpart;    // [n_gate_blocks, H*M] partial sums of phi (2 dk - dcb), the gate factor dG
   float* wpart;    // [splits, D, H*M + D] split-K partials of [dW_phi | dW_V]
   int splits;
+  float* dqpart;   // deterministic mode only (else null): [nkb, B*H, NQ, M] per-key-block dq sums
+  float* drpart;   //                                      [nkb, B*H, NQ] per-key-block row sums
+};
+
+// Layout of the deterministic backward's partials: KW keys per key block,
+// nkb key blocks, rows padded to nq (N rounded up to the query step).
+struct DetLayout {
+  int kw, nkb, nq;
 };
 
 constexpr int kGateTokensPerBlock = 64;
@@ -115,6 +124,8 @@ int dw_splits(const Dims& d);
 hipError_t launch_attn_fwd(const Dims& d, const ProjBuffers& p, _Float16* out, float* lse, hipStream_t s);
 hipError_t launch_bwd_prep(const Dims& d, const ProjBuffers& p, const _Float16* grad_out, const _Float16* out,
                            const float* lse, const BwdBuffers& g, int write_q, hipStream_t s);
+DetLayout attn_bwd_det_layout(const Dims& d);
+hipError_t launch_dq_det_reduce(const Dims& d, const BwdBuffers& g, hipStream_t s);
 hipError_t launch_attn_bwd(const Dims& d, const ProjBuffers& p, const _Float16* grad_out, const BwdBuffers& g,
                            hipStream_t s);
 

@@ -743,7 +743,14 @@ struct BwdCfg {
 // of three per 16 codes). The backward's P is then exp2 of a score off by
 // ~2^-11 of its code terms, which moves the gradients by ~1e-3 relative for
 // codes in [0, 1] at m = 16 (the launcher uses it only there).
-template <int M, int DV, bool MD, bool HILO>
+// DET: instead of adding to dq and dr with atomics, every workgroup stores its
+// sums over its own keys into per-key-block partials ([nkb][B*H][NQ][M] and
+// [nkb][B*H][NQ] fp32, NQ = N rounded up to QT, so rows past N land in
+// padding); dq_det_reduce adds them in key-block order, which makes dq and
+// the row sums identical from run to run. A store replaces each atomic one
+// for one, so the tile waits count the same operations (waves without a
+// row-sum tile issue no row-sum store and wait as if they had sent none).
+template <int M, int DV, bool MD, bool HILO, bool DET>
 __global__ __launch_bounds__((BwdCfg<M, DV>::NT), (BwdCfg<M, DV>::MIN_WG)) void attn_bwd_kernel(const f16* __restrict__ qa, const f16* __restrict__ ka,
                                                        const f16* __restrict__ vt, const f16* __restrict__ aug,
                                                        const f16* __restrict__ grad_out, float* __restrict__ dq,
@@ -768,6 +775,10 @@ __global__ __launch_bounds__((BwdCfg<M, DV>::NT), (BwdCfg<M, DV>::MIN_WG)) void 
   const int64_t rowbase = (int64_t)bh * N;
   const int64_t tokbase = (int64_t)b * N;
   const f16 one = (f16)1.f, zero = (f16)0.f;
+  // DET: this workgroup's slices of the partials
+  const int NQ = (N + C::QT - 1) / C::QT * C::QT;
+  float* const dqk = dq + ((int64_t)kblk * BH + bh) * NQ * M;
+  float* const drk = dr + ((int64_t)kblk * BH + bh) * NQ;
 
   // ---- per-wave key-side operands, loaded once
   constexpr int KCH = HILO ? C::NCH : C::NCH / 2;  // code chunks the scores read
@@ -988,6 +999,22 @@ __global__ __launch_bounds__((BwdCfg<M, DV>::NT), (BwdCfg<M, DV>::MIN_WG)) void 
   // issued right after the fragments of step st are read, so that it overlaps
   // the next step's body
   auto rowsum = [&](int st) {
+    if constexpr (DET) {  // every step stores its sums (0 without a flagged row) from the row-sum waves
+      rs_sent = rs_wave;
+      if (!rs_wave) return;  // uniform
+      const int qs = qstep(st);
+      f32x4 racc = {};
+      if (rs_need) {  // uniform
+        const f16 one16 = (f16)1.f;
+        const f16x8 ones = {one16, one16, one16, one16, one16, one16, one16, one16};
+#pragma unroll
+        for (int kc = 0; kc < C::KW / 32; ++kc) racc = mfma16x16(dqa[0][kc], ones, racc);
+      }
+      const int j = lane & 3;
+      const float rsum = j == 0 ? racc[0] : j == 1 ? racc[1] : j == 2 ? racc[2] : racc[3];
+      if ((lane & 15) < 4) drk[qs + rs_row] = rsum;
+      return;
+    }
     rs_sent = rs_need;
     if (!rs_need) return;  // uniform
     const int qs = qstep(st);
@@ -1022,6 +1049,11 @@ __global__ __launch_bounds__((BwdCfg<M, DV>::NT), (BwdCfg<M, DV>::MIN_WG)) void 
         else
           phi_op = tfrag16<C::PRB>(sPk, 32 * kc, 16 * (tile / (C::QT / 16)), lane);
         acc = mfma16x16(dqa[t][kc], phi_op, acc);
+      }
+      if constexpr (DET) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dqk[(int64_t)qs * M + (unsigned)a_off[t] + r * M] = acc[r];
+        continue;
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -1228,18 +1260,30 @@ __global__ __launch_bounds__((BwdCfg<M, DV>::NT), (BwdCfg<M, DV>::MIN_WG)) void 
   }
 }
 
-template <int M, int DV, bool HILO>
+template <int M, int DV, bool HILO, bool DET>
 static hipError_t launch_attn_bwd_c(const Dims& d, const ProjBuffers& p, const f16* grad_out, const BwdBuffers& g,
                                     hipStream_t s) {
   using C = BwdCfg<M, DV>;
   const dim3 grid(xcd_grid((d.N + C::KW - 1) / C::KW, d.B * d.H));
+  float* const dq = DET ? g.dqpart : g.dq;
+  float* const dr = DET ? g.drpart : g.dr;
   if (d.mask_diag)
-    MORPHO_KLAUNCH((attn_bwd_kernel<M, DV, true, HILO>), grid, dim3(C::NT), 0, s, p.qa, p.ka, p.vt, g.aug, grad_out,
-                   g.dq, g.dk, g.dcb, g.dr, g.dzv, d.N, d.NP, d.H, d.D, d.HM, d.B * d.H, d.causal);
+    MORPHO_KLAUNCH((attn_bwd_kernel<M, DV, true, HILO, DET>), grid, dim3(C::NT), 0, s, p.qa, p.ka, p.vt, g.aug,
+                   grad_out, dq, g.dk, g.dcb, dr, g.dzv, d.N, d.NP, d.H, d.D, d.HM, d.B * d.H, d.causal);
   else
-    MORPHO_KLAUNCH((attn_bwd_kernel<M, DV, false, HILO>), grid, dim3(C::NT), 0, s, p.qa, p.ka, p.vt, g.aug, grad_out,
-                   g.dq, g.dk, g.dcb, g.dr, g.dzv, d.N, d.NP, d.H, d.D, d.HM, d.B * d.H, d.causal);
+    MORPHO_KLAUNCH((attn_bwd_kernel<M, DV, false, HILO, DET>), grid, dim3(C::NT), 0, s, p.qa, p.ka, p.vt, g.aug,
+                   grad_out, dq, g.dk, g.dcb, dr, g.dzv, d.N, d.NP, d.H, d.D, d.HM, d.B * d.H, d.causal);
   return hipGetLastError();
+}
+
+template <int M, int DV, bool HILO>
+static hipError_t launch_attn_bwd_h(const Dims& d, const ProjBuffers& p, const f16* grad_out, const BwdBuffers& g,
+                                    hipStream_t s) {
+  if (d.det) {
+    if (!g.dqpart || !g.drpart) return hipErrorInvalidValue;
+    return launch_attn_bwd_c<M, DV, HILO, true>(d, p, grad_out, g, s);
+  }
+  return launch_attn_bwd_c<M, DV, HILO, false>(d, p, grad_out, g, s);
 }
 
 // Scores from the hi chunks alone at m = 16 with the sigmoid projection
@@ -1248,13 +1292,89 @@ template <int M, int DV>
 static hipError_t launch_attn_bwd_t(const Dims& d, const ProjBuffers& p, const f16* grad_out, const BwdBuffers& g,
                                     hipStream_t s) {
   if constexpr (M == 16)
-    if (d.proj == kProjSigmoid) return launch_attn_bwd_c<M, DV, false>(d, p, grad_out, g, s);
-  return launch_attn_bwd_c<M, DV, true>(d, p, grad_out, g, s);
+    if (d.proj == kProjSigmoid) return launch_attn_bwd_h<M, DV, false>(d, p, grad_out, g, s);
+  return launch_attn_bwd_h<M, DV, true>(d, p, grad_out, g, s);
 }
 
 hipError_t launch_attn_bwd(const Dims& d, const ProjBuffers& p, const f16* grad_out, const BwdBuffers& g,
                            hipStream_t s) {
   MORPHO_MDV_DISPATCH(launch_attn_bwd_t, d, p, grad_out, g, s);
+}
+
+// ---------------------------------------------------------------- deterministic dq
+template <int M, int DV>
+static hipError_t det_layout_t(const Dims& d, DetLayout* l) {
+  using C = BwdCfg<M, DV>;
+  l->kw = C::KW;
+  l->nkb = (d.N + C::KW - 1) / C::KW;
+  l->nq = (d.N + C::QT - 1) / C::QT * C::QT;
+  return hipSuccess;
+}
+
+DetLayout attn_bwd_det_layout(const Dims& d) {
+  DetLayout l{0, 0, 0};
+  auto f = [&]() -> hipError_t { MORPHO_MDV_DISPATCH(det_layout_t, d, &l); };
+  (void)f();
+  return l;
+}
+
+// dq[bh][q] = sum over the key blocks kb that saw query q (all of them, or kb
+// <= q / KW under the causal mask), in increasing kb, of the partials; the
+// row sum dr[bh][q].x the same way (its .y, the diagonal weight, stays).
+// One lane per 4 codes of a row: a wave reads 64 consecutive float4 of one
+// key block's partials per load.
+template <int M>
+__global__ __launch_bounds__(256) void dq_det_reduce_kernel(const float* __restrict__ dqpart,
+                                                            const float* __restrict__ drpart, float* __restrict__ dq,
+                                                            float* __restrict__ dr, int N, int NQ, int BH, int nkb,
+                                                            int KW, int causal) {
+  constexpr int V = M / 4;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)BH * N * V) return;
+  const int64_t row = idx / V;  // bh N + q
+  const int c4 = (int)(idx - row * V);
+  const int bh = (int)(row / N), q = (int)(row - (int64_t)bh * N);
+  const int nk = causal ? min(q / KW + 1, nkb) : nkb;
+  const int64_t prow = (int64_t)bh * NQ + q, kstride = (int64_t)BH * NQ;
+  const float4* src = reinterpret_cast<const float4*>(dqpart + prow * M) + c4;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int kb = 0; kb < nk; ++kb) {
+    const float4 v = src[kb * kstride * V];
+    acc.x += v.x;
+    acc.y += v.y;
+    acc.z += v.z;
+    acc.w += v.w;
+  }
+  reinterpret_cast<float4*>(dq + row * M)[c4] = acc;
+  if (c4 == 0) {
+    float r = 0.f;
+    for (int kb = 0; kb < nk; ++kb) r += drpart[kb * kstride + prow];
+    dr[2 * row] = r;
+  }
+}
+
+hipError_t launch_dq_det_reduce(const Dims& d, const BwdBuffers& g, hipStream_t s) {
+  if (!g.dqpart || !g.drpart) return hipErrorInvalidValue;
+  const DetLayout l = attn_bwd_det_layout(d);
+  const int BH = d.B * d.H;
+  const int64_t n = (int64_t)BH * d.N * (d.M / 4);
+  const dim3 grid((unsigned)((n + 255) / 256));
+  switch (d.M) {
+    case 16:
+      MORPHO_KLAUNCH(dq_det_reduce_kernel<16>, grid, dim3(256), 0, s, g.dqpart, g.drpart, g.dq, g.dr, d.N, l.nq, BH,
+                     l.nkb, l.kw, d.causal);
+      break;
+    case 32:
+      MORPHO_KLAUNCH(dq_det_reduce_kernel<32>, grid, dim3(256), 0, s, g.dqpart, g.drpart, g.dq, g.dr, d.N, l.nq, BH,
+                     l.nkb, l.kw, d.causal);
+      break;
+    case 64:
+      MORPHO_KLAUNCH(dq_det_reduce_kernel<64>, grid, dim3(256), 0, s, g.dqpart, g.drpart, g.dq, g.dr, d.N, l.nq, BH,
+                     l.nkb, l.kw, d.causal);
+      break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
 }
 
 }  // namespace morpho

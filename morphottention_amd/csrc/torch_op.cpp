@@ -53,11 +53,15 @@ morpho_stream_t current_stream(const at::Tensor& X) {
 }
 
 // The ABI's mode word: bit 0 causal, the other bits the variant
-// (MORPHO_MODE_MASK_DIAG, MORPHO_MODE_PROJ_*), which only the *_train ops take.
+// (MORPHO_MODE_MASK_DIAG, MORPHO_MODE_PROJ_*, MORPHO_MODE_DETERMINISTIC), which
+// only the *_train ops take.
 int mode_of(bool causal, int64_t variant) {
-  TORCH_CHECK((variant & ~(int64_t)(MORPHO_MODE_MASK_DIAG | MORPHO_MODE_PROJ_HARDTANH01 | MORPHO_MODE_PROJ_IDENTITY)) == 0,
-              "variant must combine MORPHO_MODE_MASK_DIAG (2) with at most one of MORPHO_MODE_PROJ_HARDTANH01 (4) "
-              "and MORPHO_MODE_PROJ_IDENTITY (8), got ", variant);
+  TORCH_CHECK((variant & ~(int64_t)(MORPHO_MODE_MASK_DIAG | MORPHO_MODE_PROJ_HARDTANH01 | MORPHO_MODE_PROJ_IDENTITY |
+                                    MORPHO_MODE_DETERMINISTIC)) == 0 &&
+                  (variant & (MORPHO_MODE_PROJ_HARDTANH01 | MORPHO_MODE_PROJ_IDENTITY)) !=
+                      (MORPHO_MODE_PROJ_HARDTANH01 | MORPHO_MODE_PROJ_IDENTITY),
+              "variant must combine MORPHO_MODE_MASK_DIAG (2) and MORPHO_MODE_DETERMINISTIC (32) with at most one "
+              "of MORPHO_MODE_PROJ_HARDTANH01 (4) and MORPHO_MODE_PROJ_IDENTITY (8), got ", variant);
   return (causal ? MORPHO_MODE_CAUSAL : 0) | (int)variant;
 }
 
@@ -114,7 +118,7 @@ std::vector<at::Tensor> backward_impl(const at::Tensor& grad_out, const at::Tens
   auto d_gate_q = at::empty_like(gate_q);
   auto d_gate_k = at::empty_like(gate_k);
   auto dW_V = at::empty_like(W_V);
-  const size_t ws_bytes = morpho_backward_workspace_size(s.B, s.N, s.D, s.H, s.M, fwd_ptr != nullptr);
+  const size_t ws_bytes = morpho_backward_workspace_size_for_mode(s.B, s.N, s.D, s.H, s.M, fwd_ptr != nullptr, mode);
   TORCH_CHECK(ws_bytes > 0, "morphottention backward: unsupported sizes");
   auto ws = at::empty({(int64_t)ws_bytes}, X.options().dtype(at::kByte));
   raise_on(morpho_backward(grad_out.data_ptr(), X.data_ptr(), W_phi.data_ptr(), gate_q.data_ptr(), gate_k.data_ptr(),
@@ -162,6 +166,8 @@ void check_tau(const at::Tensor& tau, const at::Tensor& X) {
 
 // The soft ops also accept MORPHO_MODE_SOFT_EXACT (16) in `variant`.
 int soft_mode_of(bool causal, int64_t variant) {
+  TORCH_CHECK((variant & MORPHO_MODE_DETERMINISTIC) == 0,
+              "MORPHO_MODE_DETERMINISTIC (32) applies to the softmax backward only");
   return mode_of(causal, variant & ~(int64_t)MORPHO_MODE_SOFT_EXACT) | (int)(variant & MORPHO_MODE_SOFT_EXACT);
 }
 

@@ -115,6 +115,49 @@ def test_forward_validation_never_reaches_the_device():
     assert st == 1 and L.morpho_last_error() == b"Null input pointer"
 
 
+# (N, D, H, m): keys per backward key block KW and query step QT of the
+# kernel configuration, which fix the size of the deterministic partials
+DET_LAYOUTS = [((4, 4096, 1024, 16, 16), 128, 64), ((1, 16384, 1024, 16, 32), 256, 32),
+               ((16, 2048, 2048, 32, 64), 256, 32), ((2, 1000, 1024, 8, 32), 128, 32),
+               ((3, 777, 512, 8, 16), 128, 64), ((1, 1, 64, 2, 64), 256, 32)]
+
+
+@pytest.mark.parametrize("shape,kw,qt", DET_LAYOUTS, ids=lambda v: str(v))
+def test_deterministic_workspace_adds_the_partials(shape, kw, qt):
+    """MORPHO_MODE_DETERMINISTIC adds [nkb, B*H, NQ, M] + [nkb, B*H, NQ] fp32
+    partials (nkb = ceil(N / KW) key blocks, NQ = N rounded up to the query
+    step), each 256-byte aligned; no other mode bit changes the size."""
+    from morphottention_amd import capi
+    B, N, D, H, m = shape
+    al = lambda n: (n + 255) // 256 * 256  # noqa: E731
+    nkb, nq = -(-N // kw), -(-N // qt) * qt
+    rows = nkb * B * H * nq
+    for have_fwd in (True, False):
+        base = capi.backward_workspace_size(B, N, D, H, m, have_fwd)
+        for mode in (0, 1, 2, 3, 4, 9):
+            assert capi.backward_workspace_size(B, N, D, H, m, have_fwd, mode) == base
+        for mode in (32, 33, 38):
+            assert capi.backward_workspace_size(B, N, D, H, m, have_fwd, mode) == base + al(rows * m * 4) + al(rows * 4)
+        assert capi.backward_workspace_size(B, N, D, H, m, have_fwd, 64) == 0      # unknown bit
+        assert capi.backward_workspace_size(B, N, D, H, m, have_fwd, 32 | 12) == 0  # two projections
+
+
+def test_deterministic_mode_bit_is_plumbed():
+    from morphottention_amd import MorphoAttention
+    from morphottention_amd.autograd import variant_bits
+    assert variant_bits(deterministic=True) == 32
+    assert variant_bits("identity", True, True) == 8 | 2 | 32
+    mod = MorphoAttention(64, 2, 16, device="cpu", deterministic=True)
+    assert mod.variant == 32 and mod.deterministic
+    # the size query keeps the thread's last error, like the other size queries
+    from morphottention_amd import capi
+    L = capi.lib()
+    vp = ctypes.c_void_p(0)
+    L.morpho_forward(vp, vp, vp, vp, vp, vp, vp, 2, 8, 64, 2, 16, 1.0, 0, vp, 0, None)
+    assert capi.backward_workspace_size(2, 8, 64, 2, 16, True, 32) > 0
+    assert L.morpho_last_error() == b"Null pointer"
+
+
 REF_SCHEMAS = {
     "forward": "morphottention::forward(Tensor X, Tensor W_phi, Tensor gate_q, Tensor gate_k, Tensor W_V, "
                "int H, int cube_m, float scale, bool causal) -> Tensor[]",
@@ -255,8 +298,12 @@ def test_soft_entry_points_validate_without_the_device():
     assert st == 1 and b"sgn" in L.morpho_last_error()
     st = L.morpho_soft_forward(vp, vp, vp, vp, vp, None, vp, vp, 2, 8, 64, 2, 16, 1.0, 0, 1, vp, ws, None)
     assert st == 1 and b"tau" in L.morpho_last_error()
+    st = L.morpho_soft_forward(vp, vp, vp, vp, vp, vp, vp, vp, 2, 8, 64, 2, 16, 1.0, 64, 1, vp, ws, None)
+    assert st == 1 and b"invalid mode bits" in L.morpho_last_error()  # 16 (SOFT_EXACT) is valid here, 64 is not
     st = L.morpho_soft_forward(vp, vp, vp, vp, vp, vp, vp, vp, 2, 8, 64, 2, 16, 1.0, 32, 1, vp, ws, None)
-    assert st == 1 and b"invalid mode bits" in L.morpho_last_error()  # 16 (SOFT_EXACT) is valid here, 32 is not
+    assert st == 2 and b"softmax backward only" in L.morpho_last_error()  # DETERMINISTIC
+    st = L.morpho_soft_backward(*([vp] * 14), 2, 8, 64, 2, 16, 1.0, 33, 1, None, vp, ws, None)
+    assert st == 2 and b"softmax backward only" in L.morpho_last_error()
     st = L.morpho_soft_forward(vp, vp, vp, vp, vp, vp, vp, vp, 2, 8, 64, 2, 16, 1.0, 16, 1, vp, 64, None)
     assert st == 3 and b"soft forward workspace" in L.morpho_last_error()
     st = L.morpho_soft_backward(*([vp] * 14), 2, 8, 64, 2, 16, 1.0, 0, -3, None, vp, ws, None)

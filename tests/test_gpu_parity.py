@@ -422,6 +422,105 @@ def test_backward_run_to_run_variation_is_rounding_only():
             assert bool((diff <= 2 * ulp).all()), f"{n}: run-to-run difference beyond two fp16 ulps"
 
 
+def _run_det(x, params, H, m, scale, causal, dout, projection, mask_diag, deterministic):
+    from morphottention_amd import morpho_attention
+    leaves = [t.detach().clone().requires_grad_(True) for t in (x, *params)]
+    out = morpho_attention(leaves[0], *leaves[1:], H, m, scale=scale, causal=causal, projection=projection,
+                           mask_diag=mask_diag, deterministic=deterministic)
+    out.backward(dout)
+    torch.cuda.synchronize()
+    return out.detach(), [t.grad for t in leaves]
+
+
+# (B, N, H, m, dv, causal, projection, mask_diag): the attn_bwd configurations
+# (4 waves / 128 keys at m = 16 and at m = 64 with dv = 128, 8 waves / 256 keys
+# at m = 32, 64 with dv <= 64), hi-only and hi/lo scores, steps with and without
+# flagged rows (the diagonal kept: only rows with most weight there carry a
+# row sum; masked: every row), ragged N and a single key block.
+DET_CASES = [
+    (2, 1000, 4, 16, 64, True, "sigmoid", False),
+    (2, 777, 4, 32, 64, False, "sigmoid", False),
+    (1, 600, 2, 64, 128, True, "sigmoid", True),
+    (2, 300, 2, 16, 32, False, "hardtanh01", True),
+    (3, 33, 2, 64, 32, True, "sigmoid", False),
+]
+
+
+@pytest.mark.parametrize("B,N,H,m,dv,causal,projection,mask_diag", DET_CASES,
+                         ids=[f"N{c[1]}-m{c[3]}-dv{c[4]}-{'causal' if c[5] else 'full'}-{c[6]}{'-md' if c[7] else ''}"
+                              for c in DET_CASES])
+def test_deterministic_backward_is_bitwise_reproducible(B, N, H, m, dv, causal, projection, mask_diag):
+    """MORPHO_MODE_DETERMINISTIC: three backward runs give the same bits; the
+    gradients meet the oracle bars, and differ from the atomic backward's only
+    by the order of the fp32 sums (<= 1e-3 of each tensor's largest entry)."""
+    from morphottention_amd.autograd import variant_bits
+    _say(f"[case] deterministic B={B} N={N} H={H} m={m} dv={dv} causal={causal} {projection} mask_diag={mask_diag}")
+    x, params, dout = make_inputs(B, N, H * dv, H, m, seed=720 + m + dv + N, x_mult=1.5)
+    runs = [_run_det(x, params, H, m, 0.8, causal, dout, projection, mask_diag, True) for _ in range(3)]
+    for out, grads in runs[1:]:
+        assert torch.equal(out, runs[0][0])
+        for n, g, g0 in zip(GRAD_NAMES, grads, runs[0][1]):
+            assert torch.equal(g, g0), f"{n}: deterministic backward differs between runs"
+    out, grads = runs[0]
+    _, atomic = _run_det(x, params, H, m, 0.8, causal, dout, projection, mask_diag, False)
+    for n, g, ga in zip(GRAD_NAMES, grads, atomic):
+        d = (g.float() - ga.float()).abs().max().item() / max(ga.float().abs().max().item(), 1e-30)
+        _say(f"[determinism] {n}: deterministic vs atomic {d:.2e} of max")
+        assert d <= 1e-3, f"{n}: deterministic and atomic backward differ by {d}"
+    _, lse, _ = torch.ops.morphottention.forward_train(x, *params, H, m, 0.8, causal,
+                                                       variant_bits(projection, mask_diag, True))
+    ref = mo.morpho_attention_ref_grads(x, *params, H, m, scale=0.8, causal=causal, dout=dout,
+                                        dtype=torch.float32, projection=projection, mask_diag=mask_diag)
+    check(f"deterministic N={N} m={m} dv={dv} causal={causal} {projection} mask_diag={mask_diag}", out, lse, grads,
+          *ref)
+
+
+def test_deterministic_c_abi_overwrites_every_partial():
+    """Through the C ABI with mode MORPHO_MODE_CAUSAL | MORPHO_MODE_DETERMINISTIC:
+    a workspace filled with 0x00 and one filled with 0xFF (NaN floats) give the
+    same bits, equal to the autograd path's, so every partial the reduction
+    reads was written by this call; the size query with the mode bits is what
+    the call requires."""
+    from morphottention_amd import capi
+    from morphottention_amd.autograd import variant_bits
+    L = capi.lib()
+    B, N, H, m, dv = 2, 333, 2, 16, 64
+    D = H * dv
+    mode = 1 | 32
+    x, params, dout = make_inputs(B, N, D, H, m, seed=820)
+    vp = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    out = torch.empty_like(x)
+    lse = torch.empty(B * H, N, dtype=torch.float32, device="cuda")
+    fbytes = capi.forward_workspace_size(B, N, D, H, m)
+    fws = torch.empty(fbytes, dtype=torch.uint8, device="cuda")
+    st = L.morpho_forward(*(vp(t) for t in (x, *params)), vp(out), vp(lse), B, N, D, H, m, 1.0, mode, vp(fws),
+                          fbytes, stream)
+    assert st == 0, L.morpho_last_error()
+    bbytes = capi.backward_workspace_size(B, N, D, H, m, True, mode)
+    assert bbytes > capi.backward_workspace_size(B, N, D, H, m, True)
+    results = []
+    for fill in (0x00, 0xFF):
+        bws = torch.full((bbytes,), fill, dtype=torch.uint8, device="cuda")
+        grads = [torch.empty_like(t) for t in (x, *params)]
+        st = L.morpho_backward(vp(dout), *(vp(t) for t in (x, *params)), vp(out), vp(lse), *(vp(g) for g in grads),
+                               B, N, D, H, m, 1.0, mode, vp(fws), vp(bws), bbytes, stream)
+        assert st == 0, L.morpho_last_error()
+        torch.cuda.synchronize()
+        assert all(torch.isfinite(g).all() for g in grads)
+        results.append(grads)
+    short = L.morpho_backward(vp(dout), *(vp(t) for t in (x, *params)), vp(out), vp(lse), *(vp(g) for g in results[0]),
+                              B, N, D, H, m, 1.0, mode, vp(fws), vp(bws), bbytes - 1, stream)
+    assert short == 3 and b"backward workspace" in L.morpho_last_error()
+    _, auto = _run_det(x, params, H, m, 1.0, True, dout, "sigmoid", False, True)
+    for n, a, b, c in zip(GRAD_NAMES, *results, auto):
+        assert torch.equal(a, b), f"{n}: stale workspace contents reached the result"
+        assert torch.equal(a, c), f"{n}: C ABI and autograd deterministic backward differ"
+    ref_out, ref_lse, ref_grads = oracle(x, params, H, m, 1.0, True, dout)
+    check("C ABI deterministic backward", out, lse, results[0], ref_out, ref_lse, ref_grads)
+    assert variant_bits(deterministic=True) == 32
+
+
 def test_c_abi_direct_matches_torch_op():
     from morphottention_amd import capi
     L = capi.lib()
