@@ -148,7 +148,10 @@ size_t bwd_bytes(const Dims& d) {
   s += align_up(bhn * 8);                              // dr
   s += align_up((size_t)d.T * (d.HM + d.D) * 2);       // dzv
   s += align_up(nblk * d.HM * 4);                      // gpart
-  s += align_up((size_t)dw_splits(d) * d.D * (d.HM + d.D) * 4);  // wpart
+  {
+    const BwdGemmPlan P = bwd_gemm_plan(d);
+    s += align_up((size_t)P.tiles_w * P.p * P.bt * P.bt * 4);  // wpart
+  }
   if (d.det) {
     const DetLayout l = attn_bwd_det_layout(d);
     const size_t prow = (size_t)l.nkb * d.B * d.H * l.nq;
@@ -170,8 +173,10 @@ BwdBuffers carve_bwd(void* base, const Dims& d) {
   g.dr = reinterpret_cast<float*>(p); p += align_up(bhn * 8);
   g.dzv = reinterpret_cast<_Float16*>(p); p += align_up((size_t)d.T * (d.HM + d.D) * 2);
   g.gpart = reinterpret_cast<float*>(p); p += align_up(nblk * d.HM * 4);
-  g.wpart = reinterpret_cast<float*>(p); p += align_up((size_t)dw_splits(d) * d.D * (d.HM + d.D) * 4);
-  g.splits = dw_splits(d);
+  {
+    const BwdGemmPlan P = bwd_gemm_plan(d);
+    g.wpart = reinterpret_cast<float*>(p); p += align_up((size_t)P.tiles_w * P.p * P.bt * P.bt * 4);
+  }
   g.dqpart = g.drpart = nullptr;
   if (d.det) {
     const DetLayout l = attn_bwd_det_layout(d);

@@ -90,8 +90,7 @@ struct BwdBuffers {
                    //             P_ii (0 when the diagonal is masked), written by bwd_prep
   _Float16* dzv;   // [T, H*M + D] dZ | dV
   float* gpart;    // [n_gate_blocks, H*M] partial sums of phi (2 dk - dcb), the gate factor dG
-  float* wpart;    // [splits, D, H*M + D] split-K partials of [dW_phi | dW_V]
-  int splits;
+  float* wpart;    // [tiles, pieces, bt, bt] fp32 partials of [dW_phi | dW_V] tiles (BwdGemmPlan)
   float* dqpart;   // deterministic mode only (else null): [nkb, B*H, NQ, M] per-key-block dq sums
   float* drpart;   //                                      [nkb, B*H, NQ] per-key-block row sums
 };
@@ -118,7 +117,25 @@ hipError_t launch_bwd_gemm(const Dims& d, const ProjBuffers& p, const BwdBuffers
                            hipStream_t s);
 hipError_t launch_dw_reduce(const Dims& d, const BwdBuffers& g, const _Float16* gate_q, const _Float16* gate_k,
                             _Float16* dW_phi, _Float16* dW_V, _Float16* d_gate_q, _Float16* d_gate_k, hipStream_t s);
-int dw_splits(const Dims& d);
+// Work decomposition of the backward GEMM launch: one round of kGemmSlots
+// workgroups (the CUs of an MI355X; twice as many with 128 x 128 tiles, two
+// per CU). Workgroups [0, n_a), n_a / 8 per XCD (workgroup id % 8), compute g
+// whole dX tiles each; the next tiles_w p each compute piece j < p of dW tile
+// t (workgroup n_a + p t + j): the tile's kw token k-steps split into p
+// near-equal ranges. g and p are chosen so that both kinds take about the
+// same number of k-steps. Piece j stores an fp32 tile partial that dw_reduce
+// adds in piece order, so the result does not depend on timing.
+constexpr int kGemmSlots = 256;
+struct BwdGemmPlan {
+  int bt;                   // tile edge: 256, or 128 when that finishes sooner (few tiles)
+  int n_dx, ntn_x, kx;      // dX tiles, dX column tiles, k-steps per dX tile
+  int tiles_w, ntn_w, kw;   // dW tiles, dW column tiles, k-steps per dW tile (all tokens)
+  int g, n_a;               // dX tiles per type-A workgroup, type-A workgroups
+  int p;                    // pieces per dW tile (tiles_w p type-B workgroups and partials)
+};
+BwdGemmPlan bwd_gemm_plan(const Dims& d);
+// token k-step where piece j of a dW tile's kw k-steps starts (j = p: the end)
+__host__ __device__ inline int dw_piece_k0(int kw, int p, int j) { return (int)((int64_t)kw * j / p); }
 
 // kernels_attn.hip
 hipError_t launch_attn_fwd(const Dims& d, const ProjBuffers& p, _Float16* out, float* lse, hipStream_t s);

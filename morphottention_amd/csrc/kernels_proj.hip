@@ -436,18 +436,18 @@ hipError_t launch_proj_bwd_elem(const Dims& d, const f16* gq, const f16* gk, con
 // ---------------------------------------------------------------- backward GEMMs
 // One launch computes
 //   dX = [dZ | dV] [W_phi | W_V]^T                    (dX tiles)
-//   [dW_phi | dW_V] = X^T [dZ | dV]                   (dW tiles, split-K over tokens)
-// Workgroup ids: [0, n_dw) dW, then [n_dw, n_dw + n_dx) dX; the dW tiles,
-// which run longer, are dispatched first. Split z of dW tile tl covers tokens
-// [z kchunk, (z + 1) kchunk), runs on XCD z % 8 (ids are dispatched
-// round-robin over the 8 XCDs, so the tiles of one split share their X and
-// dZ|dV panels in one L2) and stores an fp32 partial; dw_reduce sums the
-// partials in split order.
-// Square BT x BT tiles for both products: 256, or 128 when the 256 tiles (dX
-// tiles plus dW tiles times splits) would not fill one round of the 256 CUs
-// (few tokens: B8 N1024 D512 H8 m16 has 160 large workgroups, 576 small ones).
-// Either way the waves own 64-row wave tiles, which the dX epilogue's slabs
-// rely on.
+//   [dW_phi | dW_V] = X^T [dZ | dV]                   (dW tiles, split over tokens)
+// in one round of workgroups (BwdGemmPlan): ids [0, n_a) compute g whole dX
+// tiles each, ids n_a + p t + j piece j of dW tile t (a near-equal 1/p of the
+// tokens) and store its fp32 partial, which dw_reduce adds in piece order.
+// g and p give both kinds about the same number of k-steps. (Before, every
+// dW split of T / 8 tokens and every dX tile was a workgroup of its own; at
+// B4 N4096 D1024 H16 m16 a CU then ran a 32-k-step dW split or 20-k-step dX
+// tiles, and the launch took about 52 k-steps per CU for 40 of work: dX alone
+// 40.6 us, dW alone 53.4 us, both in one launch 90.1 us.)
+// Square BT x BT tiles for both products: 256, or 128 when the plan with
+// 128 tiles finishes sooner (few tokens). Either way the waves own 64-row wave
+// tiles, which the dX epilogue's slabs rely on.
 template <int BT>
 struct BwdTiles {
   static constexpr int WM = BT == 256 ? 4 : 2;
@@ -457,111 +457,145 @@ struct BwdTiles {
   static constexpr int kStageStride = BT + 8;  // halves: one 64-row slab of fp16 dX for 16-byte stores
   static_assert(64 * kStageStride * 2 <= kLds, "dX slab must fit the main loop's LDS");
   static_assert(Dx::WN == Dw::WN && Dx::WTM == 64 && Dw::WTM == 64, "shared wave grid, 64-row wave tiles");
+  static_assert(Dx::kBK == 64 && Dw::kBK == 64, "the plan counts k-steps of 64");
 };
-static int dw_tiles(const Dims& d, int bt) { return ((d.D + bt - 1) / bt) * ((d.HM + d.D + bt - 1) / bt); }
-// Splits of the token (k) range: a multiple of 8, so that every XCD gets the
-// same number of splits (split z runs on XCD z % 8), with at least as many
-// k-steps per dW split as a dX tile has (T / S >= H m + D tokens), and at
-// least 256 tokens per split. Fewer than 8 splits had left XCDs without dW
-// work (C5 bwd_gemm 2.04 -> 0.91 ms, C4 0.140 -> 0.107 ms); rounding T / (8 NC)
-// down rather than to nearest halves the partials where it is 1.5 - 2
-// (B4 N4096 D1024 H16 m16: 8 instead of 16 splits, bwd_gemm 0.108 -> 0.099 ms
-// and dw_reduce 17 -> 11 us).
-// Capped so that the dW workgroups need not exceed about 32 per XCD
-// (8 ceil(32 / tiles) splits): beyond that more splits add no parallelism, only
-// fp32 partials (splits x D x (H m + D) x 4 bytes) and reduce traffic, which
-// would otherwise grow with the token count (T = 1M at D = 1024 would need
-// about 800 splits and 4 GiB).
-int dw_splits(const Dims& d) {
-  const int NC = d.HM + d.D, by_k = (int)((d.T + 255) / 256);
-  const int64_t s8 = d.T / (8 * (int64_t)NC);  // floor(T / (8 NC))
-  const int tiles = dw_tiles(d, 256);
-  const int64_t cap = 8 * (int64_t)((32 + tiles - 1) / tiles);
-  const int64_t s = 8 * (s8 < 1 ? 1 : s8 > cap / 8 ? cap / 8 : s8);
-  const int r = (int)(s < by_k ? s : by_k);
-  return r < 1 ? 1 : r;
+
+// Plan for tile edge bt and `slots` workgroups: for each g (dX tiles per
+// type-A workgroup), the most pieces p per dW tile that still fit the round,
+// scored by the longer of the two kinds: g kx against ceil(kw / p) k-steps
+// (plus one step of epilogue per dX tile or piece). When the dW tiles alone
+// fill the round, every workgroup takes one tile over several rounds. A type-A workgroup's dX
+// tiles come from the row panels tr = 8 i + xcd, as before, so a panel of
+// dZ|dV is read into one L2.
+static BwdGemmPlan plan_for(const Dims& d, int bt, int slots, int64_t& cost) {
+  BwdGemmPlan P;
+  const int NC = d.HM + d.D, T = (int)d.T;
+  P.bt = bt;
+  const int ntm_x = (T + bt - 1) / bt;
+  P.ntn_x = (d.D + bt - 1) / bt;
+  P.n_dx = ntm_x * P.ntn_x;
+  P.kx = (NC + 63) / 64;
+  P.ntn_w = (NC + bt - 1) / bt;
+  P.tiles_w = ((d.D + bt - 1) / bt) * P.ntn_w;
+  P.kw = (T + 63) / 64;
+  const int per_xcd = ((ntm_x + 7) / 8) * P.ntn_x;  // dX tiles of one XCD
+  cost = INT64_MAX;
+  P.g = per_xcd;
+  P.n_a = 8;
+  P.p = 1;
+  for (int g = 1; g <= per_xcd; ++g) {
+    const int n_a = 8 * ((per_xcd + g - 1) / g);
+    const int pmax = (slots - n_a) / P.tiles_w;
+    if (pmax < 1) continue;
+    const int p = pmax < P.kw ? pmax : P.kw;
+    const int64_t ca = (int64_t)g * (P.kx + 1), cb = (P.kw + p - 1) / p + 1;
+    const int64_t cst = ca > cb ? ca : cb;
+    if (cst < cost) {
+      cost = cst;
+      P.g = g;
+      P.n_a = n_a;
+      P.p = p;
+    }
+    if (ca > cost) break;  // g kx only grows from here
+  }
+  if (cost == INT64_MAX) {
+    // dW tiles alone fill the round: one dX tile or one whole dW tile per
+    // workgroup over several rounds (the dispatcher balances them)
+    P.g = 1;
+    P.n_a = 8 * per_xcd;
+    P.p = 1;
+    cost = ((int64_t)P.n_dx * (P.kx + 1) + (int64_t)P.tiles_w * (P.kw + 1) + slots - 1) / slots;
+  }
+  return P;
 }
 
-static int bwd_gemm_tile(const Dims& d) {
-  const int S = dw_splits(d), T = (int)d.T;
-  const int large = 8 * dw_tiles(d, 256) * ((S + 7) / 8) + (int)gemm_tile_grid((T + 255) / 256, (d.D + 255) / 256);
-  return large < 256 && d.D % 128 == 0 && (d.HM + d.D) % 128 == 0 ? 128 : 256;
+BwdGemmPlan bwd_gemm_plan(const Dims& d) {
+  int64_t c256, c128;
+  const BwdGemmPlan p256 = plan_for(d, 256, kGemmSlots, c256);
+  if (d.D % 128 != 0 || (d.HM + d.D) % 128 != 0) return p256;
+  // 128 x 128 tiles: two workgroups per CU (64 KiB of LDS each), so twice the
+  // slots; a k-step does a quarter of the work of a 256 x 256 one at about 2/3
+  // of its rate (more LDS and L2 traffic per MFMA), and shares its CU
+  const BwdGemmPlan p128 = plan_for(d, 128, 2 * kGemmSlots, c128);
+  return 3 * c128 < 4 * c256 ? p128 : p256;
 }
 
 struct BwdGemmArgs {
   const f16* X;
   const f16* wcat;
   f16* dX;
-  int n_dw, n_dx, kchunk, dw_tiles;
+  BwdGemmPlan plan;
 };
 
 template <int BT>
 __global__ __launch_bounds__(kGemmThreads) void bwd_gemm_kernel(Dims d, BwdBuffers g, BwdGemmArgs a) {
   using DxGemm = typename BwdTiles<BT>::Dx;
   using DwGemm = typename BwdTiles<BT>::Dw;
-  constexpr int kDxBM = BT, kDxBN = BT, kDwBM = BT, kDwBN = BT;
   constexpr int kDxStageStride = BwdTiles<BT>::kStageStride;
   __shared__ __align__(16) char smem[BwdTiles<BT>::kLds];
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = w / DxGemm::WN, wn = w % DxGemm::WN;  // same wave grid for dX and dW
+  const BwdGemmPlan& P = a.plan;
   const int NC = d.HM + d.D;
   const int T = (int)d.T;
   const int id = blockIdx.x;
 
-  if (id >= a.n_dw) {
-    // ---- dX tile
-    int tm, tn;
-    if (!gemm_tile_map(id - a.n_dw, (T + kDxBM - 1) / kDxBM, (d.D + kDxBN - 1) / kDxBN, tm, tn)) return;
-    const int m0 = tm * kDxBM, n0 = tn * kDxBN;
-    f32x4 acc[DxGemm::FI][DxGemm::FJ];
-    DxGemm::run(g.dzv, NC, a.wcat, NC, T, d.D, m0, n0, 0, NC, smem, acc);
-    // fp16 through LDS in 64-row slabs (slab = wave row), then 16-byte row stores
-    f16* st = reinterpret_cast<f16*>(smem);
-    for (int slab = 0; slab < kDxBM / 64; ++slab) {
-      if (slab > 0) __syncthreads();
-      if (wm == slab) {
+  if (id < P.n_a) {
+    // ---- g dX tiles: local tiles s g .. s g + g - 1 of XCD xcd, i.e. row
+    // panel tr = 8 (L / ntn_x) + xcd, column tile L % ntn_x
+    const int xcd = id & 7, slot = id >> 3;
+    const int ntm = (T + BT - 1) / BT;
+    for (int q = 0; q < P.g; ++q) {
+      const int L = slot * P.g + q;
+      const int tm = 8 * (L / P.ntn_x) + xcd, tn = L % P.ntn_x;
+      if (tm >= ntm) break;  // uniform
+      if (q > 0) __syncthreads();  // the previous tile's slab reads are done before the stages refill
+      const int m0 = tm * BT, n0 = tn * BT;
+      f32x4 acc[DxGemm::FI][DxGemm::FJ];
+      DxGemm::run(g.dzv, NC, a.wcat, NC, T, d.D, m0, n0, 0, NC, smem, acc);
+      // fp16 through LDS in 64-row slabs (slab = wave row), then 16-byte row stores
+      f16* st = reinterpret_cast<f16*>(smem);
+      for (int slab = 0; slab < BT / 64; ++slab) {
+        if (slab > 0) __syncthreads();
+        if (wm == slab) {
 #pragma unroll
-        for (int i = 0; i < DxGemm::FI; ++i)
+          for (int i = 0; i < DxGemm::FI; ++i)
 #pragma unroll
-          for (int j = 0; j < DxGemm::FJ; ++j)
+            for (int j = 0; j < DxGemm::FJ; ++j)
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
-              st[(16 * i + 4 * (lane >> 4) + r) * kDxStageStride + DxGemm::WTN * wn + 16 * j + (lane & 15)] =
-                  (f16)acc[i][j][r];
-      }
-      __syncthreads();
-      for (int q = tid; q < 64 * (kDxBN / 8); q += kGemmThreads) {
-        const int r = q / (kDxBN / 8), c = 8 * (q % (kDxBN / 8));
-        const int row = m0 + 64 * slab + r, col = n0 + c;
-        if (row < T && col < d.D)
-          *reinterpret_cast<f16x8*>(a.dX + (int64_t)row * d.D + col) =
-              *reinterpret_cast<const f16x8*>(st + r * kDxStageStride + c);
+              for (int r = 0; r < 4; ++r)
+                st[(16 * i + 4 * (lane >> 4) + r) * kDxStageStride + DxGemm::WTN * wn + 16 * j + (lane & 15)] =
+                    (f16)acc[i][j][r];
+        }
+        __syncthreads();
+        for (int qq = tid; qq < 64 * (BT / 8); qq += kGemmThreads) {
+          const int r = qq / (BT / 8), c = 8 * (qq % (BT / 8));
+          const int row = m0 + 64 * slab + r, col = n0 + c;
+          if (row < T && col < d.D)
+            *reinterpret_cast<f16x8*>(a.dX + (int64_t)row * d.D + col) =
+                *reinterpret_cast<const f16x8*>(st + r * kDxStageStride + c);
+        }
       }
     }
     return;
   }
 
-  // ---- dW split-K tile
-  const int ntn = (NC + kDwBN - 1) / kDwBN, tiles = a.dw_tiles;
-  const int xcd = id & 7, slot = id >> 3;
-  const int tl = slot % tiles, z = xcd + 8 * (slot / tiles);
-  if (z >= g.splits) return;
-  const int m0 = (tl / ntn) * kDwBM, n0 = (tl % ntn) * kDwBN;
-  const int kbeg = min(z * a.kchunk, T), kend = min(kbeg + a.kchunk, T);
+  // ---- dW: piece j of tile tl
+  const int b = id - P.n_a, tl = b / P.p, j = b - tl * P.p;
+  if (tl >= P.tiles_w) return;
+  const int ks = dw_piece_k0(P.kw, P.p, j), ke = dw_piece_k0(P.kw, P.p, j + 1);
+  const int m0 = (tl / P.ntn_w) * BT, n0 = (tl % P.ntn_w) * BT;
   f32x4 acc[DwGemm::FI][DwGemm::FJ];
-  DwGemm::run(a.X, d.D, g.dzv, NC, d.D, NC, m0, n0, kbeg, kend, smem, acc);
-  const int64_t tot = (int64_t)d.D * NC;
-  float* part = g.wpart + (int64_t)z * tot;
+  DwGemm::run(a.X, d.D, g.dzv, NC, d.D, NC, m0, n0, 64 * ks, min(64 * ke, T), smem, acc);
+  // the piece's partial, tile-local row-major [BT][BT]
+  float* part = g.wpart + (int64_t)b * BT * BT;
 #pragma unroll
   for (int i = 0; i < DwGemm::FI; ++i)
 #pragma unroll
-    for (int j = 0; j < DwGemm::FJ; ++j) {
-      const int col = n0 + DwGemm::WTN * wn + 16 * j + (lane & 15);
+    for (int jj = 0; jj < DwGemm::FJ; ++jj) {
+      const int col = DwGemm::WTN * wn + 16 * jj + (lane & 15);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = m0 + DwGemm::WTM * wm + 16 * i + 4 * (lane >> 4) + r;
-        if (row < d.D && col < NC) part[(int64_t)row * NC + col] = acc[i][j][r];
-      }
+      for (int r = 0; r < 4; ++r) part[(DwGemm::WTM * wm + 16 * i + 4 * (lane >> 4) + r) * BT + col] = acc[i][jj][r];
     }
 }
 
@@ -569,28 +603,25 @@ hipError_t launch_bwd_gemm(const Dims& d, const ProjBuffers& p, const BwdBuffers
                            hipStream_t s) {
   BwdGemmArgs a;
   a.X = X; a.wcat = p.wcat; a.dX = dX;
-  const int S = g.splits, T = (int)d.T, bt = bwd_gemm_tile(d);
-  constexpr int kBK = BwdTiles<256>::Dw::kBK;
-  static_assert(BwdTiles<128>::Dw::kBK == kBK, "one k-step for both tile sizes");
-  a.kchunk = ((T + S - 1) / S + kBK - 1) / kBK * kBK;
-  a.dw_tiles = dw_tiles(d, bt);
-  a.n_dw = 8 * a.dw_tiles * ((S + 7) / 8);
-  a.n_dx = (int)gemm_tile_grid((T + bt - 1) / bt, (d.D + bt - 1) / bt);
-  if (bt == 128)
-    MORPHO_KLAUNCH(bwd_gemm_kernel<128>, dim3((unsigned)(a.n_dw + a.n_dx)), dim3(kGemmThreads), 0, s, d, g, a);
+  a.plan = bwd_gemm_plan(d);
+  const dim3 grid((unsigned)(a.plan.n_a + a.plan.tiles_w * a.plan.p));
+  if (a.plan.bt == 128)
+    MORPHO_KLAUNCH(bwd_gemm_kernel<128>, grid, dim3(kGemmThreads), 0, s, d, g, a);
   else
-    MORPHO_KLAUNCH(bwd_gemm_kernel<256>, dim3((unsigned)(a.n_dw + a.n_dx)), dim3(kGemmThreads), 0, s, d, g, a);
+    MORPHO_KLAUNCH(bwd_gemm_kernel<256>, grid, dim3(kGemmThreads), 0, s, d, g, a);
   return hipGetLastError();
 }
 
 // Finalisation of the weight and gate gradients, one launch. Blocks
-// [0, nw) sum the split-K partials of [dW_phi | dW_V] (4 consecutive outputs
-// per thread, splits in order); blocks [nw, nw + ceil(HM / 16)) sum the
-// per-block gate partials: 16 columns x 16 row groups per block, group g
-// summing rows g, g + 16, ... with two accumulators, the groups then combined
-// in a fixed order. Both orders are fixed, so results are deterministic.
-__global__ __launch_bounds__(256) void dw_reduce_kernel(const float* __restrict__ wpart, int splits, int D, int HM,
-                                                        f16* __restrict__ dW_phi, f16* __restrict__ dW_V, int nw,
+// [0, nw) sum the dW pieces' partials of [dW_phi | dW_V] (4 consecutive
+// outputs per thread; the pieces of the output's tile in order); blocks
+// [nw, nw + ceil(HM / 16)) sum the per-block gate partials: 16 columns x 16
+// row groups per block, group g summing rows g, g + 16, ... with two
+// accumulators, the groups then combined in a fixed order. Both orders are
+// fixed, so results are deterministic.
+__global__ __launch_bounds__(256) void dw_reduce_kernel(const float* __restrict__ wpart, int bt, int ntn_w, int pieces,
+                                                        int D, int HM, f16* __restrict__ dW_phi,
+                                                        f16* __restrict__ dW_V, int nw,
                                                         const float* __restrict__ gpart, int nblk, float scale,
                                                         const f16* __restrict__ gate_q, const f16* __restrict__ gate_k,
                                                         f16* __restrict__ d_gate_q, f16* __restrict__ d_gate_k) {
@@ -621,26 +652,29 @@ __global__ __launch_bounds__(256) void dw_reduce_kernel(const float* __restrict_
     return;
   }
   const int NC = HM + D;
-  const int64_t total = (int64_t)D * NC;
   const int64_t idx = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
-  if (idx >= total) return;
-  // splits summed in order; the loads of 8 splits are issued before their adds
-  float4 s = *reinterpret_cast<const float4*>(wpart + idx);
+  if (idx >= (int64_t)D * NC) return;
+  const int row = (int)(idx / NC), col = (int)(idx - (int64_t)row * NC);
+  const int tl = (row / bt) * ntn_w + col / bt;
+  // 4 columns never straddle a tile; piece z of the tile at partial tl pieces + z
+  const int64_t tsz = (int64_t)bt * bt;
+  const float* src = wpart + (int64_t)tl * pieces * tsz + (int64_t)(row % bt) * bt + col % bt;
+  // pieces summed in order; the loads of 8 are issued before their adds
+  float4 s = *reinterpret_cast<const float4*>(src);
   int z = 1;
-  for (; z + 8 <= splits; z += 8) {
+  for (; z + 8 <= pieces; z += 8) {
     float4 v[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = *reinterpret_cast<const float4*>(wpart + (int64_t)(z + i) * total + idx);
+    for (int i = 0; i < 8; ++i) v[i] = *reinterpret_cast<const float4*>(src + (z + i) * tsz);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       s.x += v[i].x; s.y += v[i].y; s.z += v[i].z; s.w += v[i].w;
     }
   }
-  for (; z < splits; ++z) {
-    const float4 v = *reinterpret_cast<const float4*>(wpart + (int64_t)z * total + idx);
+  for (; z < pieces; ++z) {
+    const float4 v = *reinterpret_cast<const float4*>(src + z * tsz);
     s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
   }
-  const int row = (int)(idx / NC), col = (int)(idx - (int64_t)row * NC);
   // 4 consecutive columns never straddle HM (HM and NC are multiples of 16)
   f16* dst = col < HM ? dW_phi + (int64_t)row * HM + col : dW_V + (int64_t)row * D + (col - HM);
   *reinterpret_cast<f16x4*>(dst) = f16x4{(f16)s.x, (f16)s.y, (f16)s.z, (f16)s.w};
@@ -652,8 +686,9 @@ hipError_t launch_dw_reduce(const Dims& d, const BwdBuffers& g, const f16* gq, c
   const int nw = (int)((total / 4 + 255) / 256);
   const int ngate = (d.HM + 15) / 16;
   const int nblk = (int)((d.T + kGateTokensPerBlock - 1) / kGateTokensPerBlock);
-  MORPHO_KLAUNCH(dw_reduce_kernel, dim3((unsigned)(nw + ngate)), dim3(256), 0, s, g.wpart, g.splits, d.D, d.HM,
-                     dW_phi, dW_V, nw, g.gpart, nblk, d.scale, gq, gk, dgq, dgk);
+  const BwdGemmPlan P = bwd_gemm_plan(d);
+  MORPHO_KLAUNCH(dw_reduce_kernel, dim3((unsigned)(nw + ngate)), dim3(256), 0, s, g.wpart, P.bt, P.ntn_w, P.p, d.D,
+                 d.HM, dW_phi, dW_V, nw, g.gpart, nblk, d.scale, gq, gk, dgq, dgk);
   return hipGetLastError();
 }
 
