@@ -69,11 +69,11 @@ def test_workspace_sizes():
 
 @pytest.mark.parametrize("D,H,m", [(1024, 16, 16), (2048, 32, 64)])
 def test_backward_workspace_grows_only_with_per_token_buffers(D, H, m):
-    """The split-K partials of the weight gradient (splits x D x (H m + D) fp32)
-    are capped: past a few hundred thousand tokens the backward workspace
-    grows only by its per-token buffers (dZ|dV rows, dq, dk, dcb, the row sums,
-    the dO affine rows and the per-block gate partials), not by partials whose
-    split count follows the token count."""
+    """The weight gradient's per-piece partials (dW tiles x pieces x bt x bt
+    fp32, at most one round of workgroups) do not grow with the token count:
+    the backward workspace grows only by its per-token buffers (dZ|dV rows,
+    dq, dk, dcb, the row sums, the dO affine rows and the per-block gate
+    partials)."""
     from morphottention_amd import capi
     N = 4096
     HM, NC = H * m, H * m + D
