@@ -120,9 +120,10 @@ hipError_t launch_dw_reduce(const Dims& d, const BwdBuffers& g, const _Float16* 
 // Work decomposition of the backward GEMM launch: one round of kGemmSlots
 // workgroups (the CUs of an MI355X; twice as many with 128 x 128 tiles, two
 // per CU). Workgroups [0, n_a), n_a / 8 per XCD (workgroup id % 8), compute g
-// whole dX tiles each; the next tiles_w p each compute piece j < p of dW tile
-// t (workgroup n_a + p t + j): the tile's kw token k-steps split into p
-// near-equal ranges. g and p are chosen so that both kinds take about the
+// whole dX tiles each; the next 8 ceil(tiles_w p / 8) each compute one piece
+// j < p of a dW tile t (the tile's kw token k-steps split into p near-equal
+// ranges; an XCD's workgroups take a contiguous run of the pieces in (j, t)
+// order, so they share token ranges). g and p are chosen so that both kinds take about the
 // same number of k-steps. Piece j stores an fp32 tile partial that dw_reduce
 // adds in piece order, so the result does not depend on timing.
 constexpr int kGemmSlots = 256;

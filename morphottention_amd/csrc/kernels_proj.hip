@@ -460,8 +460,9 @@ struct BwdTiles {
   static_assert(Dx::kBK == 64 && Dw::kBK == 64, "the plan counts k-steps of 64");
 };
 
-// Plan for tile edge bt and `slots` workgroups: for each g (dX tiles per
-// type-A workgroup), the most pieces p per dW tile that still fit the round,
+// Plan for tile edge bt and `slots` workgroups (the dW pieces take
+// 8 ceil(tiles_w p / 8) of them): for each g (dX tiles per type-A
+// workgroup), the most pieces p per dW tile that still fit the round,
 // scored by the longer of the two kinds: g kx against ceil(kw / p) k-steps
 // (plus one step of epilogue per dX tile or piece). When the dW tiles alone
 // fill the round, every workgroup takes one tile over several rounds. A type-A workgroup's dX
@@ -485,9 +486,10 @@ static BwdGemmPlan plan_for(const Dims& d, int bt, int slots, int64_t& cost) {
   P.p = 1;
   for (int g = 1; g <= per_xcd; ++g) {
     const int n_a = 8 * ((per_xcd + g - 1) / g);
-    const int pmax = (slots - n_a) / P.tiles_w;
-    if (pmax < 1) continue;
-    const int p = pmax < P.kw ? pmax : P.kw;
+    int p = (slots - n_a) / P.tiles_w;
+    while (p > 0 && n_a + 8 * ((P.tiles_w * p + 7) / 8) > slots) --p;  // whole runs of 8
+    if (p < 1) continue;
+    p = p < P.kw ? p : P.kw;
     const int64_t ca = (int64_t)g * (P.kx + 1), cb = (P.kw + p - 1) / p + 1;
     const int64_t cst = ca > cb ? ca : cb;
     if (cst < cost) {
@@ -580,15 +582,20 @@ __global__ __launch_bounds__(kGemmThreads) void bwd_gemm_kernel(Dims d, BwdBuffe
     return;
   }
 
-  // ---- dW: piece j of tile tl
-  const int b = id - P.n_a, tl = b / P.p, j = b - tl * P.p;
-  if (tl >= P.tiles_w) return;
+  // ---- dW: piece j of tile tl. The pieces, taken piece by piece (q = j
+  // tiles_w + tl), are dealt to the XCDs in contiguous runs (XCD x = id % 8
+  // takes q = x per_x + slot), so an XCD's workgroups share one or two token
+  // ranges of X and dZ|dV in its L2.
+  const int b = id - P.n_a, per_x = (P.tiles_w * P.p + 7) / 8;
+  const int q = (b & 7) * per_x + (b >> 3);
+  if ((b >> 3) >= per_x || q >= P.tiles_w * P.p) return;
+  const int j = q / P.tiles_w, tl = q - j * P.tiles_w;
   const int ks = dw_piece_k0(P.kw, P.p, j), ke = dw_piece_k0(P.kw, P.p, j + 1);
   const int m0 = (tl / P.ntn_w) * BT, n0 = (tl % P.ntn_w) * BT;
   f32x4 acc[DwGemm::FI][DwGemm::FJ];
   DwGemm::run(a.X, d.D, g.dzv, NC, d.D, NC, m0, n0, 64 * ks, min(64 * ke, T), smem, acc);
-  // the piece's partial, tile-local row-major [BT][BT]
-  float* part = g.wpart + (int64_t)b * BT * BT;
+  // the piece's partial, tile-local row-major [BT][BT], at tl p + j
+  float* part = g.wpart + (int64_t)(tl * P.p + j) * BT * BT;
 #pragma unroll
   for (int i = 0; i < DwGemm::FI; ++i)
 #pragma unroll
@@ -604,7 +611,7 @@ hipError_t launch_bwd_gemm(const Dims& d, const ProjBuffers& p, const BwdBuffers
   BwdGemmArgs a;
   a.X = X; a.wcat = p.wcat; a.dX = dX;
   a.plan = bwd_gemm_plan(d);
-  const dim3 grid((unsigned)(a.plan.n_a + a.plan.tiles_w * a.plan.p));
+  const dim3 grid((unsigned)(a.plan.n_a + 8 * ((a.plan.tiles_w * a.plan.p + 7) / 8)));
   if (a.plan.bt == 128)
     MORPHO_KLAUNCH(bwd_gemm_kernel<128>, grid, dim3(kGemmThreads), 0, s, d, g, a);
   else
