@@ -1337,9 +1337,24 @@ __global__ __launch_bounds__(256) void dq_det_reduce_kernel(const float* __restr
   const int nk = causal ? min(q / KW + 1, nkb) : nkb;
   const int64_t prow = (int64_t)bh * NQ + q, kstride = (int64_t)BH * NQ;
   const float4* src = reinterpret_cast<const float4*>(dqpart + prow * M) + c4;
+  const int64_t kv = kstride * V;  // float4 between consecutive key blocks
+  // key blocks added in order; the loads of 8 are issued before their adds
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int kb = 0; kb < nk; ++kb) {
-    const float4 v = src[kb * kstride * V];
+  int kb = 0;
+  for (; kb + 8 <= nk; kb += 8) {
+    float4 v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = src[(kb + i) * kv];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      acc.x += v[i].x;
+      acc.y += v[i].y;
+      acc.z += v[i].z;
+      acc.w += v[i].w;
+    }
+  }
+  for (; kb < nk; ++kb) {
+    const float4 v = src[kb * kv];
     acc.x += v.x;
     acc.y += v.y;
     acc.z += v.z;
@@ -1347,8 +1362,15 @@ __global__ __launch_bounds__(256) void dq_det_reduce_kernel(const float* __restr
   }
   reinterpret_cast<float4*>(dq + row * M)[c4] = acc;
   if (c4 == 0) {
-    float r = 0.f;
-    for (int kb = 0; kb < nk; ++kb) r += drpart[kb * kstride + prow];
+    float r = 0.f, u[8];
+    int k2 = 0;
+    for (; k2 + 8 <= nk; k2 += 8) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) u[i] = drpart[(k2 + i) * kstride + prow];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) r += u[i];
+    }
+    for (; k2 < nk; ++k2) r += drpart[k2 * kstride + prow];
     dr[2 * row] = r;
   }
 }
