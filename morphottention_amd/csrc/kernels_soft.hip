@@ -913,11 +913,16 @@ constexpr int soft_fast_bwd_waves() { return (M == 16 && DV <= 64) ? 2 : 1; }
 // the queries (fp16 hi/lo, [query][code], with a column of ones at code M).
 // The S block is loaded in swap23 query order so that E and ds are already
 // B operands of the products that contract over the queries: dV^T += G^T E,
-// and [dk | dcb]^T += [phi | 1]^T ds (three fp16 MFMAs of hi/lo pairs; the
-// ones column gives dcb). dq_i = sum_j ds_ij phi_j contracts over the keys:
-// each wave reads its ds block back from LDS as the A operand against phi of
-// its keys (registers), and the four waves' partials are summed in LDS before
-// one fp32 atomic per (query, code).
+// and [dk | dcb]^T += [phi_hi | 1]^T ds (one fp16 MFMA per 16 queries; the
+// ones column gives dcb). dq_i = sum_j ds_ij phi_hi_j contracts over the keys:
+// each wave reads its ds block back from LDS as the A operand against phi_hi
+// of its keys (registers), and the four waves' partials are summed in LDS
+// before one fp32 atomic per (query, code). The code-gradient products take
+// ds rounded once to fp16 and the fp16 hi codes, as the softmax backward does
+// (|ds_ij| <= sum_c |dO_ic|, well inside fp16's range): relative error ~2^-11
+// per term, against the 1e-2 bar. (Three MFMAs of hi/lo pairs each had been
+// used here; the products of G, E and F keep their bf16 hi/lo pairs, whose
+// range they need.)
 template <int M, int DV, bool MD>
 __global__ __launch_bounds__(256)
 __attribute__((amdgpu_waves_per_eu(soft_fast_bwd_waves<M, DV>(), soft_fast_bwd_waves<M, DV>()))) void soft_bwd_fast_kernel(
@@ -935,7 +940,6 @@ __attribute__((amdgpu_waves_per_eu(soft_fast_bwd_waves<M, DV>(), soft_fast_bwd_w
   __shared__ __align__(16) bf16 sgh[QT * GS];
   __shared__ __align__(16) bf16 sgl[QT * GS];
   __shared__ __align__(16) f16 sph[QT * PT];
-  __shared__ __align__(16) f16 spl[QT * PT];
   __shared__ __align__(16) float sds[QT * DS];
   __shared__ __align__(16) float sdq[4][QT * 32 * NB];
   __shared__ float sar[QT];
@@ -981,7 +985,7 @@ __attribute__((amdgpu_waves_per_eu(soft_fast_bwd_waves<M, DV>(), soft_fast_bwd_w
       fh[cc][j] = hi;
       fl[cc][j] = lo;
     }
-  f16x8 pkh[NB][2], pkl[NB][2];
+  f16x8 pkh[NB][2];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
@@ -989,13 +993,7 @@ __attribute__((amdgpu_waves_per_eu(soft_fast_bwd_waves<M, DV>(), soft_fast_bwd_w
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int kk = kw0 + 16 * kc + 8 * h32 + j, code = 32 * nb + l32;
-        f16 hi = (f16)0.f, lo = (f16)0.f;
-        if (kk < N && code < M) {
-          hi = qa[(rowbase + kk) * CW + code];
-          lo = qa[(rowbase + kk) * CW + M + 8 + code];
-        }
-        pkh[nb][kc][j] = hi;
-        pkl[nb][kc][j] = lo;
+        pkh[nb][kc][j] = (kk < N && code < M) ? qa[(rowbase + kk) * CW + code] : (f16)0.f;
       }
   if (kvalid) load_key_operand<M>(ka + (rowbase + key) * CW, h32, kf, kaug);
   f32x16 dva[CB], dka[MB];
@@ -1015,7 +1013,7 @@ __attribute__((amdgpu_waves_per_eu(soft_fast_bwd_waves<M, DV>(), soft_fast_bwd_w
     constexpr int GP = QT * DV / 8, GPT = (GP + 255) / 256;  // G pieces, per thread
     constexpr int PP = QT * 4 * MB, PPT = (PP + 255) / 256;  // [phi | 1] pieces, per thread
     bf16x8 gvh[GPT], gvl[GPT];
-    f16x8 pvh[PPT], pvl[PPT];
+    f16x8 pvh[PPT];
 #pragma unroll
     for (int i = 0; i < GPT; ++i) {
       const int e = tid + 256 * i, r = e / (DV / 8), c8 = 8 * (e % (DV / 8)), qq = qs + r;
@@ -1030,11 +1028,9 @@ __attribute__((amdgpu_waves_per_eu(soft_fast_bwd_waves<M, DV>(), soft_fast_bwd_w
     for (int i = 0; i < PPT; ++i) {
       const int e = tid + 256 * i, r = e / (4 * MB), c8 = 8 * (e % (4 * MB)), qq = qs + r;
       pvh[i] = f16x8{};
-      pvl[i] = f16x8{};
       if (e < PP && qq < N) {
         if (c8 < M) {
           pvh[i] = *reinterpret_cast<const f16x8*>(qa + (rowbase + qq) * CW + c8);
-          pvl[i] = *reinterpret_cast<const f16x8*>(qa + (rowbase + qq) * CW + M + 8 + c8);
         } else if (c8 == M) {
           pvh[i][0] = (f16)1.f;
         }
@@ -1052,10 +1048,7 @@ __attribute__((amdgpu_waves_per_eu(soft_fast_bwd_waves<M, DV>(), soft_fast_bwd_w
 #pragma unroll
     for (int i = 0; i < PPT; ++i) {
       const int e = tid + 256 * i, r = e / (4 * MB), c8 = 8 * (e % (4 * MB));
-      if (e < PP) {
-        *reinterpret_cast<f16x8*>(sph + r * PT + c8) = pvh[i];
-        *reinterpret_cast<f16x8*>(spl + r * PT + c8) = pvl[i];
-      }
+      if (e < PP) *reinterpret_cast<f16x8*>(sph + r * PT + c8) = pvh[i];
     }
     if (tid < QT) sar[tid] = arow > kNegInf ? arow : 0.f;  // rows without keys: every score is masked
     // ---- S block, query rows in swap23 order: register r holds query p(r)
@@ -1120,29 +1113,20 @@ __attribute__((amdgpu_waves_per_eu(soft_fast_bwd_waves<M, DV>(), soft_fast_bwd_w
         dva[cb] = mfma_bf16(ah, el[kc], dva[cb]);
         dva[cb] = mfma_bf16(al, eh[kc], dva[cb]);
       }
-    // ---- ds = E X (fp16 hi/lo, the B operand of [phi | 1]^T ds); the ds tile for dq
-    f16x8 dsh[2], dsl[2];
+    // ---- ds = E X (fp16, the B operand of [phi_hi | 1]^T ds); the ds tile for dq
+    f16x8 dsh[2];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int p = r < 8 ? 8 * h32 + r : 8 + 8 * h32 + r;
       const float dsv = e32[r] * x[r];
       sacc = fmaf(dsv, acc[r], sacc);
       sds[p * DS + 32 * w + l32] = dsv;
-      f16 hi, lo;
-      split_hi_lo(dsv, hi, lo);
-      dsh[r >> 3][r & 7] = hi;
-      dsl[r >> 3][r & 7] = lo;
+      dsh[r >> 3][r & 7] = (f16)dsv;
     }
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-      for (int kc = 0; kc < 2; ++kc) {
-        const f16x8 ah = frag_kmajor(sph, PT, 16 * kc, 32 * mb, lane);
-        const f16x8 al = frag_kmajor(spl, PT, 16 * kc, 32 * mb, lane);
-        dka[mb] = mfma16(ah, dsh[kc], dka[mb]);
-        dka[mb] = mfma16(ah, dsl[kc], dka[mb]);
-        dka[mb] = mfma16(al, dsh[kc], dka[mb]);
-      }
+      for (int kc = 0; kc < 2; ++kc) dka[mb] = mfma16(frag_kmajor(sph, PT, 16 * kc, 32 * mb, lane), dsh[kc], dka[mb]);
     __syncthreads();  // the ds tile is complete
     // ---- dq partial of this wave's keys: ds (rows = queries, k = keys) phi_k
 #pragma unroll
@@ -1153,18 +1137,8 @@ __attribute__((amdgpu_waves_per_eu(soft_fast_bwd_waves<M, DV>(), soft_fast_bwd_w
         const float* src = sds + l32 * DS + 32 * w + 16 * kc + 8 * h32;
         const float4 v0 = *reinterpret_cast<const float4*>(src);
         const float4 v1 = *reinterpret_cast<const float4*>(src + 4);
-        const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-        f16x8 ah, al;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          f16 hi, lo;
-          split_hi_lo(vv[j], hi, lo);
-          ah[j] = hi;
-          al[j] = lo;
-        }
+        const f16x8 ah = {(f16)v0.x, (f16)v0.y, (f16)v0.z, (f16)v0.w, (f16)v1.x, (f16)v1.y, (f16)v1.z, (f16)v1.w};
         dqa = mfma16(ah, pkh[nb][kc], dqa);
-        dqa = mfma16(ah, pkl[nb][kc], dqa);
-        dqa = mfma16(al, pkh[nb][kc], dqa);
       }
       // rows = queries, lane = code 32 nb + l32
 #pragma unroll
