@@ -41,7 +41,7 @@ def _rel(a, b):
     return ((a.float() - b.float()).abs().max() / b.float().abs().max().clamp_min(1e-30)).item()
 
 
-def _capture_and_replay(step, n_replays=3):
+def _capture_and_replay(step, n_replays=3, bitwise=False):
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
@@ -62,6 +62,8 @@ def _capture_and_replay(step, n_replays=3):
         assert torch.equal(static[0], eager[0]), f"replay {i}: forward output differs from eager"
         rels = [_rel(s, e) for s, e in zip(static, eager)]
         print(f"[graph] replay {i}: max rel diff {max(rels):.2e}", flush=True)
+        if bitwise:
+            assert all(torch.equal(s, e) for s, e in zip(static, eager)), f"replay {i}: gradients differ from eager"
         worst = max(worst, max(rels))
         other = [t.detach().clone() for t in step()]  # eager work between the replays
         torch.cuda.synchronize()
@@ -81,6 +83,25 @@ def test_softmax_step_replays(causal):
         return [out, *torch.autograd.grad(out, leaves, dout)]
 
     assert _capture_and_replay(step) <= 2e-3
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_deterministic_step_replays_bitwise(causal):
+    """MORPHO_MODE_DETERMINISTIC under capture: its partial-sum buffers are
+    written by kernels (no memset), and every replay's gradients equal the
+    eager step's bit for bit."""
+    from morphottention_amd import MorphoAttentionFunction
+    from morphottention_amd.autograd import variant_bits
+    B, N, H, m, dv = 2, 300, 2, 16, 64
+    x, params, dout = _inputs(B, N, H, m, dv, seed=22)
+    leaves = [x, *params]
+    variant = variant_bits(deterministic=True)
+
+    def step():
+        out = MorphoAttentionFunction.apply(x, *params, H, m, 0.8, causal, variant)
+        return [out, *torch.autograd.grad(out, leaves, dout)]
+
+    assert _capture_and_replay(step, bitwise=True) == 0.0
 
 
 def test_soft_step_replays():
