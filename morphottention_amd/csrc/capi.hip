@@ -91,13 +91,26 @@ int make_dims(int64_t B, int64_t N, int64_t D, int64_t H, int64_t M, float scale
            : causal & MORPHO_MODE_PROJ_IDENTITY ? kProjIdentity
                                                 : kProjSigmoid;
   d.det = causal & MORPHO_MODE_DETERMINISTIC ? 1 : 0;
-  // projection tiles: 256 x 320 when 320 divides H*M + D, else 256 x 256, and
-  // 128 x 128 when the large tiles would fill less than one round of the 256
-  // CUs and 128 divides H*M + D; the interleaved column order needs whole
-  // heads and 8-column pieces per tile
+  // projection tiles: 256 x 320 when 320 divides H*M + D, else 256 x 256.
+  // When those would fill less than one round of the 256 CUs, 128-row tiles
+  // of 160 or 128 columns (whichever divides H*M + D and needs fewer rounds
+  // times tile area; 160 on a tie): e.g. H*M + D = 640, T = 8192 gives 256
+  // workgroups of 128 x 160 (one round) instead of 320 of 128 x 128. The
+  // interleaved column order needs whole heads and 8-column pieces per tile.
   const int NC = d.HM + d.D;
   d.PBN = NC % 320 == 0 ? 320 : 256;
-  if (((T + 255) / 256) * ((NC + d.PBN - 1) / d.PBN) < 256 && NC % 128 == 0) d.PBN = 128;
+  if (((T + 255) / 256) * ((NC + d.PBN - 1) / d.PBN) < 256) {
+    const int64_t rows = (T + 127) / 128;
+    int64_t best = -1;
+    for (const int bn : {160, 128}) {
+      if (NC % bn) continue;
+      const int64_t cost = (rows * (NC / bn) + 255) / 256 * bn;
+      if (best < 0 || cost < best) {
+        best = cost;
+        d.PBN = bn;
+      }
+    }
+  }
   d.PCPT = d.PVPT = 0;
   if (NC % d.PBN == 0) {
     const int ntn = NC / d.PBN;

@@ -316,6 +316,8 @@ static hipError_t launch_proj_fwd_t(const Dims& d, const f16* X, const f16* gq, 
   } while (0)
   if (d.PBN == 320)
     MORPHO_PROJ_LAUNCH(256, 320);
+  else if (d.PBN == 160)
+    MORPHO_PROJ_LAUNCH(128, 160);
   else if (d.PBN == 128)
     MORPHO_PROJ_LAUNCH(128, 128);
   else
