@@ -241,6 +241,23 @@ def test_eight_wave_backward_key_blocks(m, dv, causal):
           *oracle(x, params, H, m, 0.8, causal, dout))
 
 
+@pytest.mark.parametrize("B,N,D,H,causal", [(7, 1000, 512, 8, False), (7, 1000, 512, 8, True), (3, 300, 256, 4, True)],
+                         ids=["T7000-full", "T7000-causal", "320cols-causal"])
+def test_projection_tile_128x160(B, N, D, H, causal):
+    """Projection tiles of 128 x 160. They are chosen when the 256-row tiles
+    fill less than one round of the CUs and 160-column tiles need fewer rounds
+    than 128-column ones: T = 7000 with H*M + D = 640 gives 55 row tiles x 4
+    (one round) instead of x 5, the last row tile ragged (88 rows). Or when 160
+    divides H*M + D and 128 does not: 320 columns, two tiles of 32 code and 128
+    value columns each."""
+    m = 16
+    _say(f"[case] projection 128x160 B={B} N={N} D={D} H={H} causal={causal}")
+    x, params, dout = make_inputs(B, N, D, H, m, seed=700 + N + D, gates=(1.0, 0.4))
+    out, lse, grads = run_hip(x, params, H, m, 0.8, causal, dout)
+    check(f"proj128x160 B{B} N{N} D{D} H{H} {'causal' if causal else 'full'}", out, lse, grads,
+          *oracle(x, params, H, m, 0.8, causal, dout))
+
+
 @pytest.mark.parametrize("N", [1, 2, 31, 33, 127, 129, 257])
 def test_ragged_lengths(N):
     B, H, m, dv = 3, 4, 16, 64
