@@ -91,7 +91,11 @@ const char* morpho_last_error(void);
 
 /* Bytes of device workspace morpho_forward needs (0 on invalid sizes).
  * The forward workspace holds the projected codes and values; passing it
- * unchanged to morpho_backward lets the backward skip recomputing them. */
+ * unchanged to morpho_backward lets the backward skip recomputing them.
+ * Sizes every entry point accepts: cube_m in {16, 32, 64}, D / H in {32, 64,
+ * 128}, B*N <= 2^28, B*N*D <= 2^34, B*N*H*cube_m <= 2^33, D and H*cube_m
+ * <= 65536 (every kernel grid then stays below 2^31 work-items); larger
+ * problems fail with MORPHO_ERR_INVALID_ARGUMENT. */
 size_t morpho_forward_workspace_size(int64_t B, int64_t N, int64_t D, int64_t H, int64_t cube_m);
 
 /* Forward. Replaces attention_forward_kernel_launcher (attention.cuh:28-31) and

@@ -67,9 +67,19 @@ int make_dims(int64_t B, int64_t N, int64_t D, int64_t H, int64_t M, float scale
     return fail(MORPHO_ERR_UNSUPPORTED, "cube_m must be 16, 32 or 64 (got %lld)", (long long)M);
   if (DV != 32 && DV != 64 && DV != 128)
     return fail(MORPHO_ERR_UNSUPPORTED, "head_dim_v = D / H must be 32, 64 or 128 (got %lld)", (long long)DV);
+  // Every launch's grid must stay below 2^32 work-items (the dispatch
+  // packet's 32-bit grid size): the element-wise kernels run one thread per
+  // 8 (token, feature) elements (T D / 8), the backward's gate kernel 16 per
+  // token, the deterministic dq reduction one per 4 (token, head, code)
+  // values; the bounds below keep each under 2^31. They sit near what fits in
+  // memory anyway (T D = 2^34 is a 32 GiB fp16 input).
+  if (B > ((int64_t)1 << 28) || N > ((int64_t)1 << 28))
+    return fail(MORPHO_ERR_INVALID_ARGUMENT, "problem too large: B * N must be at most 2^28 tokens");
   const int64_t T = B * N;
-  if (T > (int64_t)1 << 30 || D > 65536 || H * M > 65536)
-    return fail(MORPHO_ERR_INVALID_ARGUMENT, "problem too large for 32-bit token indexing");
+  if (T > ((int64_t)1 << 28) || D > 65536 || H * M > 65536 || T * D > ((int64_t)1 << 34) ||
+      T * H * M > ((int64_t)1 << 33))
+    return fail(MORPHO_ERR_INVALID_ARGUMENT,
+                "problem too large: needs B*N <= 2^28, B*N*D <= 2^34, B*N*H*cube_m <= 2^33, D and H*cube_m <= 65536");
   if (!__builtin_isfinite(scale)) return fail(MORPHO_ERR_INVALID_ARGUMENT, "scale must be a finite number");
   if ((causal & ~(15 | MORPHO_MODE_DETERMINISTIC)) != 0 || (causal & 12) == 12)
     return fail(MORPHO_ERR_INVALID_ARGUMENT,

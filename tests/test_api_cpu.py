@@ -65,6 +65,13 @@ def test_workspace_sizes():
     assert capi.forward_workspace_size(4, 4096, 1024, 16, 24) == 0      # unsupported cube_m
     assert capi.forward_workspace_size(4, 4096, 1000, 16, 16) == 0      # D % H != 0
     assert capi.forward_workspace_size(4, 4096, 256, 16, 16) == 0       # head_dim_v 16 unsupported
+    # launch grids stay below 2^32 work-items: tokens <= 2^28, tokens x D <= 2^34,
+    # tokens x H x cube_m <= 2^33 (each at its limit is accepted, one more token is not)
+    assert capi.forward_workspace_size(1, 1 << 24, 1024, 16, 32) > 0    # T D = 2^34, T H m = 2^33
+    assert capi.forward_workspace_size(1, (1 << 24) + 1, 1024, 16, 32) == 0
+    assert capi.forward_workspace_size(1 << 14, 1 << 14, 64, 1, 16) > 0  # T = 2^28
+    assert capi.forward_workspace_size((1 << 14) + 1, 1 << 14, 64, 1, 16) == 0
+    assert capi.forward_workspace_size(1 << 40, 1 << 40, 64, 1, 16) == 0  # no int64 overflow in T
 
 
 @pytest.mark.parametrize("D,H,m", [(1024, 16, 16), (2048, 32, 64)])
