@@ -215,6 +215,22 @@ __device__ __forceinline__ f32x16 code_dot_hi(const f16x8 (&kf)[M / 8], const f1
   return acc;
 }
 
+// Chunk swizzle of a dS^T tile (rows of RB = 128 or 64 bytes: one key's dS
+// over a 64- or 32-query step). It is written with ds_write_b128, which
+// serves 8 consecutive lanes per cycle within a 128-byte bank window (a
+// probe under rocprofv3: an XOR pattern conflict-free for b128 reads cost 16
+// LDS cycles per write, 8 of them conflicts), and read with the transposing
+// 16x16x32 pattern (ds_read_b64_tr_b16 of rows {r..r+3, r+8..r+11} x 2
+// chunks). Each aligned group of 8 rows takes 8 (RB = 128) or, per row
+// parity, 4 (RB = 64) distinct chunks, and rows r and r + 8 differ in the
+// chunk pair the transposing read touches.
+template <int RB>
+__device__ __forceinline__ int sswz(int r) {
+  static_assert(RB == 64 || RB == 128, "dS^T row bytes");
+  if constexpr (RB == 128) return (r & 7) ^ (((r >> 3) & 1) << 2);
+  else return ((r >> 1) & 3) ^ (((r >> 3) & 1) << 1);
+}
+
 // Workgroups are dispatched round-robin over the 8 XCDs (id % 8), each with
 // its own L2. Map a 1-D grid of 8 * ceil(BH / 8) * nblk workgroups so that all
 // blocks of one (batch, head) run on the same XCD and share its L2: XCD x

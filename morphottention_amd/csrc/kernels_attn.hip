@@ -628,20 +628,6 @@ __device__ __forceinline__ int rswz(int r) {
   else if constexpr (RB == 128) return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
   else return ((r & 3) << 2) | ((r >> 2) & 3);
 }
-// Chunk swizzle of the dS^T tile (rows of RB = 128 or 64 bytes: one key's dS
-// over a 64- or 32-query step). It is written with ds_write_b128, which
-// serves 8 consecutive lanes per cycle within a 128-byte bank window (a
-// probe under rocprofv3: rswz's pattern, conflict-free for b128 reads, cost
-// 16 LDS cycles per write, 8 of them conflicts), and read with the
-// transposing 16x16x32 pattern of rswz's case (b). Each aligned group of 8
-// rows takes 8 (RB = 128) or, per row parity, 4 (RB = 64) distinct chunks,
-// and rows r and r + 8 differ in the chunk pair the transposing read touches.
-template <int RB>
-__device__ __forceinline__ int sswz(int r) {
-  static_assert(RB == 64 || RB == 128, "dS^T row bytes");
-  if constexpr (RB == 128) return (r & 7) ^ (((r >> 3) & 1) << 2);
-  else return ((r >> 1) & 3) ^ (((r >> 3) & 1) << 1);
-}
 __host__ __device__ constexpr int pow2_bytes(int x) { return x <= 64 ? 64 : 2 * pow2_bytes((x + 1) / 2); }
 // stored row of logical row r in a tile whose rows are in swap23 order within each 32
 __device__ __forceinline__ int srow23(int r) { return (r & ~31) | swap23(r & 31); }

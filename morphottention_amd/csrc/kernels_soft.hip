@@ -588,11 +588,14 @@ __global__ __launch_bounds__(256) void soft_bwd_prep_kernel(const f16* __restric
     if (gh) {  // G = dO 2^(A_i + B_c - zb) for the product-form backward (0 for a row without keys)
       const float kw = sgn * kLog2e / *tau_p;
       const float a = arow[bhn];
+      // the 8 columns' extremes (max for dilation, min for erosion) in two 16-byte loads
+      const float* ext = (kw > 0.f ? vmax : vmin) + bh * DV + c;
+      const float4 x0 = *reinterpret_cast<const float4*>(ext), x1 = *reinterpret_cast<const float4*>(ext + 4);
+      const float xc[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
       bf16x8 hi, lo;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int64_t col = bh * DV + c + e;
-        const float bc = kw * (kw > 0.f ? vmax[col] : vmin[col]);
+        const float bc = kw * xc[e];
         const float gv = (live && a > kNegInf) ? (float)g[e] * fast_exp2(a + bc - z[e]) : 0.f;
         bf16 h, l;
         split_bf16(gv, h, l);
@@ -915,9 +918,12 @@ constexpr int soft_fast_bwd_waves() { return (M == 16 && DV <= 64) ? 2 : 1; }
 // B operands of the products that contract over the queries: dV^T += G^T E,
 // and [dk | dcb]^T += [phi_hi | 1]^T ds (one fp16 MFMA per 16 queries; the
 // ones column gives dcb). dq_i = sum_j ds_ij phi_hi_j contracts over the keys:
-// each wave reads its ds block back from LDS as the A operand against phi_hi
-// of its keys (registers), and the four waves' partials are summed in LDS
-// before one fp32 atomic per (query, code). The code-gradient products take
+// every lane stores its key's fp16 ds row (the step's 32 queries) into a
+// dS^T tile, and the step's 16 x 16 (query, code) dq tiles, split over the
+// waves, each contract over all 128 keys of the workgroup: the A operand is
+// read from the tile with transposing reads, phi_hi of the workgroup's keys
+// is the B operand (registers), and each result element is one fp32 atomic
+// per (query, code). The code-gradient products take
 // ds rounded once to fp16 and the fp16 hi codes, as the softmax backward does
 // (|ds_ij| <= sum_c |dO_ic|, well inside fp16's range): relative error ~2^-11
 // per term, against the 1e-2 bar. (Three MFMAs of hi/lo pairs each had been
@@ -935,13 +941,14 @@ __attribute__((amdgpu_waves_per_eu(soft_fast_bwd_waves<M, DV>(), soft_fast_bwd_w
   constexpr int GS = DV + 8;            // bf16 row stride of the G tiles
   constexpr int MB = (M + 32) / 32;     // 32-code blocks of [phi | 1]
   constexpr int PT = 32 * MB + 8;       // fp16 row stride of the [phi | 1] tiles
-  constexpr int NB = (M + 31) / 32;     // 32-code blocks of dq
-  constexpr int DS = KW + 4;            // fp32 row stride of the ds tile
+  constexpr int SRB = 2 * QT;           // dS^T row bytes (one key's ds over the step's queries)
+  constexpr int DQTILES = (QT / 16) * (M / 16);  // 16 x 16 dq tiles of a step
+  constexpr int DQT = DQTILES >= 4 ? DQTILES / 4 : 1;  // per wave (m = 16: waves 0, 1 only)
+  static_assert(DQTILES < 4 || DQTILES % 4 == 0, "dq tiles must split evenly over the waves");
   __shared__ __align__(16) bf16 sgh[QT * GS];
   __shared__ __align__(16) bf16 sgl[QT * GS];
   __shared__ __align__(16) f16 sph[QT * PT];
-  __shared__ __align__(16) float sds[QT * DS];
-  __shared__ __align__(16) float sdq[4][QT * 32 * NB];
+  __shared__ __align__(16) char sdt[KW * SRB];  // dS^T of the step: row = key, chunks swizzled by sswz
   __shared__ float sar[QT];
   __shared__ float sbc[DV];
   __shared__ float red[2][4];
@@ -985,16 +992,31 @@ __attribute__((amdgpu_waves_per_eu(soft_fast_bwd_waves<M, DV>(), soft_fast_bwd_w
       fh[cc][j] = hi;
       fl[cc][j] = lo;
     }
-  f16x8 pkh[NB][2];
+  // dq tiles of this wave: tile w + 4 t = (query block qt, code block ct).
+  // phi_hi of the workgroup's keys as their B operand (chunk kc: keys
+  // k0 + 32 kc + 8 (lane / 16) + 0..7, code 16 ct + lane % 16; zero past N),
+  // and the lane offsets of the transposing A-operand reads of the dS^T tile
+  // (16 x 16 x 32 layout: query 16 qt + lane % 16, keys 8 (lane / 16) + j).
+  const bool dq_wave = w < DQTILES;  // uniform
+  f16x8 phib[DQT][KW / 32];
+  int d_s[DQT][2];
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb)
+  for (int t = 0; t < DQT; ++t) {
+    const int tile = w + 4 * t, qt = tile % (QT / 16), ct = tile / (QT / 16);
 #pragma unroll
-    for (int kc = 0; kc < 2; ++kc)
+    for (int kc = 0; kc < KW / 32; ++kc)
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const int kk = kw0 + 16 * kc + 8 * h32 + j, code = 32 * nb + l32;
-        pkh[nb][kc][j] = (kk < N && code < M) ? qa[(rowbase + kk) * CW + code] : (f16)0.f;
+        const int kk = k0 + 32 * kc + 8 * (lane >> 4) + j;
+        phib[t][kc][j] = (dq_wave && kk < N) ? qa[(rowbase + kk) * CW + 16 * ct + (lane & 15)] : (f16)0.f;
       }
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const int row = 8 * (lane >> 4) + ((lane & 15) >> 2) + 4 * hh, col = 16 * qt + 4 * (lane & 3);
+      d_s[t][hh] = row * SRB + 16 * ((col >> 3) ^ sswz<SRB>(row)) + 2 * (col & 7);
+    }
+  }
+  const int kr = 32 * w + l32, sz = sswz<SRB>(kr);  // this lane's dS^T row (its key)
   if (kvalid) load_key_operand<M>(ka + (rowbase + key) * CW, h32, kf, kaug);
   f32x16 dva[CB], dka[MB];
 #pragma unroll
@@ -1120,36 +1142,38 @@ __attribute__((amdgpu_waves_per_eu(soft_fast_bwd_waves<M, DV>(), soft_fast_bwd_w
       const int p = r < 8 ? 8 * h32 + r : 8 + 8 * h32 + r;
       const float dsv = e32[r] * x[r];
       sacc = fmaf(dsv, acc[r], sacc);
-      sds[p * DS + 32 * w + l32] = dsv;
       dsh[r >> 3][r & 7] = (f16)dsv;
     }
+    // dS^T row of this key: queries 8 h32 + 0..7 and 16 + 8 h32 + 0..7 are
+    // logical chunks h32 and 2 + h32
+#pragma unroll
+    for (int c = 0; c < 2; ++c) *reinterpret_cast<f16x8*>(sdt + kr * SRB + 16 * ((2 * c + h32) ^ sz)) = dsh[c];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
       for (int kc = 0; kc < 2; ++kc) dka[mb] = mfma16(frag_kmajor(sph, PT, 16 * kc, 32 * mb, lane), dsh[kc], dka[mb]);
-    __syncthreads();  // the ds tile is complete
-    // ---- dq partial of this wave's keys: ds (rows = queries, k = keys) phi_k
+    __syncthreads();  // the dS^T tile is complete
+    // ---- dq of the step's queries over the workgroup's keys
+    if (dq_wave) {
+      typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      f32x16 dqa = {};
+      for (int t = 0; t < DQT; ++t) {
+        const int tile = w + 4 * t, qt = tile % (QT / 16), ct = tile / (QT / 16);
+        f32x4 a = {};
 #pragma unroll
-      for (int kc = 0; kc < 2; ++kc) {
-        const float* src = sds + l32 * DS + 32 * w + 16 * kc + 8 * h32;
-        const float4 v0 = *reinterpret_cast<const float4*>(src);
-        const float4 v1 = *reinterpret_cast<const float4*>(src + 4);
-        const f16x8 ah = {(f16)v0.x, (f16)v0.y, (f16)v0.z, (f16)v0.w, (f16)v1.x, (f16)v1.y, (f16)v1.z, (f16)v1.w};
-        dqa = mfma16(ah, pkh[nb][kc], dqa);
-      }
-      // rows = queries, lane = code 32 nb + l32
+        for (int kc = 0; kc < KW / 32; ++kc) {
+          const char* base = sdt + 32 * kc * SRB;
+          const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(base + d_s[t][0]));
+          const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(base + d_s[t][1]));
+          a = mfma16x16(__builtin_bit_cast(f16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7)),
+                        phib[t][kc], a);
+        }
+        // rows: queries 16 qt + 4 (lane / 16) + r; column: code 16 ct + lane % 16
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sdq[w][acc_row(r, lane) * 32 * NB + 32 * nb + l32] = dqa[r];
-    }
-    __syncthreads();  // the four partial dq tiles are complete
-    for (int e = tid; e < QT * M; e += 256) {
-      const int r = e / M, c = e % M;
-      if (qs + r < N) {
-        const int o = r * 32 * NB + c;
-        unsafeAtomicAdd(dq + (rowbase + qs + r) * M + c, (sdq[0][o] + sdq[1][o]) + (sdq[2][o] + sdq[3][o]));
+        for (int r = 0; r < 4; ++r) {
+          const int qq = qs + 16 * qt + 4 * (lane >> 4) + r;
+          if (qq < N) unsafeAtomicAdd(dq + (rowbase + qq) * M + 16 * ct + (lane & 15), a[r]);
+        }
       }
     }
     __syncthreads();  // LDS tiles are free for the next step
