@@ -156,6 +156,15 @@ __device__ __forceinline__ void lds_dma16_so(const void* sbase, unsigned voff, u
                : "memory", "m0");
 }
 
+// 4 bytes per lane from global memory straight into LDS: lane l writes LDS
+// byte address lds_addr + 4 l (lds_addr wave-uniform).
+__device__ __forceinline__ void lds_dma4(const float* g, unsigned lds_addr) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off"
+               :
+               : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds_addr))
+               : "memory", "m0");
+}
+
 // s_waitcnt: vector-memory count CNT and LDS count 0 (gfx9 encoding).
 template <int CNT>
 __device__ __forceinline__ void wait_vmcnt_lgkm0() {

@@ -911,10 +911,12 @@ constexpr int soft_fast_bwd_waves() { return (M == 16 && DV <= 64) ? 2 : 1; }
 // Backward, product form. With G_ic = dO_ic 2^(A_i + B_c - zb_ic) = dO_ic / S_ic:
 //     ds_ij = E_ij sum_c G_ic F_jc          (X = G F^T, then times E)
 //     dV_jc = F_jc sum_i E_ij G_ic          (dV^T = G^T E, then times F)
-// Workgroup: 4 waves x 32 keys, lane = key; per 32-query step the workgroup
-// stages G (bf16 hi/lo, [query][column]), the row references A_i and phi of
-// the queries (fp16 hi/lo, [query][code], with a column of ones at code M).
-// The S block is loaded in swap23 query order so that E and ds are already
+// Workgroup: 4 waves x 32 keys, lane = key; each 32-query step's tiles (the
+// queries' code rows, G in bf16 hi / lo [query][column], the row references
+// A_i and token biases) arrive by LDS DMA one step ahead, into the other of
+// two stages; the code rows' affine block begins with a 1 after the codes, so
+// they also serve as [phi_hi | 1] (the ones column at code M).
+// The S block is read in swap23 query order so that E and ds are already
 // B operands of the products that contract over the queries: dV^T += G^T E,
 // and [dk | dcb]^T += [phi_hi | 1]^T ds (one fp16 MFMA per 16 queries; the
 // ones column gives dcb). dq_i = sum_j ds_ij phi_hi_j contracts over the keys:
@@ -940,16 +942,25 @@ __attribute__((amdgpu_waves_per_eu(soft_fast_bwd_waves<M, DV>(), soft_fast_bwd_w
   constexpr int CW = 2 * M + 8, NCH = M / 8, CB = DV / 32, KW = 128, QT = 32;
   constexpr int GS = DV + 8;            // bf16 row stride of the G tiles
   constexpr int MB = (M + 32) / 32;     // 32-code blocks of [phi | 1]
-  constexpr int PT = 32 * MB + 8;       // fp16 row stride of the [phi | 1] tiles
   constexpr int SRB = 2 * QT;           // dS^T row bytes (one key's ds over the step's queries)
   constexpr int DQTILES = (QT / 16) * (M / 16);  // 16 x 16 dq tiles of a step
   constexpr int DQT = DQTILES >= 4 ? DQTILES / 4 : 1;  // per wave (m = 16: waves 0, 1 only)
   static_assert(DQTILES < 4 || DQTILES % 4 == 0, "dq tiles must split evenly over the waves");
-  __shared__ __align__(16) bf16 sgh[QT * GS];
-  __shared__ __align__(16) bf16 sgl[QT * GS];
-  __shared__ __align__(16) f16 sph[QT * PT];
+  // Per-step tiles, two stages filled by LDS DMA (16 bytes per lane, 1 KiB
+  // pieces): the step's query code rows [QT][CW] (fp16: the score operand,
+  // and with the affine block's leading 1 after the codes also [phi_hi | 1]
+  // for dk and dcb), G hi and lo [QT][GS] (bf16; the last 16-byte chunk of a
+  // row is padding), then A_i and the token bias b_i of the QT rows (fp32,
+  // 4 bytes per lane). Rows past N load row N - 1: finite values whose every
+  // score is masked.
+  constexpr int QCH = CW / 8, GCH = GS / 8;        // 16-byte chunks per code row, per G row
+  constexpr int NQP = (QT * QCH + 63) / 64;         // pieces of the code tile
+  constexpr int NGP = (QT * GCH + 63) / 64;         // pieces of each G tile
+  constexpr int NPC = NQP + 2 * NGP;
+  constexpr int OGH = NQP * 1024, OGL = OGH + NGP * 1024, OAB = OGL + NGP * 1024;
+  constexpr int STG = OAB + 256;                    // stage bytes
+  __shared__ __align__(16) char stg[2 * STG];
   __shared__ __align__(16) char sdt[KW * SRB];  // dS^T of the step: row = key, chunks swizzled by sswz
-  __shared__ float sar[QT];
   __shared__ float sbc[DV];
   __shared__ float red[2][4];
 
@@ -1025,64 +1036,71 @@ __attribute__((amdgpu_waves_per_eu(soft_fast_bwd_waves<M, DV>(), soft_fast_bwd_w
   for (int i = 0; i < MB; ++i) dka[i] = f32x16{};
   float sacc = 0.f;
 
+  // DMA of the tiles of the step at query qs into stage par: wave w issues
+  // pieces w, w + 4, ... of the stage, and wave 3 the A / b piece.
+  const unsigned sbase = (unsigned)(uintptr_t)(__attribute__((address_space(3))) char*)stg;
+  auto issue = [&](int qs, int par) {
+    const unsigned dst = sbase + (unsigned)(par * STG);
+    for (int i = w; i < NPC; i += 4) {  // wave-uniform
+      if (i < NQP) {
+        const int q = 64 * i + lane, r = min(q / QCH, QT - 1), c = q % QCH;
+        lds_dma16(qa + (rowbase + min(qs + r, N - 1)) * CW + 8 * c, dst + 1024u * (unsigned)i);
+      } else {
+        const int j = i < NQP + NGP ? i - NQP : i - NQP - NGP;
+        const int q = 64 * j + lane, r = min(q / GCH, QT - 1), c = min(q % GCH, DV / 8 - 1);
+        const bf16* g = i < NQP + NGP ? gh : gl;
+        lds_dma16(reinterpret_cast<const f16*>(g + (rowbase + min(qs + r, N - 1)) * DV + 8 * c),
+                  dst + 1024u * (unsigned)i);
+      }
+    }
+    if (w == 3) {
+      const int r = min(qs + (lane & 31), N - 1);
+      lds_dma4(lane < 32 ? st.arow + rowbase + r : reinterpret_cast<const float*>(tstat + rowbase + r),
+               dst + (unsigned)OAB);
+    }
+  };
+  // The key-side loads above are conditional; without a wait on every path
+  // the compiler treats them as possibly pending inside the step loop and
+  // waits for vmcnt there, which would also drain the next stage's DMA.
+  wait_vmcnt<0>();
+
   const int qstart = causal ? k0 : 0;
-  for (int qs = qstart; qs < N; qs += QT) {
-    // ---- stage G (hi/lo), A and [phi | 1] of queries qs .. qs + QT - 1 (zero
-    // past N and for rows without keys). Every global load of the tile is
-    // issued before the first LDS store, so the tile costs one memory
-    // latency; pieces are 16 bytes (G rows, and the hi / lo halves of the
-    // code rows: 8 codes, or the ones column and zero padding).
-    constexpr int GP = QT * DV / 8, GPT = (GP + 255) / 256;  // G pieces, per thread
-    constexpr int PP = QT * 4 * MB, PPT = (PP + 255) / 256;  // [phi | 1] pieces, per thread
-    bf16x8 gvh[GPT], gvl[GPT];
-    f16x8 pvh[PPT];
-#pragma unroll
-    for (int i = 0; i < GPT; ++i) {
-      const int e = tid + 256 * i, r = e / (DV / 8), c8 = 8 * (e % (DV / 8)), qq = qs + r;
-      gvh[i] = bf16x8{};
-      gvl[i] = bf16x8{};
-      if (e < GP && qq < N) {
-        gvh[i] = *reinterpret_cast<const bf16x8*>(gh + (rowbase + qq) * DV + c8);
-        gvl[i] = *reinterpret_cast<const bf16x8*>(gl + (rowbase + qq) * DV + c8);
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < PPT; ++i) {
-      const int e = tid + 256 * i, r = e / (4 * MB), c8 = 8 * (e % (4 * MB)), qq = qs + r;
-      pvh[i] = f16x8{};
-      if (e < PP && qq < N) {
-        if (c8 < M) {
-          pvh[i] = *reinterpret_cast<const f16x8*>(qa + (rowbase + qq) * CW + c8);
-        } else if (c8 == M) {
-          pvh[i][0] = (f16)1.f;
-        }
-      }
-    }
-    const float arow = tid < QT && qs + tid < N ? st.arow[rowbase + qs + tid] : kNegInf;
-#pragma unroll
-    for (int i = 0; i < GPT; ++i) {
-      const int e = tid + 256 * i, r = e / (DV / 8), c8 = 8 * (e % (DV / 8));
-      if (e < GP) {
-        *reinterpret_cast<bf16x8*>(sgh + r * GS + c8) = gvh[i];
-        *reinterpret_cast<bf16x8*>(sgl + r * GS + c8) = gvl[i];
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < PPT; ++i) {
-      const int e = tid + 256 * i, r = e / (4 * MB), c8 = 8 * (e % (4 * MB));
-      if (e < PP) *reinterpret_cast<f16x8*>(sph + r * PT + c8) = pvh[i];
-    }
-    if (tid < QT) sar[tid] = arow > kNegInf ? arow : 0.f;  // rows without keys: every score is masked
+  if (qstart < N) issue(qstart, 0);
+  int par = 0;
+  for (int qs = qstart; qs < N; qs += QT, par ^= 1) {
+    // this step's stage has landed (the previous step's dq atomics, issued
+    // after it, may still be in flight), for every wave after the barrier,
+    // which also frees the other stage and the dS^T tile
+    if (qs == qstart)
+      wait_vmcnt_lgkm0<0>();
+    else if (dq_wave)  // uniform
+      wait_vmcnt_lgkm0<4 * DQT>();
+    else
+      wait_vmcnt_lgkm0<0>();
+    __syncthreads();
+    if (qs + QT < N) issue(qs + QT, par ^ 1);
+    const char* sq = stg + par * STG;
+    const bf16* sgh = reinterpret_cast<const bf16*>(sq + OGH);
+    const bf16* sgl = reinterpret_cast<const bf16*>(sq + OGL);
+    const float* sa_ = reinterpret_cast<const float*>(sq + OAB);
+    const float* sb_ = sa_ + QT;
     // ---- S block, query rows in swap23 order: register r holds query p(r)
-    const int qrow = qs + swap23(l32);
     f16x8 qf[NCH];
-    f16x4 qaug = {};
+    f16x4 qaug;
+    {
+      const f16* qrow = reinterpret_cast<const f16*>(sq) + swap23(l32) * CW;
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) qf[c] = f16x8{};
-    if (qrow < N) load_query_operand<M>(qa + (rowbase + qrow) * CW, tstat[rowbase + qrow].x, h32, qf, qaug);
+      for (int c = 0; c < NCH; ++c) qf[c] = *reinterpret_cast<const f16x8*>(qrow + chunk_off<M>(c) + 8 * h32);
+      qaug = *reinterpret_cast<const f16x4*>(qrow + M + 4 * h32);
+      if (h32 == 0) {  // the affine block {1, 1, b_hi, b_lo}: the accumulator is log2e s_ij
+        f16 bh_, bl_;
+        split_hi_lo(sb_[swap23(l32)], bh_, bl_);
+        qaug[2] = bh_;
+        qaug[3] = bl_;
+      }
+    }
     f32x16 acc = code_dot<M, false>(kf, qf, f32x16{});
     acc = mfma8(qaug, kaug, acc);
-    __syncthreads();  // staging complete
     // ---- E = 2^(u - A_i) (bf16 hi/lo, the B operand of G^T E); the per-score
     // mask only for blocks with ragged queries or keys, keys after some query
     // or the diagonal (wave-uniform)
@@ -1096,15 +1114,16 @@ __attribute__((amdgpu_waves_per_eu(soft_fast_bwd_waves<M, DV>(), soft_fast_bwd_w
         const int p = r < 8 ? 8 * h32 + r : 8 + 8 * h32 + r;
         const int qq = qs + p;
         const bool drop = (qq >= N) | !kvalid | (causal != 0 && key > qq) | (MD && key == qq);
-        // sar[p] (p < 32) is read for every score and the result selected:
+        // sa_[p] (p < 32) is read for every score and the result selected:
         // a read under the condition compiles to one divergent block, with
-        // its own LDS wait, per score
-        const float ev = fast_exp2(ks * acc[r] - sar[p]);
+        // its own LDS wait, per score. A row without keys has A = -inf, and
+        // every one of its scores is dropped here.
+        const float ev = fast_exp2(ks * acc[r] - sa_[p]);
         e32[r] = drop ? 0.f : ev;
       }
     } else {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) e32[r] = fast_exp2(ks * acc[r] - sar[r < 8 ? 8 * h32 + r : 8 + 8 * h32 + r]);
+      for (int r = 0; r < 16; ++r) e32[r] = fast_exp2(ks * acc[r] - sa_[r < 8 ? 8 * h32 + r : 8 + 8 * h32 + r]);
     }
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -1151,7 +1170,7 @@ __attribute__((amdgpu_waves_per_eu(soft_fast_bwd_waves<M, DV>(), soft_fast_bwd_w
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-      for (int kc = 0; kc < 2; ++kc) dka[mb] = mfma16(frag_kmajor(sph, PT, 16 * kc, 32 * mb, lane), dsh[kc], dka[mb]);
+      for (int kc = 0; kc < 2; ++kc) dka[mb] = mfma16(frag_kmajor(reinterpret_cast<const f16*>(sq), CW, 16 * kc, 32 * mb, lane), dsh[kc], dka[mb]);
     __syncthreads();  // the dS^T tile is complete
     // ---- dq of the step's queries over the workgroup's keys
     if (dq_wave) {
@@ -1168,15 +1187,16 @@ __attribute__((amdgpu_waves_per_eu(soft_fast_bwd_waves<M, DV>(), soft_fast_bwd_w
           a = mfma16x16(__builtin_bit_cast(f16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7)),
                         phib[t][kc], a);
         }
-        // rows: queries 16 qt + 4 (lane / 16) + r; column: code 16 ct + lane % 16
+        // rows: queries 16 qt + 4 (lane / 16) + r; column: code 16 ct + lane % 16.
+        // Always issued (a fixed count per step: the stage waits count on
+        // it); rows past N add 0 to row N - 1.
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int qq = qs + 16 * qt + 4 * (lane >> 4) + r;
-          if (qq < N) unsafeAtomicAdd(dq + (rowbase + qq) * M + 16 * ct + (lane & 15), a[r]);
+          unsafeAtomicAdd(dq + (rowbase + min(qq, N - 1)) * M + 16 * ct + (lane & 15), qq < N ? a[r] : 0.f);
         }
       }
     }
-    __syncthreads();  // LDS tiles are free for the next step
   }
 
   // ---- epilogue: dV_jc = F_jc (G^T E)_cj; dk, dcb; sum dV * w for dtau
