@@ -432,7 +432,8 @@ MORPHO_EXPORT int morpho_backward(const void* grad_out, const void* X, const voi
   // the forward leaves the backward's query affine block in its code rows; a
   // projection computed here still holds its own
   MORPHO_LAUNCH("bwd_prep", launch_bwd_prep(d, p, go, static_cast<const _Float16*>(out), lse, g, have_fwd ? 0 : 1, s));
-  MORPHO_LAUNCH("attn_bwd", launch_attn_bwd(d, p, go, g, s));
+  MORPHO_LAUNCH("attn_bwd", launch_attn_bwd(d, p, go, static_cast<const _Float16*>(gate_q),
+                                            static_cast<const _Float16*>(gate_k), g, s));
   if (d.det) MORPHO_LAUNCH("dq_reduce", launch_dq_det_reduce(d, g, s));
   MORPHO_LAUNCH("proj_bwd_elem", launch_proj_bwd_elem(d, static_cast<const _Float16*>(gate_q),
                                                       static_cast<const _Float16*>(gate_k), p, g, true, s));

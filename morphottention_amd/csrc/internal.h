@@ -144,8 +144,8 @@ hipError_t launch_bwd_prep(const Dims& d, const ProjBuffers& p, const _Float16* 
                            const float* lse, const BwdBuffers& g, int write_q, hipStream_t s);
 DetLayout attn_bwd_det_layout(const Dims& d);
 hipError_t launch_dq_det_reduce(const Dims& d, const BwdBuffers& g, hipStream_t s);
-hipError_t launch_attn_bwd(const Dims& d, const ProjBuffers& p, const _Float16* grad_out, const BwdBuffers& g,
-                           hipStream_t s);
+hipError_t launch_attn_bwd(const Dims& d, const ProjBuffers& p, const _Float16* grad_out, const _Float16* gate_q,
+                           const _Float16* gate_k, const BwdBuffers& g, hipStream_t s);
 
 // kernels_soft.hip: soft tropical aggregation (out = sgn tau ln sum_j
 // exp(sgn (s + v) / tau)). `tau` is a device pointer to one float; sgn is +1

@@ -728,7 +728,8 @@ struct BwdCfg {
 // ~2^-22, as in the forward); without it only the hi chunks (one MFMA instead
 // of three per 16 codes). The backward's P is then exp2 of a score off by
 // ~2^-11 of its code terms, which moves the gradients by ~1e-3 relative for
-// codes in [0, 1] at m = 16 (the launcher uses it only there).
+// codes in [0, 1] at m = 16 with moderate code weights (the kernel below
+// uses it only there).
 // DET: instead of adding to dq and dr with atomics, every workgroup stores its
 // sums over its own keys into per-key-block partials ([nkb][B*H][NQ][M] and
 // [nkb][B*H][NQ] fp32, NQ = N rounded up to QT, so rows past N land in
@@ -736,23 +737,24 @@ struct BwdCfg {
 // the row sums identical from run to run. A store replaces each atomic one
 // for one, so the tile waits count the same operations (waves without a
 // row-sum tile issue no row-sum store and wait as if they had sent none).
+// The body of attn_bwd_kernel for key block kblk of (batch, head) bh. The
+// LDS tiles are the kernel's: stg (2 stages), sdS (dS^T of the whole
+// workgroup, two buffers of KW rows = keys) and sPk (phi_hi of the
+// workgroup's keys, row = key).
 template <int M, int DV, bool MD, bool HILO, bool DET>
-__global__ __launch_bounds__((BwdCfg<M, DV>::NT), (BwdCfg<M, DV>::MIN_WG)) void attn_bwd_kernel(const f16* __restrict__ qa, const f16* __restrict__ ka,
-                                                       const f16* __restrict__ vt, const f16* __restrict__ aug,
-                                                       const f16* __restrict__ grad_out, float* __restrict__ dq,
-                                                       float* __restrict__ dk, float* __restrict__ dcb,
-                                                       float* __restrict__ dr, f16* __restrict__ dzv, int N, int NP,
-                                                       int H, int D, int HM, int BH, int causal) {
+__device__ __forceinline__ void attn_bwd_body(char* stg, char* sdS0, char* sPk, int bh, int kblk,
+                                              const f16* __restrict__ qa, const f16* __restrict__ ka,
+                                              const f16* __restrict__ vt, const f16* __restrict__ aug,
+                                              const f16* __restrict__ grad_out, float* __restrict__ dq,
+                                              float* __restrict__ dk, float* __restrict__ dcb, float* __restrict__ dr,
+                                              f16* __restrict__ dzv, int N, int NP, int H, int D, int HM, int BH,
+                                              int causal) {
   using C = BwdCfg<M, DV>;
-  __shared__ __align__(16) char stg[2 * C::STAGE];
-  __shared__ __align__(16) char sdS[2][C::KW * C::SRB];  // dS^T of the whole workgroup: row = key
-  __shared__ __align__(16) char sPk[C::KW * C::PRB];     // phi_hi of the workgroup's keys: row = key
+  auto sdS = [&](int par) { return sdS0 + par * (C::KW * C::SRB); };
 
   const int tid = threadIdx.x, lane = tid & 63, h32 = lane >> 5, l32 = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, scalar
-  int bh, kblk;
   const int nkb = (N + C::KW - 1) / C::KW;
-  if (!(causal ? xcd_map_lpt(nkb, BH, bh, kblk) : xcd_map(nkb, BH, bh, kblk))) return;
   const int k0 = kblk * C::KW;  // causal: low key blocks see the most queries; they start first
   const int kw0 = k0 + 32 * w;
   const int key = kw0 + l32;
@@ -1081,7 +1083,7 @@ __global__ __launch_bounds__((BwdCfg<M, DV>::NT), (BwdCfg<M, DV>::MIN_WG)) void 
     __builtin_amdgcn_s_barrier();
     if (step + 1 < nsteps) issue(step + 1);  // its stage last served step - 1
     if (step >= 1) {
-      dq_load(sdS[PAR ^ 1]);
+      dq_load(sdS(PAR ^ 1));
       rowsum(step - 1);
     }
 
@@ -1089,7 +1091,7 @@ __global__ __launch_bounds__((BwdCfg<M, DV>::NT), (BwdCfg<M, DV>::MIN_WG)) void 
     const char* tQ = stg + PAR * C::STAGE;
     const char* tO = tQ + C::OOFF;
     const char* tA = tQ + C::AOFF;
-    char* tS = sdS[PAR];
+    char* tS = sdS(PAR);
     // this step's row-sum flag (one affine row per lane; rows repeat when
     // QT = 32), for the next step's rowsum()
     // (a whole 16-byte affine row per lane: a 2-byte read at a 16-byte stride
@@ -1215,7 +1217,7 @@ __global__ __launch_bounds__((BwdCfg<M, DV>::NT), (BwdCfg<M, DV>::MIN_WG)) void 
   if (nsteps > 0) {
     wait_vmcnt_lgkm0<4 * C::DQT + 1>();
     __builtin_amdgcn_s_barrier();  // dS^T of the last step from every wave
-    dq_load(sdS[(nsteps - 1) & 1]);
+    dq_load(sdS((nsteps - 1) & 1));
     rowsum(nsteps - 1);
     dq_finish(nsteps - 1);
   }
@@ -1246,45 +1248,89 @@ __global__ __launch_bounds__((BwdCfg<M, DV>::NT), (BwdCfg<M, DV>::MIN_WG)) void 
   }
 }
 
-template <int M, int DV, bool HILO, bool DET>
-static hipError_t launch_attn_bwd_c(const Dims& d, const ProjBuffers& p, const f16* grad_out, const BwdBuffers& g,
-                                    hipStream_t s) {
+// Bound on a head's code weights sum_c |scale gate_q_c gate_k_c| up to which
+// the scores may come from the fp16 hi codes alone: the scores' error is
+// then ~2^-12 of that sum, and an fp64 emulation of the backward put the
+// worst gradient error at 4.4e-3 for m = 16 at scale 2 with unit gates (sum
+// 32; 9.5e-3 at scale 4), against the 1e-2 bar.
+constexpr float kHiOnlyWeight = 32.f;
+
+// Key-side (KV-outer) backward kernel: maps the workgroup to its key block
+// (causal: longest first) and runs the body. HIOK (m = 16, sigmoid
+// projection, codes in [0, 1]): the scores come from the hi codes alone
+// where the head's code weights are within kHiOnlyWeight, from hi and lo
+// elsewhere (the decision is the workgroup's; both bodies share the LDS
+// tiles). Without HIOK always from hi and lo.
+template <int M, int DV, bool MD, bool HIOK, bool DET>
+__global__ __launch_bounds__((BwdCfg<M, DV>::NT), (BwdCfg<M, DV>::MIN_WG)) void attn_bwd_kernel(
+    const f16* __restrict__ qa, const f16* __restrict__ ka, const f16* __restrict__ vt, const f16* __restrict__ aug,
+    const f16* __restrict__ grad_out, float* __restrict__ dq, float* __restrict__ dk, float* __restrict__ dcb,
+    float* __restrict__ dr, f16* __restrict__ dzv, const f16* __restrict__ gate_q, const f16* __restrict__ gate_k,
+    float scale, int N, int NP, int H, int D, int HM, int BH, int causal) {
+  using C = BwdCfg<M, DV>;
+  __shared__ __align__(16) char stg[2 * C::STAGE];
+  __shared__ __align__(16) char sdS[2 * C::KW * C::SRB];
+  __shared__ __align__(16) char sPk[C::KW * C::PRB];
+  int bh, kblk;
+  const int nkb = (N + C::KW - 1) / C::KW;
+  if (!(causal ? xcd_map_lpt(nkb, BH, bh, kblk) : xcd_map(nkb, BH, bh, kblk))) return;
+  bool hilo = true;
+  if constexpr (HIOK) {
+    const int h = bh % H;
+    float wsum = 0.f;
+#pragma unroll
+    for (int c = 0; c < M; ++c) wsum += fabsf((float)gate_q[h * M + c] * (float)gate_k[h * M + c]);
+    hilo = __builtin_amdgcn_readfirstlane(fabsf(scale) * wsum > kHiOnlyWeight ? 1 : 0) != 0;
+  }
+  if (hilo)
+    attn_bwd_body<M, DV, MD, true, DET>(stg, sdS, sPk, bh, kblk, qa, ka, vt, aug, grad_out, dq, dk, dcb, dr, dzv, N,
+                                        NP, H, D, HM, BH, causal);
+  else if constexpr (HIOK)
+    attn_bwd_body<M, DV, MD, false, DET>(stg, sdS, sPk, bh, kblk, qa, ka, vt, aug, grad_out, dq, dk, dcb, dr, dzv, N,
+                                         NP, H, D, HM, BH, causal);
+}
+
+template <int M, int DV, bool HIOK, bool DET>
+static hipError_t launch_attn_bwd_c(const Dims& d, const ProjBuffers& p, const f16* grad_out, const f16* gate_q,
+                                    const f16* gate_k, const BwdBuffers& g, hipStream_t s) {
   using C = BwdCfg<M, DV>;
   const dim3 grid(xcd_grid((d.N + C::KW - 1) / C::KW, d.B * d.H));
   float* const dq = DET ? g.dqpart : g.dq;
   float* const dr = DET ? g.drpart : g.dr;
   if (d.mask_diag)
-    MORPHO_KLAUNCH((attn_bwd_kernel<M, DV, true, HILO, DET>), grid, dim3(C::NT), 0, s, p.qa, p.ka, p.vt, g.aug,
-                   grad_out, dq, g.dk, g.dcb, dr, g.dzv, d.N, d.NP, d.H, d.D, d.HM, d.B * d.H, d.causal);
+    MORPHO_KLAUNCH((attn_bwd_kernel<M, DV, true, HIOK, DET>), grid, dim3(C::NT), 0, s, p.qa, p.ka, p.vt, g.aug,
+                   grad_out, dq, g.dk, g.dcb, dr, g.dzv, gate_q, gate_k, d.scale, d.N, d.NP, d.H, d.D, d.HM,
+                   d.B * d.H, d.causal);
   else
-    MORPHO_KLAUNCH((attn_bwd_kernel<M, DV, false, HILO, DET>), grid, dim3(C::NT), 0, s, p.qa, p.ka, p.vt, g.aug,
-                   grad_out, dq, g.dk, g.dcb, dr, g.dzv, d.N, d.NP, d.H, d.D, d.HM, d.B * d.H, d.causal);
+    MORPHO_KLAUNCH((attn_bwd_kernel<M, DV, false, HIOK, DET>), grid, dim3(C::NT), 0, s, p.qa, p.ka, p.vt, g.aug,
+                   grad_out, dq, g.dk, g.dcb, dr, g.dzv, gate_q, gate_k, d.scale, d.N, d.NP, d.H, d.D, d.HM,
+                   d.B * d.H, d.causal);
   return hipGetLastError();
 }
 
-template <int M, int DV, bool HILO>
-static hipError_t launch_attn_bwd_h(const Dims& d, const ProjBuffers& p, const f16* grad_out, const BwdBuffers& g,
-                                    hipStream_t s) {
+template <int M, int DV, bool HIOK>
+static hipError_t launch_attn_bwd_h(const Dims& d, const ProjBuffers& p, const f16* grad_out, const f16* gate_q,
+                                    const f16* gate_k, const BwdBuffers& g, hipStream_t s) {
   if (d.det) {
     if (!g.dqpart || !g.drpart) return hipErrorInvalidValue;
-    return launch_attn_bwd_c<M, DV, HILO, true>(d, p, grad_out, g, s);
+    return launch_attn_bwd_c<M, DV, HIOK, true>(d, p, grad_out, gate_q, gate_k, g, s);
   }
-  return launch_attn_bwd_c<M, DV, HILO, false>(d, p, grad_out, g, s);
+  return launch_attn_bwd_c<M, DV, HIOK, false>(d, p, grad_out, gate_q, gate_k, g, s);
 }
 
-// Scores from the hi chunks alone at m = 16 with the sigmoid projection
+// The hi-only scores are possible at m = 16 with the sigmoid projection
 // (codes in [0, 1]; the forward's scores stay exact); hi and lo elsewhere.
 template <int M, int DV>
-static hipError_t launch_attn_bwd_t(const Dims& d, const ProjBuffers& p, const f16* grad_out, const BwdBuffers& g,
-                                    hipStream_t s) {
+static hipError_t launch_attn_bwd_t(const Dims& d, const ProjBuffers& p, const f16* grad_out, const f16* gate_q,
+                                    const f16* gate_k, const BwdBuffers& g, hipStream_t s) {
   if constexpr (M == 16)
-    if (d.proj == kProjSigmoid) return launch_attn_bwd_h<M, DV, false>(d, p, grad_out, g, s);
-  return launch_attn_bwd_h<M, DV, true>(d, p, grad_out, g, s);
+    if (d.proj == kProjSigmoid) return launch_attn_bwd_h<M, DV, true>(d, p, grad_out, gate_q, gate_k, g, s);
+  return launch_attn_bwd_h<M, DV, false>(d, p, grad_out, gate_q, gate_k, g, s);
 }
 
-hipError_t launch_attn_bwd(const Dims& d, const ProjBuffers& p, const f16* grad_out, const BwdBuffers& g,
-                           hipStream_t s) {
-  MORPHO_MDV_DISPATCH(launch_attn_bwd_t, d, p, grad_out, g, s);
+hipError_t launch_attn_bwd(const Dims& d, const ProjBuffers& p, const f16* grad_out, const f16* gate_q,
+                           const f16* gate_k, const BwdBuffers& g, hipStream_t s) {
+  MORPHO_MDV_DISPATCH(launch_attn_bwd_t, d, p, grad_out, gate_q, gate_k, g, s);
 }
 
 // ---------------------------------------------------------------- deterministic dq

@@ -258,6 +258,39 @@ def test_projection_tile_128x160(B, N, D, H, causal):
           *oracle(x, params, H, m, 0.8, causal, dout))
 
 
+def test_backward_hi_only_scores_guard():
+    """At m = 16 with the sigmoid projection the backward recomputes its
+    scores from the fp16 hi codes alone only for heads whose code weights
+    sum_c |scale gate_q gate_k| are at most 32; above that from hi and lo
+    (an unconditional hi-only backward measured d_gate errors of 1.04e-2
+    against fp64 at scale 4 with unit gates). Against the fp64 oracle: scale 4
+    with unit gates (sum 64, every head hi / lo) within 3e-3 per tensor; one
+    causal launch at scale 1 with heads 0-3 at unit gates (sum 16, hi only,
+    within the 1e-2 bar) and heads 4-7 at gates 1.6 (sum 41, hi / lo, within
+    3e-3; hi-only there measured up to 6.0e-3)."""
+    B, N, D, H, m = 2, 512, 512, 8, 16
+    dv = D // H
+    x, params, dout = make_inputs(B, N, D, H, m, seed=820)
+    gq, gk = params[1].clone(), params[2].clone()
+    gq[4:] = 1.6
+    gk[4:] = 1.6
+    for name, p, scale, causal, hilo_heads in [("scale 4, unit gates", params, 4.0, False, range(H)),
+                                               ("mixed heads", [params[0], gq, gk, params[3]], 1.0, True, range(4, H))]:
+        _say(f"[case] hi-only guard: {name}")
+        out, lse, grads = run_hip(x, p, H, m, scale, causal, dout)
+        _, _, r = mo.morpho_attention_ref_grads(x, *p, H, m, scale=scale, causal=causal, dout=dout,
+                                                dtype=torch.float64, batch_chunk=1, head_chunk=8)
+        _say(f"[parity-fp64] guard {name}: " + " ".join(f"{n}={rel_err(g, ref):.2e}"
+                                                       for n, g, ref in zip(GRAD_NAMES, grads, r)))
+        for i in range(len(GRAD_NAMES)):
+            assert rel_err(grads[i], r[i]) <= GRAD_TOL, f"{name}: {GRAD_NAMES[i]}"
+        for h in hilo_heads:  # the heads whose scores must come from hi and lo
+            errs = [rel_err(grads[1][:, h * m:(h + 1) * m], r[1][:, h * m:(h + 1) * m]),
+                    rel_err(grads[2][h], r[2][h]), rel_err(grads[3][h], r[3][h]),
+                    rel_err(grads[4][:, h * dv:(h + 1) * dv], r[4][:, h * dv:(h + 1) * dv])]
+            assert max(errs) <= 3e-3, f"{name}: head {h} gradient errors {errs} (hi-only scores?)"
+
+
 @pytest.mark.parametrize("N", [1, 2, 31, 33, 127, 129, 257])
 def test_ragged_lengths(N):
     B, H, m, dv = 3, 4, 16, 64
