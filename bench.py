@@ -599,6 +599,18 @@ def main():
     torch.cuda.synchronize()
     recs = capi.timing_read()
     capi.timing_enable(False)
+
+    # --- the same K steps again, after every pass above (about 2K + 8 more
+    # steps of load): beside the line, not its value. The driver's window
+    # follows W warm-up steps after an idle GPU, while the clock is still
+    # settling; this shows the step once it has.
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms_after = e0.elapsed_time(e1) / args.steps
     per = {}
     for name, ms in recs:
         per.setdefault(name, []).append(ms)
@@ -621,7 +633,7 @@ def main():
     for k, v in sorted(kernels.items(), key=lambda kv: -kv[1]["avg_ms"]):
         log(f"  {k:18s} {v['avg_ms']:8.4f} ms  x{v['launches_per_step']:.0f}/step  {v['tflops']} TFLOP/s")
     log(f"step {ms_step:.4f} ms  fwd {ms_fwd:.4f} ms  step-level {(f_fwd + f_bwd) / (ms_step * 1e-3) / 1e12:.1f} "
-        f"TFLOP/s")
+        f"TFLOP/s  (the same steps after the other passes: {ms_after:.4f} ms)")
 
     log(f"{dominant} over the timed steps: {dom_avg:.4f} ms ({len(dom_recs)} launches, HIP events)")
     roofline = {"bound": "mfma", "kernel": dominant, "achieved": round(achieved, 2), "peak": PEAK_FP16_TFLOPS,
@@ -652,6 +664,7 @@ def main():
                                f"causal={causal} fwd+bwd", "global_batch": B, "seq_len": N},
         "fwd_ms": round(ms_fwd, 4),
         "fwd_tokens_per_s": round(B * N / (ms_fwd * 1e-3), 1),
+        "ms_per_step_after_passes": round(ms_after, 4),
         "step_roofline_frac": round((f_fwd + f_bwd) / 2.5e15 / (ms_step * 1e-3), 4),
         "fwd_roofline": fwd_roof,
         "roofline": roofline,
