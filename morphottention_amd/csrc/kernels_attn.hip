@@ -922,8 +922,7 @@ __device__ __forceinline__ void attn_bwd_body(char* stg, char* sdS0, char* sPk, 
   int d_s[C::DQT][2];
 #pragma unroll
   for (int t = 0; t < C::DQT; ++t) {
-    const int tile = w + C::NW * t;
-    const int qt = tile % (C::QT / 16), ct = tile / (C::QT / 16);
+    const int qt = (w + C::NW * t) % (C::QT / 16);
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
       const int row = 8 * (lane >> 4) + ((lane & 15) >> 2) + 4 * hh;

@@ -1154,11 +1154,10 @@ __attribute__((amdgpu_waves_per_eu(soft_fast_bwd_waves<M, DV>(), soft_fast_bwd_w
         dva[cb] = mfma_bf16(ah, el[kc], dva[cb]);
         dva[cb] = mfma_bf16(al, eh[kc], dva[cb]);
       }
-    // ---- ds = E X (fp16, the B operand of [phi_hi | 1]^T ds); the ds tile for dq
+    // ---- ds = E X (fp16, the B operand of [phi_hi | 1]^T ds, and the dS^T row for dq)
     f16x8 dsh[2];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int p = r < 8 ? 8 * h32 + r : 8 + 8 * h32 + r;
       const float dsv = e32[r] * x[r];
       sacc = fmaf(dsv, acc[r], sacc);
       dsh[r >> 3][r & 7] = (f16)dsv;
