@@ -197,10 +197,17 @@ __global__ __launch_bounds__(kGemmThreads) void proj_fwd_kernel(const f16* __res
             phl[e] = (f16)(phi - (float)phh[e]);
           }
           // kc = cg phi: lo is the exact product minus hi, so hi + lo carries
-          // kc to ~2^-22 however the compiler rounds hi (it may convert the
-          // product to fp16 in one rounding, v_fma_mixlo_f16)
-          kch[e] = (f16)(cg * phi);
-          kcl[e] = (f16)__builtin_fmaf(cg, phi, -(float)kch[e]);
+          // kc to ~2^-22 however hi was rounded, provided lo and the stored
+          // hi are one value. The conversion (f16)(cg phi) may otherwise be
+          // selected twice, as one rounding of the exact product
+          // (v_fma_mixlo_f16) for the fma and as a rounding of the fp32
+          // product (v_cvt_pk_f16_f32) for the store, and at an fp16 rounding
+          // tie the two differ by an ulp (about 1 code in 16k); the opaque
+          // copy makes hi a single value.
+          f16 hi = (f16)(cg * phi);
+          asm("" : "+v"(hi));
+          kch[e] = hi;
+          kcl[e] = (f16)__builtin_fmaf(cg, phi, -(float)hi);
           sumb += wgt * phi;
           tii += wgt * phi * (2.f * phi - 1.f);
           U += fmaxf(0.f, wgt * (2.f * phi - 1.f));

@@ -330,6 +330,40 @@ def test_single_key_output_is_v_hi_bitwise():
     assert torch.equal(out.view(bh, dv), vt)
 
 
+@pytest.mark.parametrize("projection", ["sigmoid", "hardtanh01", "identity"])
+def test_code_rows_carry_the_codes(projection):
+    """Every stored key code pair carries kc = 2 scale log2e G phi: kc_hi +
+    kc_lo against c1 G (phi_hi + phi_lo) from the same token's query row,
+    relative error <= 2^-18 per code (a consistent pair is exact to ~2^-21).
+    Both halves must come from one rounding of the product: evaluated twice
+    (once as one rounding of the exact product, once via the fp32 product),
+    the two roundings differ at fp16 ties, about 1 code in 16k, and the pair
+    then misses kc by a whole fp16 ulp (2^-11), which moves every score
+    against that key. 2^20 codes per projection, read from the forward
+    workspace (carve_proj: qa, then ka, [B H, N, 2m + 8] fp16)."""
+    B, N, H, m, dv = 2, 2048, 4, 64, 64
+    scale = 0.9
+    from morphottention_amd.autograd import variant_bits
+    _say(f"[case] code rows {projection}: B={B} N={N} H={H} m={m}")
+    x, params, _ = make_inputs(B, N, H * dv, H, m, seed=33, x_mult=1.5, gates=(1.0, 0.4))
+    _, _, ws = torch.ops.morphottention.forward_train(x, *params, H, m, scale, False, variant_bits(projection))
+    torch.cuda.synchronize()
+    al = lambda n: (n + 255) // 256 * 256  # noqa: E731
+    bhn, CW = B * H * N, 2 * m + 8
+    qa = ws[:bhn * CW * 2].view(torch.float16).view(B, H, N, CW).double()
+    ka = ws[al(bhn * CW * 2):al(bhn * CW * 2) + bhn * CW * 2].view(torch.float16).view(B, H, N, CW).double()
+    phi = qa[..., :m] + qa[..., m + 8:]
+    G = (params[1].double() * params[2].double())[None, :, None, :]
+    kc = 2.0 * scale * 1.4426950408889634 * G * phi
+    # bar: 2^-18 relative, with an absolute floor of 2^-20 (fp16 subnormal
+    # halves of codes near 0, negligible in an exponent)
+    ratio = ((ka[..., :m] + ka[..., m + 8:]) - kc).abs() / (2.0 ** -18 * kc.abs() + 2.0 ** -20)
+    worst = ratio.max().item()
+    _say(f"[parity] code rows {projection}: max error of kc_hi + kc_lo {worst:.2e} of the bar, "
+         f"codes beyond it: {int((ratio > 1).sum())} of {ratio.numel()}")
+    assert worst <= 1.0
+
+
 def test_scale_zero_is_a_mean():
     B, N, H, m, dv = 2, 96, 2, 16, 64
     x, params, dout = make_inputs(B, N, H * dv, H, m, seed=300)
@@ -418,6 +452,56 @@ def test_exact_max_path_with_large_signed_gates(causal):
     x, params, dout = make_inputs(B, N, H * dv, H, m, seed=400, gates=(0.0, 3.0))
     out, lse, grads = run_hip(x, params, H, m, 1.0, causal, dout)
     check(f"signed gates causal={causal}", out, lse, grads, *oracle(x, params, H, m, 1.0, causal, dout))
+
+
+def _sweep_cases(n=24, seed=20251):
+    """Seeded random cases over everything the op accepts at small sizes:
+    batch, length (short and multi-block, ragged), heads, cube width, head
+    width, causal, projection, masked diagonal, deterministic mode, scale,
+    gates and input magnitude. Kept where the fp32 oracle is a sound judge of
+    the code-path gradients: scale <= 1 at m = 64, inputs <= 1.5 N(0,1), the
+    Identity projection at m <= 32 and scale <= 0.7 (its codes are unbounded)."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        m = int(rng.choice([16, 32, 64]))
+        dv = int(rng.choice([32, 64, 128]))
+        H, B = int(rng.integers(1, 4)), int(rng.integers(1, 4))
+        N = int(rng.integers(2, 70)) if rng.random() < 0.4 else int(rng.integers(70, 420))
+        causal = bool(rng.integers(0, 2))
+        projection = str(rng.choice(["sigmoid", "sigmoid", "sigmoid", "sigmoid", "hardtanh01", "identity"]))
+        if projection == "identity" and m == 64:
+            projection = "sigmoid"
+        mask_diag = bool(rng.random() < 0.2)
+        det = bool(rng.random() < 0.25)
+        scale = float(np.round(rng.uniform(0.2, 1.0 if m == 64 else 1.5), 3))
+        if projection == "identity":
+            scale = min(scale, 0.7)
+        gates = (float(rng.choice([0.5, 1.0, 1.5])), float(rng.choice([0.0, 0.3])))
+        x_mult = float(rng.choice([0.5, 1.0, 1.5]))
+        cases.append((i, B, N, H, m, dv, causal, projection, mask_diag, det, scale, gates, x_mult))
+    return cases
+
+
+SWEEP = _sweep_cases()
+
+
+@pytest.mark.parametrize("case", SWEEP, ids=[
+    f"s{c[0]}-B{c[1]}-N{c[2]}-H{c[3]}-m{c[4]}-dv{c[5]}-{'causal' if c[6] else 'full'}-{c[7]}"
+    f"{'-md' if c[8] else ''}{'-det' if c[9] else ''}" for c in SWEEP])
+def test_random_sweep(case):
+    """Each seeded case against the fp32 oracle at the north star's bars."""
+    from morphottention_amd.autograd import variant_bits
+    i, B, N, H, m, dv, causal, projection, mask_diag, det, scale, gates, x_mult = case
+    _say(f"[case] sweep {i}: B={B} N={N} H={H} m={m} dv={dv} causal={causal} {projection} mask_diag={mask_diag} "
+         f"det={det} scale={scale} gates={gates} x_mult={x_mult}")
+    x, params, dout = make_inputs(B, N, H * dv, H, m, seed=3000 + i, x_mult=x_mult, gates=gates)
+    out, grads = _run_det(x, params, H, m, scale, causal, dout, projection, mask_diag, det)
+    _, lse, _ = torch.ops.morphottention.forward_train(x, *params, H, m, scale, causal,
+                                                       variant_bits(projection, mask_diag, det))
+    ref = mo.morpho_attention_ref_grads(x, *params, H, m, scale=scale, causal=causal, dout=dout,
+                                        dtype=torch.float32, projection=projection, mask_diag=mask_diag)
+    check(f"sweep {i}", out, lse, grads, *ref)
 
 
 def test_gate_gradients_share_one_factor():
