@@ -144,6 +144,47 @@ def test_soft_variants_masked_diagonal_and_projection():
            projection="hardtanh01", mask_diag=True)
 
 
+def _soft_sweep_cases(n=20, seed=777):
+    """Seeded random cases: batch, length (short and multi-block, ragged),
+    heads, cube and head width, causal, dilation / erosion, temperature
+    (log-uniform 0.1-4, so some calls take the element-wise fallback),
+    scale, projection, masked diagonal (N >= 2) and input magnitude."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        m = int(rng.choice([16, 32, 64]))
+        dv = int(rng.choice([32, 64, 128]))
+        H, B = int(rng.integers(1, 4)), int(rng.integers(1, 3))
+        N = int(rng.integers(2, 70)) if rng.random() < 0.4 else int(rng.integers(70, 300))
+        causal = bool(rng.integers(0, 2))
+        sgn = int(rng.choice([1, -1]))
+        tau = float(np.round(np.exp(rng.uniform(np.log(0.1), np.log(4.0))), 3))
+        scale = float(np.round(rng.uniform(0.3, 1.2), 3))
+        projection = str(rng.choice(["sigmoid", "sigmoid", "sigmoid", "hardtanh01"]))
+        mask_diag = bool(rng.random() < 0.15)
+        x_mult = float(rng.choice([0.5, 1.0, 1.5]))
+        cases.append((i, B, N, H, m, dv, causal, sgn, tau, scale, projection, mask_diag, x_mult))
+    return cases
+
+
+SOFT_SWEEP = _soft_sweep_cases()
+
+
+@pytest.mark.parametrize("case", SOFT_SWEEP, ids=[
+    f"s{c[0]}-B{c[1]}-N{c[2]}-H{c[3]}-m{c[4]}-dv{c[5]}-{'causal' if c[6] else 'full'}-"
+    f"{'dil' if c[7] > 0 else 'ero'}-tau{c[8]}-{c[10]}{'-md' if c[11] else ''}" for c in SOFT_SWEEP])
+def test_soft_random_sweep(case):
+    """Each seeded case against the fp32 oracle at the bars above."""
+    i, B, N, H, m, dv, causal, sgn, tau, scale, projection, mask_diag, x_mult = case
+    _say(f"[case] soft sweep {i}: B={B} N={N} H={H} m={m} dv={dv} causal={causal} sgn={sgn} tau={tau} "
+         f"scale={scale} {projection} mask_diag={mask_diag} x_mult={x_mult}")
+    x, params, dout = _inputs(B, N, H, m, dv, seed=4000 + i, x_mult=x_mult)
+    out, zb, grads = _run(x, params, tau, H, m, scale, causal, sgn, dout, projection=projection, mask_diag=mask_diag)
+    _check(f"sweep {i}", out, zb, grads, x, params, tau, H, m, scale, causal, sgn, dout, projection=projection,
+           mask_diag=mask_diag)
+
+
 def test_small_tau_tends_to_the_hard_tropical_product():
     """tau = 1e-3: max_j (s + V) <= out <= max_j (s + V) + tau ln n, up to the
     fp16 rounding of out and the fp16 inputs' projection in fp32."""
