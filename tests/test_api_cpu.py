@@ -74,6 +74,70 @@ def test_workspace_sizes():
     assert capi.forward_workspace_size(1 << 40, 1 << 40, 64, 1, 16) == 0  # no int64 overflow in T
 
 
+def _size_valid(B, N, D, H, m):
+    """The documented size contract of the C ABI (include/morphottention.h)."""
+    if min(B, N, D, H) <= 0 or D % H or m not in (16, 32, 64) or D // H not in (32, 64, 128):
+        return False
+    if B > 1 << 28 or N > 1 << 28:
+        return False
+    T = B * N
+    return T <= 1 << 28 and D <= 65536 and H * m <= 65536 and T * D <= 1 << 34 and T * H * m <= 1 << 33
+
+
+def test_workspace_sizes_follow_the_size_contract():
+    """Property over 1000 random problems whose token counts sit at, one past,
+    inside or far beyond the limit that binds for their head shape (plus
+    zero, negative and unsupported sizes; about a quarter are valid, and an
+    expected limit off by one token or by a factor of two fails the test):
+    every workspace size function returns 0
+    exactly when the documented contract is broken; otherwise the forward
+    workspace holds at least the code rows, values, remainders, row
+    statistics and weights it is carved into, the backward workspace without
+    a forward one is the one with it plus the forward's, and the
+    deterministic mode only adds to it."""
+    from hypothesis import given, settings, strategies as st
+    from morphottention_amd import capi
+
+    @st.composite
+    def problems(draw):
+        # the head shape first, then a token count aimed at the limit that
+        # binds for it (exactly at it, one past it, inside or far beyond), then
+        # a split of the tokens into B x N (B a power of two, so an exact
+        # limit stays exact); a few draws use degenerate sizes instead
+        H = draw(st.sampled_from([1, 1, 1, 2, 3, 8, 16, 32, 512, 1 << 12, 1 << 20]))
+        dv = draw(st.sampled_from([32, 64, 128] * 3 + [16, 96, 256]))
+        m = draw(st.sampled_from([16, 32, 64] * 3 + [8, 24, 128]))
+        if draw(st.integers(0, 9)) == 0:
+            return draw(st.integers(-2, 2)), draw(st.integers(-2, 1 << 40)), H * dv, H, m
+        tmax = min(1 << 28, (1 << 34) // (H * dv), (1 << 33) // (H * m))
+        kind = draw(st.integers(0, 3))
+        T = max(1, [tmax, tmax + 1, draw(st.integers(1, max(1, tmax))), draw(st.integers(tmax + 1, 8 * tmax + 8))][kind])
+        B = 1 << draw(st.integers(0, max(0, min(40, T.bit_length() - 1))))
+        return B, max(1, T // B), H * dv, H, m
+
+    @settings(max_examples=1000, deadline=None, derandomize=True)
+    @given(p=problems())
+    def prop(p):
+        B, N, D, H, m = p
+        dv = D // H
+        ok = _size_valid(B, N, D, H, m)
+        f = capi.forward_workspace_size(B, N, D, H, m)
+        bw = capi.backward_workspace_size(B, N, D, H, m, True)
+        bwo = capi.backward_workspace_size(B, N, D, H, m, False)
+        bd = capi.backward_workspace_size(B, N, D, H, m, True, mode=1 | 32)
+        sf = capi.soft_forward_workspace_size(B, N, D, H, m)
+        assert (f > 0) == ok and (bw > 0) == ok and (bwo > 0) == ok and (bd > 0) == ok and (sf > 0) == ok, \
+            (B, N, D, H, m, f, bw, bwo, bd, sf)
+        if ok:
+            T = B * N
+            NP = (N + 63) // 64 * 64
+            carved = 2 * T * H * (2 * m + 8) * 2 + B * H * NP * dv * 3 + T * H * 16 + 2 * (H * m + D) * D * 2
+            assert carved <= f < 2 ** 62
+            assert bwo == bw + f and bd >= bw and sf >= f
+
+    prop()
+
+
 @pytest.mark.parametrize("D,H,m", [(1024, 16, 16), (2048, 32, 64)])
 def test_backward_workspace_grows_only_with_per_token_buffers(D, H, m):
     """The weight gradient's per-piece partials (dW tiles x pieces x bt x bt
