@@ -515,6 +515,54 @@ def test_random_sweep(case):
     check(f"sweep {i}", out, lse, grads, *ref)
 
 
+@pytest.mark.parametrize("projection", ["sigmoid", "hardtanh01"])
+def test_causal_rows_ignore_later_tokens(projection):
+    """Causal: out and lse of rows < n0 are bit-identical when the inputs of
+    tokens >= n0 change (perturbed by 2 N(0,1)), for cut points inside a
+    32-row block, at a 64-key tile edge and past the first 256-query
+    workgroup. (The exact-max path, which the Identity projection and the
+    masked diagonal take, is decided per workgroup, so there a later row can
+    change an earlier row's rounding; those are excluded.)"""
+    from morphottention_amd.autograd import variant_bits
+    B, N, H, m, dv = 2, 700, 2, 16, 64
+    _say(f"[case] causality {projection} B={B} N={N}")
+    x, params, _ = make_inputs(B, N, H * dv, H, m, seed=950, x_mult=1.5, gates=(1.5, 0.3))
+    vb = variant_bits(projection)
+    out, lse, _ = torch.ops.morphottention.forward_train(x, *params, H, m, 1.0, True, vb)
+    g = torch.Generator(device="cuda").manual_seed(951)
+    for n0 in (44, 64, 300):
+        x2 = x.clone()
+        x2[:, n0:] = (x2[:, n0:].float() + 2.0 * torch.randn(x2[:, n0:].shape, device="cuda", generator=g)).half()
+        out2, lse2, _ = torch.ops.morphottention.forward_train(x2, *params, H, m, 1.0, True, vb)
+        assert torch.equal(out2[:, :n0], out[:, :n0]), f"n0={n0}: an earlier row's output changed"
+        assert torch.equal(lse2.view(B * H, N)[:, :n0], lse.view(B * H, N)[:, :n0]), f"n0={n0}: lse changed"
+        assert not torch.equal(out2[:, n0:], out[:, n0:])
+
+
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+def test_forward_is_batch_and_head_equivariant(causal):
+    """Permuting the batch permutes out and lse; permuting the heads (the
+    column blocks of W_phi and W_V and the rows of the gates) permutes the
+    output's head columns and lse's head rows. Every (batch, head) problem is
+    computed by the same code whatever workgroup, XCD or projection tile
+    column it lands on, so both hold bit for bit."""
+    B, N, H, m, dv = 3, 300, 4, 32, 64
+    _say(f"[case] equivariance causal={causal}")
+    x, params, _ = make_inputs(B, N, H * dv, H, m, seed=960, gates=(1.0, 0.4))
+    W_phi, gq, gk, W_V = params
+    out, lse = torch.ops.morphottention.forward(x, *params, H, m, 0.9, causal)
+    pb = torch.tensor([2, 0, 1], device="cuda")
+    out_b, lse_b = torch.ops.morphottention.forward(x[pb].contiguous(), *params, H, m, 0.9, causal)
+    assert torch.equal(out_b, out[pb])
+    assert torch.equal(lse_b.view(B, H, N), lse.view(B, H, N)[pb])
+    ph = torch.tensor([3, 1, 0, 2], device="cuda")
+    cols = lambda w, width: w.view(w.shape[0], H, width)[:, ph].reshape(w.shape[0], H * width).contiguous()  # noqa: E731
+    params_h = [cols(W_phi, m), gq[ph].contiguous(), gk[ph].contiguous(), cols(W_V, dv)]
+    out_h, lse_h = torch.ops.morphottention.forward(x, *params_h, H, m, 0.9, causal)
+    assert torch.equal(out_h.view(B, N, H, dv), out.view(B, N, H, dv)[:, :, ph])
+    assert torch.equal(lse_h.view(B, H, N), lse.view(B, H, N)[:, ph])
+
+
 def test_gate_gradients_share_one_factor():
     """Kernel outputs obey d_gate_q * gate_q == d_gate_k * gate_k (same dG)."""
     B, N, H, m, dv = 2, 160, 2, 16, 64
