@@ -1120,6 +1120,11 @@ __device__ __forceinline__ void attn_bwd_body(char* stg, char* sdS0, char* sPk, 
         p16[r >> 3][r & 7] = (f16)pr;
         ds16[r >> 3][r & 7] = (f16)(pr * dp[r]);
       }
+      // one value per rounded dS: the dk / dcb products read these registers
+      // and dq / the row sums read their LDS copy, and the diagonal
+      // correction relies on both being the same halves (a conversion
+      // selected twice, once from the exact product, could differ at ties)
+      asm("" : "+v"(ds16[0]), "+v"(ds16[1]));
       if (C::DCB_VALU) {
         typedef _Float16 h2 __attribute__((ext_vector_type(2)));
         const h2 ones2 = {(f16)1.f, (f16)1.f};

@@ -1162,6 +1162,10 @@ __attribute__((amdgpu_waves_per_eu(soft_fast_bwd_waves<M, DV>(), soft_fast_bwd_w
       sacc = fmaf(dsv, acc[r], sacc);
       dsh[r >> 3][r & 7] = (f16)dsv;
     }
+    // one value per rounded ds for both of its readers (dk below, dq through
+    // the dS^T copy): a conversion of the product selected twice could differ
+    // at fp16 ties
+    asm("" : "+v"(dsh[0]), "+v"(dsh[1]));
     // dS^T row of this key: queries 8 h32 + 0..7 and 16 + 8 h32 + 0..7 are
     // logical chunks h32 and 2 + h32
 #pragma unroll
