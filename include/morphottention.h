@@ -102,7 +102,12 @@ size_t morpho_forward_workspace_size(int64_t B, int64_t N, int64_t D, int64_t H,
  * the launch part of morpho_forward (attention.cpp:15-57).
  * Writes out [B, N, D] (float16) and lse [B*H, N] (float32, base 2;
  * -FLT_MAX, with out = 0, for a row without unmasked keys: only query 0 under
- * MORPHO_MODE_CAUSAL | MORPHO_MODE_MASK_DIAG, or N = 1 with MASK_DIAG). */
+ * MORPHO_MODE_CAUSAL | MORPHO_MODE_MASK_DIAG, or N = 1 with MASK_DIAG).
+ * Numeric range: the key codes hold 2 * scale * log2(e) * gate_q[h][c] *
+ * gate_k[h][c] * phi in float16, so |scale * gate_q * gate_k * phi| must stay
+ * below 22,700 for every code (phi <= 1 except with the Identity projection);
+ * beyond it the codes overflow and the outputs are NaN. The reference keeps
+ * gate * phi in float16 and applies scale in float32. */
 int morpho_forward(const void* X, const void* W_phi, const void* gate_q, const void* gate_k, const void* W_V,
                    void* out, float* lse, int64_t B, int64_t N, int64_t D, int64_t H, int64_t cube_m, float scale,
                    int causal, void* workspace, size_t workspace_bytes, morpho_stream_t stream);
