@@ -410,3 +410,40 @@ def test_soft_fake_kernels_and_module():
         SoftMorphAttention(64, 2, 16, tau=0.0)
     with pytest.raises(ValueError, match="CUDA tensor"):
         mod(torch.randn(1, 4, 64))
+
+
+def test_bench_work_counts_match_the_survey_table():
+    """bench.py's algorithmic counts, which set roofline.achieved and the step
+    fraction, against the independently computed table of the measurement
+    plan (pairs P, F_fwd and F_bwd in GFLOP, MFMA-ideal times at 2.5 PFLOP/s,
+    the C3 exp bound and compulsory bytes), to the table's printed digits."""
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("bench_mod", os.path.join(ROOT, "bench.py"))
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    table = {  # cfg: (P, F_fwd, F_bwd, ideal fwd ms, ideal fwd+bwd ms)
+        "C2": (6.71e7, 16.11, 34.36, 0.0064, 0.0202),
+        "C3": (5.37e8, 128.87, 274.92, 0.0515, 0.1615),
+        "C4": (2.15e9, 463.88, 1065.21, 0.1856, 0.6116),
+        "C5": (2.15e9, 1099.51, 2473.90, 0.4398, 1.4294),
+    }
+    for cfg, (P, ff, fb, tf, tfb) in table.items():
+        B, N, D, H, m, _scale, causal = bench.CONFIGS[cfg][:7]
+        p = bench.pairs(B, N, H, causal)
+        f_fwd, f_bwd = bench.step_flops(B, N, D, H, m, causal)
+        assert abs(p - P) <= 0.005 * P, cfg
+        assert round(f_fwd / 1e9, 2) == pytest.approx(ff, abs=0.011), cfg
+        assert round(f_bwd / 1e9, 2) == pytest.approx(fb, abs=0.011), cfg
+        assert round(f_fwd / 2.5e15 * 1e3, 4) == pytest.approx(tf, abs=1e-4), cfg
+        assert round((f_fwd + f_bwd) / 2.5e15 * 1e3, 4) == pytest.approx(tfb, abs=1e-4), cfg
+        # the per-kernel counts add up to the step's
+        k = lambda n: bench.kernel_flops(n, B, N, D, H, m, causal)  # noqa: E731
+        assert k("proj_fwd") + k("attn_fwd") == pytest.approx(f_fwd, rel=1e-12)
+        assert k("attn_bwd") + k("bwd_gemm") == pytest.approx(f_bwd, rel=1e-12)
+    B, N, D, H, m, _scale, causal = bench.CONFIGS["C3"][:7]
+    assert bench.kernel_flops("attn_bwd", B, N, D, H, m, causal) / 1e9 == pytest.approx(189.0, abs=0.5)
+    bound, t = bench.roofline_terms(*bench.step_flops(B, N, D, H, m, causal)[:1], bench.pairs(B, N, H, causal),
+                                    bench.compulsory_bytes(B, N, D, H, m)[0])
+    assert bound == "exp" and t["exp"] == pytest.approx(0.0548, abs=1e-4) and t["mfma"] == pytest.approx(0.0515, abs=1e-4)
+    fwd_b, bwd_b = bench.compulsory_bytes(B, N, D, H, m)
+    assert fwd_b / 1e6 == pytest.approx(70.8, abs=0.1) and bwd_b / 1e6 == pytest.approx(140.5, abs=0.1)
