@@ -70,6 +70,16 @@ void raise_on(int status, const char* what) {
               "): ", morpho_last_error());
 }
 
+// A workspace size of 0 means the sizes fail the ABI's validation; report its
+// reason (empty dimension, unsupported cube_m or head width, problem too
+// large). morpho_forward validates the sizes before it looks at any pointer
+// or touches the device, so a call without buffers only returns that error.
+void raise_size_error(int64_t B, int64_t N, int64_t D, int64_t H, int64_t M, int mode, const char* what) {
+  const int st = morpho_forward(nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, B, N, D, H, M, 1.0f,
+                                mode, nullptr, 0, nullptr);
+  raise_on(st == MORPHO_OK ? MORPHO_ERR_INVALID_ARGUMENT : st, what);
+}
+
 std::vector<at::Tensor> forward_impl(const at::Tensor& X, const at::Tensor& W_phi, const at::Tensor& gate_q,
                                      const at::Tensor& gate_k, const at::Tensor& W_V, int64_t H, int64_t cube_m,
                                      double scale, bool causal, int64_t variant, bool keep_workspace) {
@@ -79,8 +89,7 @@ std::vector<at::Tensor> forward_impl(const at::Tensor& X, const at::Tensor& W_ph
   auto out = at::empty_like(X);
   auto lse = at::empty({s.B * H, s.N}, X.options().dtype(at::kFloat));
   const size_t ws_bytes = morpho_forward_workspace_size(s.B, s.N, s.D, s.H, s.M);
-  TORCH_CHECK(ws_bytes > 0, "morphottention forward: unsupported sizes (cube_m must be 16, 32 or 64; "
-              "D / H must be 32, 64 or 128)");
+  if (ws_bytes == 0) raise_size_error(s.B, s.N, s.D, s.H, s.M, mode, "forward");
   auto ws = at::empty({(int64_t)ws_bytes}, X.options().dtype(at::kByte));
   raise_on(morpho_forward(X.data_ptr(), W_phi.data_ptr(), gate_q.data_ptr(), gate_k.data_ptr(), W_V.data_ptr(),
                           out.data_ptr(), lse.data_ptr<float>(), s.B, s.N, s.D, s.H, s.M, (float)scale, mode,
@@ -104,6 +113,9 @@ std::vector<at::Tensor> backward_impl(const at::Tensor& grad_out, const at::Tens
   TORCH_CHECK(grad_out.sizes() == X.sizes(), "grad_out must match X shape [B, N, D]");
   TORCH_CHECK(out.sizes() == X.sizes(), "out must match X shape [B, N, D]");
   TORCH_CHECK(lse.dim() == 2 && lse.size(0) == s.B * H && lse.size(1) == s.N, "lse must be [B*H, N]");
+  TORCH_CHECK(grad_out.device() == X.device() && out.device() == X.device() && lse.device() == X.device() &&
+                  (!fwd_ws || fwd_ws->device() == X.device()),
+              "all tensors must be on the same device as X");
   const c10::hip::HIPGuardMasqueradingAsCUDA guard(X.device());
   const void* fwd_ptr = nullptr;
   if (fwd_ws) {
@@ -119,7 +131,7 @@ std::vector<at::Tensor> backward_impl(const at::Tensor& grad_out, const at::Tens
   auto d_gate_k = at::empty_like(gate_k);
   auto dW_V = at::empty_like(W_V);
   const size_t ws_bytes = morpho_backward_workspace_size_for_mode(s.B, s.N, s.D, s.H, s.M, fwd_ptr != nullptr, mode);
-  TORCH_CHECK(ws_bytes > 0, "morphottention backward: unsupported sizes");
+  if (ws_bytes == 0) raise_size_error(s.B, s.N, s.D, s.H, s.M, mode, "backward");
   auto ws = at::empty({(int64_t)ws_bytes}, X.options().dtype(at::kByte));
   raise_on(morpho_backward(grad_out.data_ptr(), X.data_ptr(), W_phi.data_ptr(), gate_q.data_ptr(), gate_k.data_ptr(),
                            W_V.data_ptr(), out.data_ptr(), lse.data_ptr<float>(), dX.data_ptr(), dW_phi.data_ptr(),
@@ -188,8 +200,7 @@ std::vector<at::Tensor> op_soft_forward(const at::Tensor& X, const at::Tensor& W
   auto out = at::empty_like(X);
   auto zb = at::empty({s.B * H, s.N, s.D / H}, X.options().dtype(at::kFloat));
   const size_t ws_bytes = morpho_soft_forward_workspace_size(s.B, s.N, s.D, s.H, s.M);
-  TORCH_CHECK(ws_bytes > 0, "morphottention soft_forward: unsupported sizes (cube_m must be 16, 32 or 64; "
-              "D / H must be 32, 64 or 128)");
+  if (ws_bytes == 0) raise_size_error(s.B, s.N, s.D, s.H, s.M, mode & ~MORPHO_MODE_SOFT_EXACT, "soft_forward");
   auto ws = at::empty({(int64_t)ws_bytes}, X.options().dtype(at::kByte));
   raise_on(morpho_soft_forward(X.data_ptr(), W_phi.data_ptr(), gate_q.data_ptr(), gate_k.data_ptr(), W_V.data_ptr(),
                                tau.data_ptr<float>(), out.data_ptr(), zb.data_ptr<float>(), s.B, s.N, s.D, s.H, s.M,
@@ -216,6 +227,8 @@ std::vector<at::Tensor> op_soft_backward(const at::Tensor& grad_out, const at::T
   TORCH_CHECK(workspace.is_cuda() && workspace.scalar_type() == at::kByte && workspace.is_contiguous() &&
                   (size_t)workspace.numel() >= need,
               "workspace must be the uint8 CUDA tensor returned by soft_forward for these sizes");
+  TORCH_CHECK(grad_out.device() == X.device() && zb.device() == X.device() && workspace.device() == X.device(),
+              "all tensors must be on the same device as X");
   const c10::hip::HIPGuardMasqueradingAsCUDA guard(X.device());
   auto dX = at::empty_like(X);
   auto dW_phi = at::empty_like(W_phi);

@@ -822,7 +822,17 @@ def test_error_messages():
         ops.forward(x, params[0][:, :16].contiguous(), *params[1:], 2, 16, 1.0, False)
     with pytest.raises(RuntimeError, match="D must be divisible by H"):
         ops.forward(x, *params, 3, 16, 1.0, False)
-    with pytest.raises(RuntimeError, match="unsupported"):
+    with pytest.raises(RuntimeError, match=r"unsupported\): cube_m must be 16, 32 or 64 \(got 24\)"):
         W = torch.zeros(128, 48, dtype=torch.float16, device="cuda")
         g = torch.ones(2, 24, dtype=torch.float16, device="cuda")
         ops.forward(x, W, g, g, params[3], 2, 24, 1.0, False)
+    # a workspace size of 0 carries the ABI's own reason
+    with pytest.raises(RuntimeError, match=r"forward failed \(invalid argument\): Invalid dimensions"):
+        ops.forward(x[:0].contiguous(), *params, 2, 16, 1.0, False)
+    with pytest.raises(RuntimeError, match=r"backward failed \(unsupported\): head_dim_v = D / H must be"):
+        xb = torch.zeros(1, 16, 96, dtype=torch.float16, device="cuda")
+        Wp = torch.zeros(96, 32, dtype=torch.float16, device="cuda")
+        gg = torch.ones(2, 16, dtype=torch.float16, device="cuda")
+        Wv = torch.zeros(96, 96, dtype=torch.float16, device="cuda")
+        lse = torch.zeros(2, 16, dtype=torch.float32, device="cuda")
+        ops.backward(xb, xb, Wp, gg, gg, Wv, xb, lse, 2, 16, 1.0, False)
