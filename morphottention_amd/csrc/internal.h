@@ -138,8 +138,11 @@ BwdGemmPlan bwd_gemm_plan(const Dims& d);
 // token k-step where piece j of a dW tile's kw k-steps starts (j = p: the end)
 __host__ __device__ inline int dw_piece_k0(int kw, int p, int j) { return (int)((int64_t)kw * j / p); }
 
-// kernels_attn.hip
+// kernels_attn_fwd.hip (cube_m 16, 32) and kernels_attn_fwd_m64.hip
 hipError_t launch_attn_fwd(const Dims& d, const ProjBuffers& p, _Float16* out, float* lse, hipStream_t s);
+hipError_t launch_attn_fwd_m64(const Dims& d, const ProjBuffers& p, _Float16* out, float* lse, hipStream_t s);
+
+// kernels_attn.hip
 hipError_t launch_bwd_prep(const Dims& d, const ProjBuffers& p, const _Float16* grad_out, const _Float16* out,
                            const float* lse, const BwdBuffers& g, int write_q, hipStream_t s);
 DetLayout attn_bwd_det_layout(const Dims& d);

@@ -61,7 +61,7 @@ def test_no_kernel_has_an_empty_divergent_block(tmp_path):
 
     def asm_of(src):
         out = tmp_path / (src + ".s")
-        subprocess.run([b.HIPCC, *b.HIP_FLAGS, "--cuda-device-only", "-S", os.path.join(CSRC, src), "-o", str(out)],
+        subprocess.run([b.HIPCC, *b.flags_for(src), "--cuda-device-only", "-S", os.path.join(CSRC, src), "-o", str(out)],
                        check=True, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL)
         return src, out.read_text()
 
