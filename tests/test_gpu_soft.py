@@ -323,3 +323,41 @@ def test_soft_product_form_at_the_benchmarked_head_shape(sgn):
          + f" dtau {dtau_err:.2e} of {ref_grads[5].abs().item():.2e} (bar {dtau_bar:.2e})")
     assert excess <= FWD_TOL and zerr <= zbar
     assert all(r <= GRAD_TOL for r in rels[:5]) and dtau_err <= dtau_bar
+
+
+def test_soft_c_abi_direct_matches_ops():
+    """morpho_soft_forward / morpho_soft_backward through ctypes, the C ABI a
+    caller without PyTorch binds, on workspaces filled with 0xFF bytes: the
+    forward's out and zb equal the torch ops' bit for bit; the gradients agree
+    to 1e-3 of each tensor's largest entry (the backward's dq is accumulated
+    with fp32 atomics, so their order, not the arithmetic, may differ)."""
+    import ctypes
+    from morphottention_amd import capi
+    L = capi.lib()
+    B, N, H, m, dv, scale = 2, 100, 2, 16, 64, 0.8
+    D = H * dv
+    _say(f"[case] soft C ABI B={B} N={N} H={H} m={m} dv={dv}")
+    x, params, dout = _inputs(B, N, H, m, dv, seed=990)
+    tau = torch.tensor([0.5], dtype=torch.float32, device="cuda")
+    ops = torch.ops.morphottention
+    ref_out, ref_zb, ref_ws = ops.soft_forward(x, *params, tau, H, m, scale, True, 1, 0)
+    ref_grads = ops.soft_backward(dout, x, *params, tau, ref_zb, ref_ws, H, m, scale, True, 1, 0)
+    vp = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    out, zb = torch.empty_like(ref_out), torch.empty_like(ref_zb)
+    fbytes = capi.soft_forward_workspace_size(B, N, D, H, m)
+    ws = torch.full((fbytes,), 255, dtype=torch.uint8, device="cuda")
+    st = L.morpho_soft_forward(*(vp(t) for t in (x, *params, tau, out, zb)), B, N, D, H, m, scale, 1, 1, vp(ws),
+                               fbytes, stream)
+    assert st == 0, L.morpho_last_error()
+    bbytes = capi.soft_backward_workspace_size(B, N, D, H, m, True)
+    wb = torch.full((bbytes,), 255, dtype=torch.uint8, device="cuda")
+    grads = [torch.empty_like(t) for t in (x, *params, tau)]
+    st = L.morpho_soft_backward(*(vp(t) for t in (dout, x, *params, tau, zb, *grads)), B, N, D, H, m, scale, 1, 1,
+                                vp(ws), vp(wb), bbytes, stream)
+    assert st == 0, L.morpho_last_error()
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref_out) and torch.equal(zb, ref_zb)
+    for n, g, r in zip(NAMES, grads, ref_grads):
+        d = (g.float() - r.float()).abs().max().item() / max(r.float().abs().max().item(), 1e-30)
+        assert torch.isfinite(g).all() and d <= 1e-3, f"{n}: C ABI and op differ by {d}"
