@@ -34,7 +34,7 @@ PEAK_FP16_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
 # the kernel whose roofline the line reports (the longest of a step at every GPU config)
 DOMINANT = "attn_bwd"
 PEAK_HBM_GBS = 8000.0
-# v_exp_f32 at quarter rate: 256 CUs x 16 lanes/clk x 2.4 GHz (BASELINE.md roofline constants)
+# v_exp_f32 at quarter rate: 256 CUs x 16 lanes/clk x 2.4 GHz (a conservative transcendental bound)
 PEAK_EXP_PER_S = 9.8e12
 # the CPU reference configuration, timed in every run
 C1 = (2, 128, 256, 8, 16, 1.0, False, 0, 1.0)
@@ -340,8 +340,8 @@ def _time_cpu(fn, warmup=2, runs=5, budget_s=15.0):
 def cpu_baseline(cfg, name):
     """The reference has no CPU path (its ops are CUDA-only), so the CPU
     baseline is the eager fp32 oracle (oracle/morpho_oracle.py) on the host
-    cores, on the same fp16 input values upcast to fp32 (CPU
-    baseline plan): configs[0] (C1) in full, and a bounded sample of this
+    cores, on the same fp16 input values upcast to fp32: configs[0] (C1)
+    in full, and a bounded sample of this
     workload, one batch row with all heads and the full sequence. Each: 2
     warm-up calls, then the median of up to 5 timed calls, forward and
     forward + backward."""
